@@ -1,0 +1,141 @@
+/*
+ * kairyu_quant.h - C ABI of the MI355X (gfx950) quantized-linear kernels.
+ *
+ * Drop-in boundary for the reference's kernel layer
+ * (reference: kairyu/kernels/quant_gemm_gpu.py).  Every entry point takes raw
+ * device pointers, element counts and a hipStream_t (passed as void*), never
+ * a framework type, launches asynchronously on that stream and returns
+ * KQ_OK or an error code; kq_last_error() gives the message of the calling
+ * thread's most recent failure.  Host wrappers map KQ_EINVAL to ValueError and
+ * every other code to RuntimeError, the reference's fail-closed convention
+ * (quant_gemm_gpu.py:418-520).
+ *
+ * Conventions
+ *   - Matrices are row-major with unit stride in the last dimension; `ld*`
+ *     arguments give the row pitch in elements where a caller may pass views.
+ *   - dtype codes: KQ_DTYPE_F16, KQ_DTYPE_BF16, KQ_DTYPE_F32; KQ_DTYPE_NONE
+ *     marks an absent optional operand (bias).
+ *   - FP8 means OCP e4m3fn bytes (torch.float8_e4m3fn).
+ *   - `workspace` is scratch device memory (split-K partial sums, the
+ *     act-order activation gather).  It may be NULL for the W8A8 entry points
+ *     (no split-K then); W4A16 calls need kq_w4a16_workspace_size() bytes.
+ *     Calls that share one workspace must be ordered on one stream.
+ */
+#ifndef KAIRYU_QUANT_H
+#define KAIRYU_QUANT_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define KQ_OK 0
+#define KQ_EINVAL 1       /* bad shape / layout / argument (ValueError)   */
+#define KQ_EUNSUPPORTED 2 /* device or dtype not supported (RuntimeError) */
+#define KQ_ELAUNCH 3      /* HIP launch failure (RuntimeError)            */
+#define KQ_EWORKSPACE 4   /* workspace too small (RuntimeError)           */
+
+#define KQ_DTYPE_NONE (-1)
+#define KQ_DTYPE_F16 0
+#define KQ_DTYPE_BF16 1
+#define KQ_DTYPE_F32 2
+
+/* Library version (major*10000 + minor*100 + patch). */
+int kq_version(void);
+
+/* Message of the calling thread's last failed call ("" if none). */
+const char* kq_last_error(void);
+
+/* 1 when `device` is a gfx950 GPU this library was built for, else 0.
+ * Replaces the SM capability floors of quant_gemm_gpu.py:409-415. */
+int kq_device_supported(int device);
+
+/* Per-row fp32 absolute maximum of x[rows, k] (fp16/bf16).
+ * Replaces _row_amax_kernel / fp8_activation_amax (quant_gemm_gpu.py:79-94,575-593). */
+int kq_row_amax(const void* x, int x_dtype, int64_t rows, int64_t k, int64_t ldx,
+                float* amax, void* stream);
+
+/* Dynamic per-token symmetric INT8 quantization: scale = max(amax,1e-12)/127
+ * (IEEE division), q = rint(clamp(x/scale, +-127)).
+ * Replaces _scaled_activation_quant_kernel with ROUND_TO_INT
+ * (quant_gemm_gpu.py:26-76,538-572; CPU oracle kairyu/quant/int8.py:25-30). */
+int kq_act_quant_i8(const void* x, int x_dtype, int64_t rows, int64_t k, int64_t ldx,
+                    int8_t* xq, float* xscale, void* stream);
+
+/* Per-token FP8 e4m3 quantization q = e4m3(clamp(x/scale, +-448)).
+ * scale_mode 0: dynamic, scale = max(amax,1e-12)/448 (kairyu/quant/fp8.py:33-45)
+ * scale_mode 1: static scalar scale_in[0] (checkpoint input_scale)
+ * scale_mode 2: given per row scale_in[rows] (TP global amax, linear.py:496-518)
+ * The scale used for each row is written to xscale[rows].
+ * Replaces _scaled_activation_quant_kernel without ROUND_TO_INT. */
+int kq_act_quant_fp8(const void* x, int x_dtype, int64_t rows, int64_t k, int64_t ldx,
+                     const float* scale_in, int scale_mode, uint8_t* xq, float* xscale,
+                     void* stream);
+
+/* INT8 W8A8: acc = xq[m,k] . w[n,k] exactly in int32, then
+ * out = fp32(acc) * xscale[m] * wscale[n] (+ bias[n]), each step rounded
+ * separately, cast to out_dtype.  acc_out (optional, int32 [m,n]) receives
+ * the raw accumulators.  Replaces _int8_w8a8_kernel / int8_linear_forward
+ * (quant_gemm_gpu.py:160-221,657-687; oracle kairyu/quant/int8.py:33-41). */
+int kq_w8a8_i8_gemm(const int8_t* xq, const float* xscale, const int8_t* w,
+                    const float* wscale, const void* bias, int bias_dtype, void* out,
+                    int out_dtype, int32_t* acc_out, int64_t m, int64_t n, int64_t k,
+                    void* workspace, size_t workspace_bytes, void* stream);
+
+/* FP8 W8A8: out = (xq . w in fp32) * xscale[m] * wscale[n or 0] (+ bias).
+ * wscale_per_channel selects wscale[n] vs a per-tensor wscale[0].
+ * Replaces torch._scaled_mm / _fp8_w8a8_kernel of fp8_linear_forward
+ * (quant_gemm_gpu.py:97-157,596-654; oracle kairyu/quant/fp8.py:48-56). */
+int kq_w8a8_fp8_gemm(const uint8_t* xq, const float* xscale, const uint8_t* w,
+                     const float* wscale, int wscale_per_channel, const void* bias,
+                     int bias_dtype, void* out, int out_dtype, int64_t m, int64_t n,
+                     int64_t k, void* workspace, size_t workspace_bytes, void* stream);
+
+/* AWQ W4A16 ("gemm" layout): qweight int32 [k, n/8] packed along n in order
+ * [0,2,4,6,1,3,5,7], qzeros int32 [k/g, n/8] same packing, scales fp16 [k/g, n].
+ * w = fp16((q - z) * s); x is fed to the dot as fp16 (bf16 saturated to
+ * +-65504); fp32 accumulation; out in x_dtype.
+ * Replaces _awq_w4a16_kernel / awq_linear_forward (quant_gemm_gpu.py:224-315,690-724;
+ * format kairyu/quant/awq.py:14-74). */
+int kq_w4a16_awq_gemm(const void* x, int x_dtype, const int32_t* qweight,
+                      const int32_t* qzeros, const void* scales, const void* bias,
+                      int bias_dtype, void* out, int64_t m, int64_t n, int64_t k,
+                      int group_size, void* workspace, size_t workspace_bytes,
+                      void* stream);
+
+/* GPTQ W4A16: qweight int32 [k/8, n] packed LSB-first along k, qzeros int32
+ * [groups, n/8] packed along n storing z-1, scales fp16 [groups, n].
+ * w = fp16((q - (z_stored + 1)) * s[group(k)]).
+ * gidx_mode 0: group(k) = k / group_size, qweight rows in checkpoint order.
+ * gidx_mode 1: qweight rows were permuted by kq_gptq_permute_qweight with
+ *              `perm`; permuted row j reads x[:, perm[j]] and has group
+ *              j / group_size.
+ * gidx_mode 2: arbitrary g_idx[k] (per-element group lookup).
+ * Replaces _gptq_w4a16_kernel / gptq_linear_forward (quant_gemm_gpu.py:318-407,
+ * 727-761; format kairyu/quant/gptq.py:15-90). */
+int kq_w4a16_gptq_gemm(const void* x, int x_dtype, const int32_t* qweight,
+                       const int32_t* qzeros, const void* scales, const int32_t* g_idx,
+                       const int32_t* perm, int gidx_mode, const void* bias,
+                       int bias_dtype, void* out, int64_t m, int64_t n, int64_t k,
+                       int group_size, void* workspace, size_t workspace_bytes,
+                       void* stream);
+
+/* Bytes of `workspace` a W4A16 call of this shape needs (gidx_mode as for
+ * kq_w4a16_gptq_gemm; AWQ uses 0).  No reference counterpart: sizing helper
+ * for the caller-owned scratch buffer. */
+size_t kq_w4a16_workspace_size(int64_t m, int64_t n, int64_t k, int gidx_mode);
+
+/* Load-time act-order repack: out row j of the unpacked [k, n] nibble matrix
+ * is source row perm[j]; packing stays GPTQ (k/8 words, LSB-first).  Derived
+ * operand only; checkpoint buffers are untouched (the reference caches derived
+ * runtime operands the same way, quant_gemm_gpu.py:802-850). */
+int kq_gptq_permute_qweight(const int32_t* qweight, const int32_t* perm, int32_t* out,
+                            int64_t n, int64_t k, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* KAIRYU_QUANT_H */

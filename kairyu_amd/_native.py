@@ -1,0 +1,157 @@
+"""ctypes binding of ``libkairyu_quant.so`` (C ABI in ``include/kairyu_quant.h``).
+
+The library is loaded after ``import torch`` so that its ``libamdhip64.so.7``
+dependency resolves to the HIP runtime torch already loaded: both then share
+one device context and torch's streams can be passed straight through.  There
+is no fallback of any kind: a missing or unloadable library raises
+``RuntimeError`` at the first device call.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+from pathlib import Path
+
+import torch
+
+LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libkairyu_quant.so"
+
+KQ_OK = 0
+KQ_EINVAL = 1
+KQ_EUNSUPPORTED = 2
+KQ_ELAUNCH = 3
+KQ_EWORKSPACE = 4
+
+DTYPE_NONE = -1
+DTYPE_F16 = 0
+DTYPE_BF16 = 1
+DTYPE_F32 = 2
+
+# split-K partial sums and the act-order activation gather; 32 MiB covers
+# every decode shape at its preferred split count.
+DEFAULT_WORKSPACE_BYTES = 32 * 1024 * 1024
+
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+_I64 = ctypes.c_int64
+_SZ = ctypes.c_size_t
+
+_SIGNATURES: dict[str, list] = {
+    "kq_version": [],
+    "kq_last_error": [],
+    "kq_device_supported": [_I],
+    "kq_row_amax": [_P, _I, _I64, _I64, _I64, _P, _P],
+    "kq_act_quant_i8": [_P, _I, _I64, _I64, _I64, _P, _P, _P],
+    "kq_act_quant_fp8": [_P, _I, _I64, _I64, _I64, _P, _I, _P, _P, _P],
+    "kq_w8a8_i8_gemm": [_P, _P, _P, _P, _P, _I, _P, _I, _P, _I64, _I64, _I64, _P, _SZ, _P],
+    "kq_w8a8_fp8_gemm": [_P, _P, _P, _P, _I, _P, _I, _P, _I, _I64, _I64, _I64, _P, _SZ, _P],
+    "kq_w4a16_awq_gemm": [_P, _I, _P, _P, _P, _P, _I, _P, _I64, _I64, _I64, _I, _P, _SZ, _P],
+    "kq_w4a16_gptq_gemm": [
+        _P, _I, _P, _P, _P, _P, _P, _I, _P, _I, _P, _I64, _I64, _I64, _I, _P, _SZ, _P,
+    ],
+    "kq_gptq_permute_qweight": [_P, _P, _P, _I64, _I64, _P],
+    "kq_w4a16_workspace_size": [_I64, _I64, _I64, _I],
+}
+
+_lock = threading.Lock()
+_lib: ctypes.CDLL | None = None
+_load_error: str | None = None
+
+
+def _load() -> ctypes.CDLL:
+    global _lib, _load_error
+    with _lock:
+        if _lib is not None:
+            return _lib
+        path = Path(os.environ.get("KAIRYU_AMD_LIB", LIB_PATH))
+        if not path.is_file():
+            _load_error = f"{path} is not built; run kairyu_amd.build.build() (hipcc, gfx950)"
+            raise RuntimeError(_load_error)
+        try:
+            lib = ctypes.CDLL(str(path))
+        except OSError as error:
+            _load_error = f"cannot load {path}: {error}"
+            raise RuntimeError(_load_error) from error
+        for name, argtypes in _SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.argtypes = argtypes
+            fn.restype = {"kq_last_error": ctypes.c_char_p,
+                          "kq_w4a16_workspace_size": ctypes.c_size_t}.get(name, ctypes.c_int)
+        _lib = lib
+        return lib
+
+
+def library() -> ctypes.CDLL:
+    """The loaded kernel library; raises RuntimeError when it is unavailable."""
+
+    return _load()
+
+
+def exported_symbols() -> tuple[str, ...]:
+    return tuple(_SIGNATURES)
+
+
+def call(name: str, *args) -> None:
+    """Invoke one C entry point and map its status to the reference's exceptions."""
+
+    lib = _load()
+    status = getattr(lib, name)(*args)
+    if status == KQ_OK:
+        return
+    message = lib.kq_last_error().decode(errors="replace")
+    if status == KQ_EINVAL:
+        raise ValueError(f"{name}: {message}")
+    raise RuntimeError(f"{name} failed ({status}): {message}")
+
+
+def dtype_code(dtype: torch.dtype | None) -> int:
+    if dtype is None:
+        return DTYPE_NONE
+    if dtype is torch.float16:
+        return DTYPE_F16
+    if dtype is torch.bfloat16:
+        return DTYPE_BF16
+    if dtype is torch.float32:
+        return DTYPE_F32
+    raise RuntimeError(f"unsupported dtype {dtype} at the kernel boundary")
+
+
+def ptr(tensor: torch.Tensor | None) -> int | None:
+    return None if tensor is None else tensor.data_ptr()
+
+
+def stream_handle(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+_supported: dict[int, bool] = {}
+
+
+def device_supported(index: int) -> bool:
+    if index not in _supported:
+        _supported[index] = bool(_load().kq_device_supported(index))
+    return _supported[index]
+
+
+_workspaces: dict[int, torch.Tensor] = {}
+
+
+def workspace(device: torch.device, nbytes: int = DEFAULT_WORKSPACE_BYTES) -> torch.Tensor:
+    """Per-device scratch buffer (split-K partials, act-order activation gather).
+
+    Allocated once per device through torch's caching allocator, grown when a
+    call needs more, and reused by every call (also inside captured graphs:
+    grow it with an eager call of the largest shape before capture).  Calls
+    sharing it must be ordered on one stream, like the engine's single-stream
+    decode loop.
+    """
+
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    buffer = _workspaces.get(index)
+    if buffer is None or buffer.numel() < nbytes:
+        buffer = torch.empty(max(nbytes, DEFAULT_WORKSPACE_BYTES), dtype=torch.uint8,
+                             device=torch.device("cuda", index))
+        _workspaces[index] = buffer
+    return buffer

@@ -1,0 +1,240 @@
+// Per-token activation kernels: row amax, INT8 and FP8 quantization.
+//
+// One workgroup (up to 1024 threads) per row; the row is read once into
+// registers (8 elements per chunk, up to 8 chunks per thread: K <= 65536),
+// reduced for its amax and quantized from registers.  Arithmetic follows
+// the reference's CPU oracle exactly (kairyu/quant/int8.py:25-30,
+// kairyu/quant/fp8.py:33-45): fp32 amax, IEEE division for the scale and for
+// x/scale, round-half-even for INT8, RNE e4m3 after a +-448 clamp for FP8.
+#include "kq_common.h"
+
+#include <algorithm>
+
+namespace kq {
+
+// Loads up to 8 consecutive elements of a fp16/bf16 row as fp32; elements at
+// or beyond `k` read as 0.
+KQ_DEV void load8_f32(const uint16_t* row, int64_t i, int64_t k, int dtype, bool vec_ok,
+                      float v[8]) {
+  if (vec_ok && i + 8 <= k) {
+    u32x4 raw = *(const u32x4*)(row + i);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      uint32_t w = raw[j];
+      uint16_t lo = (uint16_t)(w & 0xffffu), hi = (uint16_t)(w >> 16);
+      v[2 * j] = dtype == KQ_DTYPE_BF16 ? bf16_to_f32(lo) : f16_to_f32(lo);
+      v[2 * j + 1] = dtype == KQ_DTYPE_BF16 ? bf16_to_f32(hi) : f16_to_f32(hi);
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      int64_t c = i + j;
+      v[j] = c < k ? (dtype == KQ_DTYPE_BF16 ? bf16_to_f32(row[c]) : f16_to_f32(row[c])) : 0.0f;
+    }
+  }
+}
+
+KQ_DEV float block_max(float v, float* red) {
+  v = wave_max(v);
+  if (lane_id() == 0) red[wave_id()] = v;
+  __syncthreads();
+  float r = red[0];
+  for (int w = 1; w < (int)(blockDim.x >> 6); ++w) r = fmaxf(r, red[w]);
+  __syncthreads();
+  return r;
+}
+
+// Clamp that keeps NaN (torch.clamp semantics).
+KQ_DEV float clamp_keep_nan(float v, float lim) {
+  return v < -lim ? -lim : (v > lim ? lim : v);
+}
+
+// Single-pass row kernels: each thread holds NCH chunks of 8 elements of the
+// row in registers (chunk c = tid + blockDim.x * i), so the row is read from
+// HBM once; the amax is reduced across the workgroup and the quantized bytes
+// are produced from the registers.
+template <int NCH>
+KQ_DEV float load_row_regs(const uint16_t* row, int64_t k, int dtype, bool vec_ok,
+                           float v[NCH][8]) {
+  float m = 0.0f;
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    const int64_t i = ((int64_t)threadIdx.x + (int64_t)blockDim.x * c) * 8;
+    load8_f32(row, i, k, dtype, vec_ok, v[c]);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) m = fmaxf(m, fabsf(v[c][e]));
+  }
+  return m;
+}
+
+template <int NCH>
+__global__ void __launch_bounds__(1024)
+row_amax_kernel(const uint16_t* __restrict__ x, int dtype, int64_t k, int64_t ldx,
+                bool vec_ok, float* __restrict__ out) {
+  __shared__ float red[16];
+  float v[NCH][8];
+  float m = load_row_regs<NCH>(x + (int64_t)blockIdx.x * ldx, k, dtype, vec_ok, v);
+  m = block_max(m, red);
+  if (threadIdx.x == 0) out[blockIdx.x] = m;
+}
+
+KQ_DEV void store8(uint8_t* qrow, int64_t i, int64_t k, uint32_t lo, uint32_t hi) {
+  if (i + 8 <= k && (k & 7) == 0) {
+    *(u32x2*)(qrow + i) = u32x2{lo, hi};
+  } else {
+    for (int j = 0; j < 8 && i + j < k; ++j)
+      qrow[i + j] = (uint8_t)((((j < 4) ? lo : hi) >> (8 * (j & 3))) & 0xffu);
+  }
+}
+
+template <int NCH>
+__global__ void __launch_bounds__(1024)
+act_quant_i8_kernel(const uint16_t* __restrict__ x, int dtype, int64_t k, int64_t ldx,
+                    bool vec_ok, int8_t* __restrict__ xq, float* __restrict__ xscale) {
+  __shared__ float red[16];
+  const int64_t r = blockIdx.x;
+  float v[NCH][8];
+  float amax = block_max(load_row_regs<NCH>(x + r * ldx, k, dtype, vec_ok, v), red);
+  const float s = __fdiv_rn(fmaxf(amax, 1e-12f), 127.0f);
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    const int64_t i = ((int64_t)threadIdx.x + (int64_t)blockDim.x * c) * 8;
+    if (i >= k) break;
+    uint32_t packed[2] = {0u, 0u};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float q = __builtin_rintf(clamp_keep_nan(__fdiv_rn(v[c][e], s), 127.0f));
+      packed[e >> 2] |= ((uint32_t)(int32_t)q & 0xffu) << (8 * (e & 3));
+    }
+    store8((uint8_t*)xq + r * k, i, k, packed[0], packed[1]);
+  }
+  if (threadIdx.x == 0) xscale[r] = s;
+}
+
+template <int NCH>
+__global__ void __launch_bounds__(1024)
+act_quant_fp8_kernel(const uint16_t* __restrict__ x, int dtype, int64_t k, int64_t ldx,
+                     bool vec_ok, const float* __restrict__ scale_in, int scale_mode,
+                     uint8_t* __restrict__ xq, float* __restrict__ xscale) {
+  __shared__ float red[16];
+  const int64_t r = blockIdx.x;
+  float v[NCH][8];
+  const float amax = load_row_regs<NCH>(x + r * ldx, k, dtype, vec_ok, v);
+  float s;
+  if (scale_mode == 0) s = __fdiv_rn(fmaxf(block_max(amax, red), 1e-12f), 448.0f);
+  else if (scale_mode == 1) s = scale_in[0];
+  else s = scale_in[r];
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    const int64_t i = ((int64_t)threadIdx.x + (int64_t)blockDim.x * c) * 8;
+    if (i >= k) break;
+    uint32_t packed[2] = {0u, 0u};
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      packed[e >> 2] |= f32_to_e4m3(clamp_keep_nan(__fdiv_rn(v[c][e], s), 448.0f)) << (8 * (e & 3));
+    store8(xq + r * k, i, k, packed[0], packed[1]);
+  }
+  if (threadIdx.x == 0) xscale[r] = s;
+}
+
+// Row geometry: threads (multiple of 64, <= 1024) and chunks per thread.
+struct RowPlan {
+  int threads, nch;
+};
+
+static RowPlan plan_rows(int64_t k) {
+  const int64_t chunks = (k + 7) / 8;
+  RowPlan p{};
+  p.nch = chunks <= 1024 ? 1 : (chunks <= 2048 ? 2 : (chunks <= 4096 ? 4 : 8));
+  const int64_t per = (chunks + p.nch - 1) / p.nch;
+  p.threads = (int)std::min<int64_t>(1024, std::max<int64_t>(64, (per + 63) / 64 * 64));
+  return p;
+}
+
+static int check_rows(const char* what, const void* x, int dtype, int64_t rows, int64_t k,
+                      int64_t ldx) {
+  if (dtype != KQ_DTYPE_F16 && dtype != KQ_DTYPE_BF16) {
+    set_error("%s: activation dtype must be fp16 or bf16 (code %d)", what, dtype);
+    return KQ_EUNSUPPORTED;
+  }
+  if (rows < 0 || k < 1 || ldx < k || rows > 0x7fffffffLL || k > 65536) {
+    set_error("%s: bad shape rows=%lld k=%lld ldx=%lld", what, (long long)rows,
+              (long long)k, (long long)ldx);
+    return KQ_EINVAL;
+  }
+  if (rows > 0 && x == nullptr) {
+    set_error("%s: null activation", what);
+    return KQ_EINVAL;
+  }
+  return KQ_OK;
+}
+
+static bool vec_ok(const void* x, int64_t ldx) {
+  return ((uintptr_t)x % 16) == 0 && (ldx % 8) == 0;
+}
+
+}  // namespace kq
+
+using namespace kq;
+
+extern "C" int kq_row_amax(const void* x, int x_dtype, int64_t rows, int64_t k, int64_t ldx,
+                           float* amax, void* stream) {
+  int rc = check_rows("kq_row_amax", x, x_dtype, rows, k, ldx);
+  if (rc) return rc;
+  if (rows == 0) return KQ_OK;
+  const RowPlan p = plan_rows(k);
+  const bool v = vec_ok(x, ldx);
+  const dim3 g((unsigned)rows), b(p.threads);
+  hipStream_t st = (hipStream_t)stream;
+  const uint16_t* xs = (const uint16_t*)x;
+  switch (p.nch) {
+    case 1: hipLaunchKernelGGL(row_amax_kernel<1>, g, b, 0, st, xs, x_dtype, k, ldx, v, amax); break;
+    case 2: hipLaunchKernelGGL(row_amax_kernel<2>, g, b, 0, st, xs, x_dtype, k, ldx, v, amax); break;
+    case 4: hipLaunchKernelGGL(row_amax_kernel<4>, g, b, 0, st, xs, x_dtype, k, ldx, v, amax); break;
+    default: hipLaunchKernelGGL(row_amax_kernel<8>, g, b, 0, st, xs, x_dtype, k, ldx, v, amax); break;
+  }
+  return check_launch("kq_row_amax");
+}
+
+extern "C" int kq_act_quant_i8(const void* x, int x_dtype, int64_t rows, int64_t k,
+                               int64_t ldx, int8_t* xq, float* xscale, void* stream) {
+  int rc = check_rows("kq_act_quant_i8", x, x_dtype, rows, k, ldx);
+  if (rc) return rc;
+  if (rows == 0) return KQ_OK;
+  const RowPlan p = plan_rows(k);
+  const bool v = vec_ok(x, ldx);
+  const dim3 g((unsigned)rows), b(p.threads);
+  hipStream_t st = (hipStream_t)stream;
+  const uint16_t* xs = (const uint16_t*)x;
+  switch (p.nch) {
+    case 1: hipLaunchKernelGGL(act_quant_i8_kernel<1>, g, b, 0, st, xs, x_dtype, k, ldx, v, xq, xscale); break;
+    case 2: hipLaunchKernelGGL(act_quant_i8_kernel<2>, g, b, 0, st, xs, x_dtype, k, ldx, v, xq, xscale); break;
+    case 4: hipLaunchKernelGGL(act_quant_i8_kernel<4>, g, b, 0, st, xs, x_dtype, k, ldx, v, xq, xscale); break;
+    default: hipLaunchKernelGGL(act_quant_i8_kernel<8>, g, b, 0, st, xs, x_dtype, k, ldx, v, xq, xscale); break;
+  }
+  return check_launch("kq_act_quant_i8");
+}
+
+extern "C" int kq_act_quant_fp8(const void* x, int x_dtype, int64_t rows, int64_t k,
+                                int64_t ldx, const float* scale_in, int scale_mode,
+                                uint8_t* xq, float* xscale, void* stream) {
+  int rc = check_rows("kq_act_quant_fp8", x, x_dtype, rows, k, ldx);
+  if (rc) return rc;
+  if (scale_mode < 0 || scale_mode > 2 || (scale_mode != 0 && scale_in == nullptr)) {
+    set_error("kq_act_quant_fp8: bad scale_mode %d", scale_mode);
+    return KQ_EINVAL;
+  }
+  if (rows == 0) return KQ_OK;
+  const RowPlan p = plan_rows(k);
+  const bool v = vec_ok(x, ldx);
+  const dim3 g((unsigned)rows), b(p.threads);
+  hipStream_t st = (hipStream_t)stream;
+  const uint16_t* xs = (const uint16_t*)x;
+  switch (p.nch) {
+    case 1: hipLaunchKernelGGL(act_quant_fp8_kernel<1>, g, b, 0, st, xs, x_dtype, k, ldx, v, scale_in, scale_mode, xq, xscale); break;
+    case 2: hipLaunchKernelGGL(act_quant_fp8_kernel<2>, g, b, 0, st, xs, x_dtype, k, ldx, v, scale_in, scale_mode, xq, xscale); break;
+    case 4: hipLaunchKernelGGL(act_quant_fp8_kernel<4>, g, b, 0, st, xs, x_dtype, k, ldx, v, scale_in, scale_mode, xq, xscale); break;
+    default: hipLaunchKernelGGL(act_quant_fp8_kernel<8>, g, b, 0, st, xs, x_dtype, k, ldx, v, scale_in, scale_mode, xq, xscale); break;
+  }
+  return check_launch("kq_act_quant_fp8");
+}

@@ -1,0 +1,398 @@
+// W8A8 GEMMs for gfx950: INT8 (v_mfma_i32_16x16x64_i8) and FP8 e4m3
+// (v_mfma_scale_f32_16x16x128_f8f6f4 with unit scales).
+//
+//   out[m, n] = epilogue( sum_k xq[m, k] * w[n, k] )
+//   INT8: fp32(acc) * xscale[m] * wscale[n] (+ bias[n]), int32 accumulation
+//         exact; each multiply/add rounded separately (no FMA contraction), the
+//         CPU oracle's op order (kairyu/quant/int8.py:33-41, linear.py:547-553).
+//   FP8 : acc (fp32) * xscale[m] * wscale[n or 0] (+ bias[n])
+//         (kairyu/quant/fp8.py:48-56, linear.py:463-469).
+//
+// Two kernels:
+//   * skinny (M <= 64): a workgroup owns 16 output columns; its 8 waves split
+//     K, stream weight rows straight into MFMA B-operand registers and reduce
+//     through LDS.  Small-N shapes also split K across workgroups, finished
+//     by a separate reduce kernel (no inter-workgroup sync).  HBM-bound.
+//   * tiled (M > 64): 128x128x128 workgroup tiles, 4 waves of 64x64, LDS
+//     double buffer with an XOR chunk swizzle.  MFMA-bound.
+#include "kq_common.h"
+#include "kq_splitk.h"
+
+namespace kq {
+
+enum { kFmtI8 = 0, kFmtFp8 = 1 };
+
+template <int FMT> struct W8Traits;
+template <> struct W8Traits<kFmtI8> {
+  static constexpr int kStep = 64;   // K per MFMA
+  static constexpr int kLane = 16;   // bytes per lane per operand
+  using Acc = i32x4;
+  using Frag = i32x4;
+};
+template <> struct W8Traits<kFmtFp8> {
+  static constexpr int kStep = 128;
+  static constexpr int kLane = 32;
+  using Acc = f32x4;
+  using Frag = i32x8;
+};
+
+struct Epi {
+  const float* xscale;
+  const float* wscale;
+  int ws_per_channel;
+  const void* bias;
+  int bias_dtype;
+  void* out;
+  int out_dtype;
+  int32_t* acc_out;
+  int M, N;
+};
+
+template <int FMT>
+KQ_DEV void epi_store(const Epi& ep, int m, int n, typename W8Traits<FMT>::Acc acc, int r) {
+  if (m >= ep.M || n >= ep.N) return;
+  float v;
+  if constexpr (FMT == kFmtI8) {
+    if (ep.acc_out) ep.acc_out[(int64_t)m * ep.N + n] = acc[r];
+    v = (float)acc[r];
+  } else {
+    v = acc[r];
+  }
+  v = __fmul_rn(v, ep.xscale[m]);
+  v = __fmul_rn(v, ep.ws_per_channel ? ep.wscale[n] : ep.wscale[0]);
+  if (ep.bias_dtype != KQ_DTYPE_NONE) v = __fadd_rn(v, load_as_f32(ep.bias, ep.bias_dtype, n));
+  ((uint16_t*)ep.out)[(int64_t)m * ep.N + n] = f32_to_out(v, ep.out_dtype);
+}
+
+// Raw 32-bit pattern of accumulator element r.  (Goes through a scalar
+// conversion: a bit cast applied directly to an ext-vector element selected
+// element 0 for every r with this compiler.)
+KQ_DEV uint32_t acc_bits(i32x4 a, int r) { return (uint32_t)(int)a[r]; }
+KQ_DEV uint32_t acc_bits(f32x4 a, int r) { return __float_as_uint((float)a[r]); }
+
+template <int FMT>
+KQ_DEV typename W8Traits<FMT>::Frag load_frag(const uint8_t* p, bool lo_ok, bool hi_ok) {
+  using Frag = typename W8Traits<FMT>::Frag;
+  Frag f;
+  if constexpr (FMT == kFmtI8) {
+    f = lo_ok ? *(const i32x4*)p : i32x4{0, 0, 0, 0};
+  } else {
+    i32x4 lo = lo_ok ? *(const i32x4*)p : i32x4{0, 0, 0, 0};
+    i32x4 hi = hi_ok ? *(const i32x4*)(p + 16) : i32x4{0, 0, 0, 0};
+    f = i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  }
+  return f;
+}
+
+template <int FMT>
+KQ_DEV typename W8Traits<FMT>::Acc mfma_w8(typename W8Traits<FMT>::Frag a,
+                                           typename W8Traits<FMT>::Frag b,
+                                           typename W8Traits<FMT>::Acc c) {
+  if constexpr (FMT == kFmtI8) return mfma_i8(a, b, c);
+  else return mfma_fp8(a, b, c);
+}
+
+// ------------------------------------------------------------------ skinny
+// Workgroup = 16 output columns x a K range; its waves split the K range and
+// reduce through LDS.  Lane (j, kg) streams 16 (INT8) or 32 (FP8) contiguous
+// weight bytes of row n = tile*16 + j straight into the MFMA B operand.
+constexpr int kSkinnyWaves = 8;
+constexpr int kSkinnyCols = 16;
+
+template <int FMT, int MT, int U>
+__global__ void __launch_bounds__(64 * kSkinnyWaves)
+w8a8_skinny_kernel(const uint8_t* __restrict__ xq, const uint8_t* __restrict__ w, int K,
+                   int steps_per_split, int splits, Epi ep, void* __restrict__ partials) {
+  using T = W8Traits<FMT>;
+  using Acc = typename T::Acc;
+  using Frag = typename T::Frag;
+  __shared__ uint32_t red[(kSkinnyWaves - 1) * MT * 4 * 64];
+  const int lane = lane_id(), wave = wave_id();
+  const int j = lane & 15, kg = lane >> 4;
+  const int tile = blockIdx.x / splits, split = blockIdx.x % splits;
+  const int n = tile * kSkinnyCols + j;
+  const bool n_ok = n < ep.N;
+  const int nsteps = (K + T::kStep - 1) / T::kStep;
+  const int sbeg = split * steps_per_split;
+  const int send = min(nsteps, sbeg + steps_per_split);
+  const int per_wave = (send - sbeg + kSkinnyWaves - 1) / kSkinnyWaves;
+  const int wbeg = sbeg + wave * per_wave;
+  const int wend = min(send, wbeg + per_wave);
+  const uint8_t* wrow = w + (int64_t)(n_ok ? n : 0) * K;
+
+  Acc acc[MT];
+#pragma unroll
+  for (int t = 0; t < MT; ++t) acc[t] = Acc{0, 0, 0, 0};
+
+  for (int st = wbeg; st < wend; st += U) {
+    Frag b[U];
+    Frag a[U][MT];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const bool s_ok = st + u < wend;
+      const int k = (st + u) * T::kStep + kg * T::kLane;
+      b[u] = load_frag<FMT>(wrow + k, s_ok && n_ok && k < K, s_ok && n_ok && k + 16 < K);
+#pragma unroll
+      for (int t = 0; t < MT; ++t) {
+        const int m = t * 16 + j;
+        const bool m_ok = s_ok && m < ep.M;
+        a[u][t] = load_frag<FMT>(xq + (int64_t)(m < ep.M ? m : 0) * K + k, m_ok && k < K,
+                                 m_ok && k + 16 < K);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int t = 0; t < MT; ++t) acc[t] = mfma_w8<FMT>(a[u][t], b[u], acc[t]);
+  }
+
+  // fixed-order reduction of the waves' K ranges
+  if (wave > 0) {
+#pragma unroll
+    for (int t = 0; t < MT; ++t)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        red[(((wave - 1) * MT + t) * 4 + r) * 64 + lane] = acc_bits(acc[t], r);
+  }
+  __syncthreads();
+  if (wave != 0) return;
+  for (int w2 = 1; w2 < kSkinnyWaves; ++w2)
+#pragma unroll
+    for (int t = 0; t < MT; ++t)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const uint32_t bits = red[(((w2 - 1) * MT + t) * 4 + r) * 64 + lane];
+        if constexpr (FMT == kFmtI8) acc[t][r] += (int)bits;
+        else acc[t][r] = __fadd_rn(acc[t][r], __uint_as_float(bits));
+      }
+
+  if (splits == 1) {
+#pragma unroll
+    for (int t = 0; t < MT; ++t)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) epi_store<FMT>(ep, t * 16 + kg * 4 + r, n, acc[t], r);
+    return;
+  }
+  uint32_t* part = (uint32_t*)partials + (size_t)split * ep.M * ep.N;
+#pragma unroll
+  for (int t = 0; t < MT; ++t)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int m = t * 16 + kg * 4 + r;
+      if (m < ep.M && n_ok) part[(int64_t)m * ep.N + n] = acc_bits(acc[t], r);
+    }
+}
+
+// ------------------------------------------------------------------- tiled
+constexpr int kTile = 128;      // BM = BN = BK(bytes) = 128
+constexpr int kTileBytes = kTile * kTile;
+
+// byte offset of 16-byte chunk `c` (0..7) of row `r` in a swizzled tile
+KQ_DEV int swz(int r, int c) { return r * kTile + ((c ^ (r & 7)) << 4); }
+
+template <int FMT>
+__global__ void __launch_bounds__(256)
+w8a8_tile_kernel(const uint8_t* __restrict__ xq, const uint8_t* __restrict__ w, int K,
+                 int tiles_n, Epi ep) {
+  using T = W8Traits<FMT>;
+  using Acc = typename T::Acc;
+  using Frag = typename T::Frag;
+  __shared__ __attribute__((aligned(16))) uint8_t smem[2][2][kTileBytes];
+
+  const int tid = threadIdx.x, lane = lane_id(), wave = wave_id();
+  const int j = lane & 15, kg = lane >> 4;
+  const int wm = wave >> 1, wn = wave & 1;
+  // grouped tile order: 8 row-tiles share each sweep over column tiles
+  const int nblocks = gridDim.x;
+  const int pid = xcd_swizzle(blockIdx.x, nblocks);
+  const int tiles_m = (ep.M + kTile - 1) / kTile;
+  const int group = 8 * tiles_n;
+  const int gid = pid / group;
+  const int first_m = gid * 8;
+  const int gsize = min(tiles_m - first_m, 8);
+  const int tm = first_m + (pid % group) % gsize;
+  const int tn = (pid % group) / gsize;
+  const int m0 = tm * kTile, n0 = tn * kTile;
+
+  Acc acc[4][4];
+#pragma unroll
+  for (int a = 0; a < 4; ++a)
+#pragma unroll
+    for (int b = 0; b < 4; ++b) acc[a][b] = Acc{0, 0, 0, 0};
+
+  i32x4 ra[4], rb[4];
+  auto gload = [&](int k0) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int c = tid + 256 * q;
+      const int row = c >> 3, ch = c & 7;
+      const int kc = k0 + ch * 16;
+      const int m = m0 + row, n = n0 + row;
+      ra[q] = (m < ep.M && kc < K) ? *(const i32x4*)(xq + (int64_t)m * K + kc) : i32x4{0, 0, 0, 0};
+      rb[q] = (n < ep.N && kc < K) ? *(const i32x4*)(w + (int64_t)n * K + kc) : i32x4{0, 0, 0, 0};
+    }
+  };
+  auto sstore = [&](int buf) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int c = tid + 256 * q;
+      const int row = c >> 3, ch = c & 7;
+      *(i32x4*)(&smem[buf][0][swz(row, ch)]) = ra[q];
+      *(i32x4*)(&smem[buf][1][swz(row, ch)]) = rb[q];
+    }
+  };
+  auto lfrag = [&](const uint8_t* s, int row, int ch0) -> Frag {
+    if constexpr (FMT == kFmtI8) {
+      return *(const i32x4*)(s + swz(row, ch0));
+    } else {
+      i32x4 lo = *(const i32x4*)(s + swz(row, ch0));
+      i32x4 hi = *(const i32x4*)(s + swz(row, ch0 + 1));
+      return i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    }
+  };
+
+  const int nk = (K + kTile - 1) / kTile;
+  gload(0);
+  sstore(0);
+  __syncthreads();
+  for (int s = 0; s < nk; ++s) {
+    const int cur = s & 1;
+    if (s + 1 < nk) gload((s + 1) * kTile);
+    const uint8_t* sa = smem[cur][0];
+    const uint8_t* sb = smem[cur][1];
+    constexpr int kSteps = kTile / T::kStep;
+#pragma unroll
+    for (int ks = 0; ks < kSteps; ++ks) {
+      const int ch0 = ks * (T::kStep / 16) + kg * (T::kLane / 16);
+      Frag fa[4], fb[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) fa[i] = lfrag(sa, wm * 64 + i * 16 + j, ch0);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) fb[i] = lfrag(sb, wn * 64 + i * 16 + j, ch0);
+#pragma unroll
+      for (int a = 0; a < 4; ++a)
+#pragma unroll
+        for (int b = 0; b < 4; ++b) acc[a][b] = mfma_w8<FMT>(fa[a], fb[b], acc[a][b]);
+    }
+    if (s + 1 < nk) sstore(cur ^ 1);
+    __syncthreads();
+  }
+
+#pragma unroll
+  for (int a = 0; a < 4; ++a)
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        epi_store<FMT>(ep, m0 + wm * 64 + a * 16 + kg * 4 + r, n0 + wn * 64 + b * 16 + j,
+                       acc[a][b], r);
+}
+
+// --------------------------------------------------------------- generic
+// One thread per output; any K.  Used only when K is not a multiple of 16.
+template <int FMT>
+__global__ void w8a8_generic_kernel(const uint8_t* __restrict__ xq, const uint8_t* __restrict__ w,
+                                    int K, Epi ep) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= (int64_t)ep.M * ep.N) return;
+  const int m = (int)(idx / ep.N), n = (int)(idx % ep.N);
+  typename W8Traits<FMT>::Acc acc = {0, 0, 0, 0};
+  if constexpr (FMT == kFmtI8) {
+    int s = 0;
+    for (int k = 0; k < K; ++k)
+      s += (int)(int8_t)xq[(int64_t)m * K + k] * (int)(int8_t)w[(int64_t)n * K + k];
+    acc[0] = s;
+  } else {
+    float s = 0.0f;
+    for (int k = 0; k < K; ++k)
+      s = __fadd_rn(s, __fmul_rn(e4m3_to_f32(xq[(int64_t)m * K + k]),
+                                 e4m3_to_f32(w[(int64_t)n * K + k])));
+    acc[0] = s;
+  }
+  epi_store<FMT>(ep, m, n, acc, 0);
+}
+
+// ------------------------------------------------------------------ host
+template <int FMT, int MT>
+static void launch_skinny(const uint8_t* xq, const uint8_t* w, int K, const Epi& ep,
+                          void* workspace, size_t ws_bytes, hipStream_t stream) {
+  using T = W8Traits<FMT>;
+  const int tiles = (ep.N + kSkinnyCols - 1) / kSkinnyCols;
+  const int nsteps = (K + T::kStep - 1) / T::kStep;
+  // Fill the 256 CUs: split K across workgroups only when there are fewer
+  // tiles than CUs and every wave keeps >= 2 MFMA steps.
+  int splits = 1;
+  const size_t plane = (size_t)ep.M * ep.N * 4;
+  while (workspace && tiles * splits < 256 && nsteps / (splits * 2 * kSkinnyWaves) >= 2 &&
+         plane * splits * 2 <= ws_bytes)
+    splits *= 2;
+  const int steps_per_split = (nsteps + splits - 1) / splits;
+  constexpr int U = FMT == kFmtI8 ? 4 : 2;
+  hipLaunchKernelGGL((w8a8_skinny_kernel<FMT, MT, U>), dim3(tiles * splits),
+                     dim3(64 * kSkinnyWaves), 0, stream, xq, w, K, steps_per_split, splits, ep,
+                     workspace);
+  if (splits > 1) {
+    ReduceArgs r{workspace, splits, ep.M, ep.N, ep.xscale, ep.wscale, ep.ws_per_channel,
+                 ep.bias, ep.bias_dtype, ep.out, ep.out_dtype, ep.acc_out};
+    launch_splitk_reduce(FMT == kFmtI8 ? kReduceI8 : kReduceFp8, r, stream);
+  }
+}
+
+template <int FMT>
+static int run_w8a8(const char* what, const uint8_t* xq, const uint8_t* w, int64_t m,
+                    int64_t n, int64_t k, const Epi& ep, void* workspace, size_t ws_bytes,
+                    hipStream_t stream) {
+  if (m < 0 || n < 1 || k < 1 || m > 0x7fffffff || n > 0x7fffffff || k > 0x7fffffff ||
+      m * k > 0x7fffffffffffLL) {
+    set_error("%s: bad shape m=%lld n=%lld k=%lld", what, (long long)m, (long long)n,
+              (long long)k);
+    return KQ_EINVAL;
+  }
+  if (ep.out_dtype != KQ_DTYPE_F16 && ep.out_dtype != KQ_DTYPE_BF16) {
+    set_error("%s: output dtype must be fp16 or bf16", what);
+    return KQ_EUNSUPPORTED;
+  }
+  if (m == 0) return KQ_OK;
+  const int K = (int)k;
+  if ((K % 16) != 0 || ((uintptr_t)xq % 16) || ((uintptr_t)w % 16)) {
+    const int64_t total = m * n;
+    hipLaunchKernelGGL(w8a8_generic_kernel<FMT>, dim3((unsigned)((total + 255) / 256)),
+                       dim3(256), 0, stream, xq, w, K, ep);
+    return check_launch(what);
+  }
+  if (m <= 16) launch_skinny<FMT, 1>(xq, w, K, ep, workspace, ws_bytes, stream);
+  else if (m <= 32) launch_skinny<FMT, 2>(xq, w, K, ep, workspace, ws_bytes, stream);
+  else if (m <= 64) launch_skinny<FMT, 4>(xq, w, K, ep, workspace, ws_bytes, stream);
+  else {
+    const int tiles_m = (int)((m + kTile - 1) / kTile);
+    const int tiles_n = (int)((n + kTile - 1) / kTile);
+    hipLaunchKernelGGL(w8a8_tile_kernel<FMT>, dim3(tiles_m * tiles_n), dim3(256), 0, stream, xq,
+                       w, K, tiles_n, ep);
+  }
+  return check_launch(what);
+}
+
+}  // namespace kq
+
+using namespace kq;
+
+extern "C" int kq_w8a8_i8_gemm(const int8_t* xq, const float* xscale, const int8_t* w,
+                               const float* wscale, const void* bias, int bias_dtype,
+                               void* out, int out_dtype, int32_t* acc_out, int64_t m, int64_t n,
+                               int64_t k, void* workspace, size_t workspace_bytes,
+                               void* stream) {
+  Epi ep{xscale, wscale, 1, bias, bias_dtype, out, out_dtype, acc_out, (int)m, (int)n};
+  return run_w8a8<kFmtI8>("kq_w8a8_i8_gemm", (const uint8_t*)xq, (const uint8_t*)w, m, n, k, ep,
+                          workspace, workspace_bytes, (hipStream_t)stream);
+}
+
+extern "C" int kq_w8a8_fp8_gemm(const uint8_t* xq, const float* xscale, const uint8_t* w,
+                                const float* wscale, int wscale_per_channel, const void* bias,
+                                int bias_dtype, void* out, int out_dtype, int64_t m, int64_t n,
+                                int64_t k, void* workspace, size_t workspace_bytes,
+                                void* stream) {
+  Epi ep{xscale, wscale, wscale_per_channel, bias, bias_dtype, out, out_dtype, nullptr,
+         (int)m, (int)n};
+  return run_w8a8<kFmtFp8>("kq_w8a8_fp8_gemm", xq, w, m, n, k, ep, workspace, workspace_bytes,
+                           (hipStream_t)stream);
+}

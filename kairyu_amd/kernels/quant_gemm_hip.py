@@ -1,0 +1,350 @@
+"""Device forwards of the quantized linear formats on gfx950.
+
+Interface of kairyu/kernels/quant_gemm_gpu.py:409-1024 (``_prepare``,
+``_validate_layout``, ``_quantize_activation``, ``fp8_activation_amax``,
+``fp8/int8/awq/gptq_linear_forward``, ``linear_forward``).  Each forward
+validates fail-closed before launch (RuntimeError for backend / device / dtype
+problems, ValueError for shape and packed-layout mismatches), flattens ``x`` to
+``[M, K]``, allocates the output in ``x.dtype`` and launches the HIP kernels of
+``libkairyu_quant.so`` on torch's current stream.  No path materializes a
+floating-point ``[out, in]`` weight and there is no dequantized fallback.
+"""
+
+from __future__ import annotations
+
+from functools import lru_cache
+
+import torch
+
+from kairyu_amd import _native
+
+REQUIRED_ARCH = "gfx950"
+
+
+@lru_cache(maxsize=None)
+def _arch_of(index: int) -> str:
+    return str(torch.cuda.get_device_properties(index).gcnArchName).split(":")[0]
+
+
+def _device_arch(device: torch.device) -> str:
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    return _arch_of(index)
+
+
+def _prepare(x: torch.Tensor, module, scheme: str, *, allocate_output: bool = True):
+    try:
+        _native.library()
+    except RuntimeError as error:
+        raise RuntimeError(
+            f"{scheme} device execution requires the kairyu_amd HIP library: {error}"
+        ) from error
+    if not x.is_cuda:
+        raise RuntimeError(f"{scheme} fused kernel requires a ROCm device activation")
+    if x.dtype not in (torch.float16, torch.bfloat16):
+        raise RuntimeError(
+            f"{scheme} fused kernel supports float16/bfloat16 activations, got {x.dtype}"
+        )
+    arch = _device_arch(x.device)
+    if arch != REQUIRED_ARCH:
+        raise RuntimeError(
+            f"{scheme} fused kernel requires {REQUIRED_ARCH}, got {arch}; "
+            "no dequantized GPU fallback exists"
+        )
+    if x.shape[-1] != module.in_features:
+        raise ValueError(f"{scheme} linear expected K={module.in_features}, got {x.shape[-1]}")
+    payload = list(module.buffers(recurse=False))
+    if module.bias is not None:
+        payload.append(module.bias)
+    misplaced = [t.device for t in payload if t.device != x.device]
+    if misplaced:
+        raise RuntimeError(
+            f"{scheme} fused kernel requires module payloads on {x.device}; found {misplaced[0]}"
+        )
+    _validate_layout(module, scheme)
+    flat = x.reshape(-1, x.shape[-1]).contiguous()
+    out = (
+        torch.empty((flat.shape[0], module.out_features), device=x.device, dtype=x.dtype)
+        if allocate_output
+        else None
+    )
+    return flat, out
+
+
+def _validate_layout(module, scheme: str) -> None:
+    n, k = module.out_features, module.in_features
+    if scheme == "fp8":
+        if tuple(module.weight.shape) != (n, k):
+            raise ValueError(f"FP8 weight shape {tuple(module.weight.shape)} != {(n, k)}")
+        if module.weight.dtype != torch.float8_e4m3fn:
+            raise ValueError(f"FP8 weight dtype {module.weight.dtype} != float8_e4m3fn")
+        if module.weight_scale.numel() not in (1, n):
+            raise ValueError(
+                "FP8 weight_scale must be scalar or per-output-channel, got "
+                f"{tuple(module.weight_scale.shape)}"
+            )
+        if not module.activation_dynamic and module.input_scale.numel() != 1:
+            raise ValueError("static FP8 input_scale must be scalar")
+    elif scheme == "int8":
+        if tuple(module.weight.shape) != (n, k):
+            raise ValueError(f"INT8 weight shape {tuple(module.weight.shape)} != {(n, k)}")
+        if module.weight.dtype != torch.int8:
+            raise ValueError(f"INT8 weight dtype {module.weight.dtype} != int8")
+        if module.weight_scale.numel() != n:
+            raise ValueError("INT8 weight_scale must be per-output-channel")
+    elif scheme == "awq":
+        expected = ((k, n // 8), (k // module.group_size, n // 8), (k // module.group_size, n))
+        actual = tuple(tuple(t.shape) for t in (module.qweight, module.qzeros, module.scales))
+        if actual != expected:
+            raise ValueError(f"AWQ packed layout {actual} != {expected}")
+    elif scheme == "gptq":
+        groups = -(-k // module.group_size)
+        expected = ((k // 8, n), (groups, n // 8), (groups, n), (k,))
+        actual = tuple(
+            tuple(t.shape) for t in (module.qweight, module.qzeros, module.scales, module.g_idx)
+        )
+        if actual != expected:
+            raise ValueError(f"GPTQ packed layout {actual} != {expected}")
+    elif scheme == "fp8_block":
+        expected = ((n, k), (-(-n // 128), -(-k // 128)))
+        actual = (tuple(module.weight.shape), tuple(module.weight_scale_inv.shape))
+        if actual != expected:
+            raise ValueError(f"block FP8 layout {actual} != {expected}")
+    if scheme in ("awq", "gptq") and module.scales.dtype != torch.float16:
+        raise RuntimeError(
+            f"{scheme} kernels consume fp16 checkpoint scales, got {module.scales.dtype}"
+        )
+
+
+def _f32(t: torch.Tensor) -> torch.Tensor:
+    t = t.reshape(-1)
+    if t.dtype != torch.float32:
+        t = t.to(torch.float32)
+    return t.contiguous()
+
+
+def _bias(module, add_bias: bool) -> torch.Tensor | None:
+    if not add_bias or module.bias is None:
+        return None
+    return module.bias.contiguous()
+
+
+def _workspace(device: torch.device, nbytes: int = 0) -> torch.Tensor:
+    return _native.workspace(device, nbytes)
+
+
+def _w4_workspace(device: torch.device, m: int, n: int, k: int, mode: int) -> torch.Tensor:
+    need = int(_native.library().kq_w4a16_workspace_size(m, n, k, mode))
+    return _workspace(device, need)
+
+
+def _quantize_activation(
+    flat: torch.Tensor,
+    dtype: torch.dtype,
+    quant_max: float,
+    static_scale: torch.Tensor | None = None,
+    row_scale: torch.Tensor | None = None,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """Per-token quantization of ``flat [M, K]`` -> (int8 or e4m3 ``[M, K]``, fp32 ``[M, 1]``)."""
+
+    if static_scale is not None and row_scale is not None:
+        raise ValueError("activation quantization accepts one scale source")
+    if dtype not in (torch.int8, torch.float8_e4m3fn):
+        raise RuntimeError(f"unsupported activation quantization dtype {dtype}")
+    rows, k = flat.shape
+    quantized = torch.empty((rows, k), device=flat.device, dtype=dtype)
+    scales = torch.empty((rows, 1), device=flat.device, dtype=torch.float32)
+    stream = _native.stream_handle(flat.device)
+    if dtype is torch.int8:
+        if static_scale is not None or row_scale is not None or quant_max != 127.0:
+            raise ValueError("INT8 activation quantization is dynamic per token with max 127")
+        _native.call(
+            "kq_act_quant_i8",
+            flat.data_ptr(), _native.dtype_code(flat.dtype), rows, k, flat.stride(0),
+            quantized.data_ptr(), scales.data_ptr(), stream,
+        )
+        return quantized, scales
+    if quant_max != 448.0:
+        raise ValueError("FP8 e4m3 activation quantization uses max 448")
+    mode, source = 0, None
+    if row_scale is not None:
+        mode, source = 2, _f32(row_scale.reshape(rows, 1).to(flat.device))
+    elif static_scale is not None:
+        mode, source = 1, _f32(static_scale.to(flat.device))
+    _native.call(
+        "kq_act_quant_fp8",
+        flat.data_ptr(), _native.dtype_code(flat.dtype), rows, k, flat.stride(0),
+        _native.ptr(source), mode, quantized.data_ptr(), scales.data_ptr(), stream,
+    )
+    return quantized, scales
+
+
+def fp8_activation_amax(x: torch.Tensor) -> torch.Tensor:
+    """Per-token fp32 amax ``[..., 1]`` without an fp32 activation temporary."""
+
+    _native.library()
+    if x.dtype not in (torch.float16, torch.bfloat16):
+        raise RuntimeError(f"activation amax supports float16/bfloat16, got {x.dtype}")
+    flat = x.reshape(-1, x.shape[-1]).contiguous()
+    out = torch.empty((flat.shape[0], 1), device=flat.device, dtype=torch.float32)
+    _native.call(
+        "kq_row_amax",
+        flat.data_ptr(), _native.dtype_code(flat.dtype), flat.shape[0], flat.shape[1],
+        flat.stride(0), out.data_ptr(), _native.stream_handle(flat.device),
+    )
+    return out.reshape(*x.shape[:-1], 1)
+
+
+def fp8_linear_forward(
+    x: torch.Tensor,
+    module,
+    activation_scale: torch.Tensor | None = None,
+    *,
+    add_bias: bool = True,
+) -> torch.Tensor:
+    flat, out = _prepare(x, module, "fp8")
+    input_scale = None if module.activation_dynamic else module.input_scale
+    x_q, x_scale = _quantize_activation(
+        flat, torch.float8_e4m3fn, 448.0, static_scale=input_scale, row_scale=activation_scale
+    )
+    weight_scale = _f32(module.weight_scale)
+    bias = _bias(module, add_bias)
+    ws = _workspace(x.device)
+    m, k = flat.shape
+    _native.call(
+        "kq_w8a8_fp8_gemm",
+        x_q.data_ptr(), x_scale.data_ptr(), module.weight.data_ptr(), weight_scale.data_ptr(),
+        int(weight_scale.numel() != 1), _native.ptr(bias),
+        _native.dtype_code(None if bias is None else bias.dtype), out.data_ptr(),
+        _native.dtype_code(x.dtype), m, module.out_features, k, ws.data_ptr(), ws.numel(),
+        _native.stream_handle(x.device),
+    )
+    return out.reshape(*x.shape[:-1], module.out_features)
+
+
+def int8_linear_forward(x: torch.Tensor, module, *, add_bias: bool = True,
+                        accumulators: torch.Tensor | None = None) -> torch.Tensor:
+    """INT8 W8A8.  ``accumulators`` (int32 ``[M, N]``, optional) receives the raw
+    int32 dot products for bit-exact checks."""
+
+    flat, out = _prepare(x, module, "int8")
+    x_q, x_scale = _quantize_activation(flat, torch.int8, 127.0)
+    weight_scale = _f32(module.weight_scale)
+    bias = _bias(module, add_bias)
+    ws = _workspace(x.device)
+    m, k = flat.shape
+    if accumulators is not None and (
+        accumulators.dtype != torch.int32
+        or tuple(accumulators.shape) != (m, module.out_features)
+        or not accumulators.is_contiguous()
+        or accumulators.device != x.device
+    ):
+        raise ValueError("accumulators must be a contiguous int32 [M, N] tensor on the device")
+    _native.call(
+        "kq_w8a8_i8_gemm",
+        x_q.data_ptr(), x_scale.data_ptr(), module.weight.data_ptr(), weight_scale.data_ptr(),
+        _native.ptr(bias), _native.dtype_code(None if bias is None else bias.dtype),
+        out.data_ptr(), _native.dtype_code(x.dtype), _native.ptr(accumulators), m,
+        module.out_features, k, ws.data_ptr(), ws.numel(), _native.stream_handle(x.device),
+    )
+    return out.reshape(*x.shape[:-1], module.out_features)
+
+
+GIDX_UNIFORM = 0
+GIDX_PERMUTED = 1
+GIDX_PER_K = 2
+
+
+def awq_linear_forward(x: torch.Tensor, module, *, add_bias: bool = True) -> torch.Tensor:
+    flat, out = _prepare(x, module, "awq")
+    bias = _bias(module, add_bias)
+    m, k = flat.shape
+    ws = _w4_workspace(x.device, m, module.out_features, k, GIDX_UNIFORM)
+    _native.call(
+        "kq_w4a16_awq_gemm",
+        flat.data_ptr(), _native.dtype_code(flat.dtype), module.qweight.data_ptr(),
+        module.qzeros.data_ptr(), module.scales.data_ptr(), _native.ptr(bias),
+        _native.dtype_code(None if bias is None else bias.dtype), out.data_ptr(), m,
+        module.out_features, k, module.group_size, ws.data_ptr(), ws.numel(),
+        _native.stream_handle(x.device),
+    )
+    return out.reshape(*x.shape[:-1], module.out_features)
+
+
+def _gptq_operands(module, device: torch.device):
+    """(gidx_mode, qweight operand, perm or None) for a GPTQ module.
+
+    ``g_idx == k // group_size`` runs on the checkpoint buffers directly.  An
+    act-order ``g_idx`` whose stable sort groups every ``group_size`` rows
+    together gets a K-permuted copy of ``qweight`` (derived, non-persistent,
+    rebuilt when a source tensor's version changes) and gathers ``x`` through
+    the permutation; any other ``g_idx`` uses the per-element group path.
+    """
+
+    g_idx, qweight = module.g_idx, module.qweight
+    key = (id(g_idx), g_idx._version, id(qweight), qweight._version, str(device))
+    cached = module.__dict__.get("_kq_gptq_operands")
+    if cached is not None and cached[0] == key:
+        return cached[1]
+    k, group = module.in_features, module.group_size
+    natural = torch.arange(k, device=device, dtype=torch.int64) // group
+    gi = g_idx.to(torch.int64)
+    if torch.equal(gi, natural):
+        result = (GIDX_UNIFORM, qweight, None)
+    else:
+        perm = torch.argsort(gi, stable=True)
+        if group % 8 == 0 and torch.equal(gi[perm], natural):
+            perm32 = perm.to(torch.int32).contiguous()
+            permuted = torch.empty_like(qweight)
+            _native.call(
+                "kq_gptq_permute_qweight",
+                qweight.data_ptr(), perm32.data_ptr(), permuted.data_ptr(),
+                module.out_features, k, _native.stream_handle(device),
+            )
+            result = (GIDX_PERMUTED, permuted, perm32)
+        else:
+            result = (GIDX_PER_K, qweight, None)
+    object.__setattr__(module, "_kq_gptq_operands", (key, result))
+    return result
+
+
+def gptq_linear_forward(x: torch.Tensor, module, *, add_bias: bool = True) -> torch.Tensor:
+    flat, out = _prepare(x, module, "gptq")
+    mode, qweight, perm = _gptq_operands(module, x.device)
+    g_idx = module.g_idx if module.g_idx.dtype == torch.int32 else module.g_idx.to(torch.int32)
+    bias = _bias(module, add_bias)
+    m, k = flat.shape
+    ws = _w4_workspace(x.device, m, module.out_features, k, mode)
+    _native.call(
+        "kq_w4a16_gptq_gemm",
+        flat.data_ptr(), _native.dtype_code(flat.dtype), qweight.data_ptr(),
+        module.qzeros.data_ptr(), module.scales.data_ptr(), g_idx.data_ptr(),
+        _native.ptr(perm), mode, _native.ptr(bias),
+        _native.dtype_code(None if bias is None else bias.dtype), out.data_ptr(), m,
+        module.out_features, k, module.group_size, ws.data_ptr(), ws.numel(),
+        _native.stream_handle(x.device),
+    )
+    return out.reshape(*x.shape[:-1], module.out_features)
+
+
+def block_fp8_linear_forward(x: torch.Tensor, module, *, add_bias: bool = True) -> torch.Tensor:
+    flat, out = _prepare(x, module, "fp8_block")
+    from kairyu_amd import moe
+
+    result = moe.block_fp8_dense_forward(flat, module, add_bias=add_bias, out=out)
+    return result.reshape(*x.shape[:-1], module.out_features)
+
+
+_DISPATCH = {
+    "fp8": fp8_linear_forward,
+    "int8": int8_linear_forward,
+    "awq": awq_linear_forward,
+    "gptq": gptq_linear_forward,
+    "fp8_block": block_fp8_linear_forward,
+}
+
+
+def linear_forward(x: torch.Tensor, module, *, add_bias: bool = True) -> torch.Tensor:
+    scheme = getattr(module, "quant_scheme", None)
+    if scheme not in _DISPATCH:
+        raise RuntimeError(f"no fused GPU kernel registered for {scheme!r}")
+    return _DISPATCH[scheme](x, module, add_bias=add_bias)

@@ -1,0 +1,140 @@
+"""Seeded synthetic workloads for the BASELINE configurations.
+
+Each builder returns ready-to-run quantized modules (the package's own
+``AwqLinear`` / ``GptqLinear`` / ``Fp8Linear`` / ``Int8Linear``) and
+activations, generated with ``torch.Generator`` on the requested device, plus
+the algorithmic byte / FLOP counts the roofline uses.  No checkpoint or
+dataset is involved (there is no network); shapes and distributions follow
+the configuration text.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+
+import torch
+
+from kairyu_amd.quant import awq as awq_format
+from kairyu_amd.quant import gptq as gptq_format
+from kairyu_amd.quant.fp8 import quantize_fp8
+from kairyu_amd.quant.int8 import quantize_int8_weight
+from kairyu_amd.quant.linear import AwqLinear, Fp8Linear, GptqLinear, Int8Linear
+
+
+@dataclass
+class Workload:
+    name: str
+    module: torch.nn.Module
+    x: torch.Tensor
+    bytes: int
+    flops: int
+    bound: str  # "hbm" | "mfma"
+    extra: dict = field(default_factory=dict)
+
+
+def _gen(device, seed: int) -> torch.Generator:
+    g = torch.Generator(device=device)
+    g.manual_seed(seed)
+    return g
+
+
+def _uniform(shape, lo, hi, g, device, dtype=torch.float32):
+    return (torch.rand(shape, generator=g, device=device) * (hi - lo) + lo).to(dtype)
+
+
+def awq_layer(m: int = 16, n: int = 4096, k: int = 4096, group: int = 128, seed: int = 0,
+              device="cuda", x_dtype=torch.float16) -> Workload:
+    """C1: AWQ W4A16, asymmetric int4, q,z ~ U{0..15}, scales ~ U(0.002, 0.02)."""
+
+    g = _gen(device, seed)
+    q = torch.randint(0, 16, (k, n), generator=g, device=device, dtype=torch.int32)
+    z = torch.randint(0, 16, (k // group, n), generator=g, device=device, dtype=torch.int32)
+    scales = _uniform((k // group, n), 0.002, 0.02, g, device, torch.float16)
+    x = torch.randn((m, k), generator=g, device=device).to(x_dtype)
+    module = AwqLinear(k, n, bias=False, group_size=group).to(device)
+    module.qweight.copy_(awq_format.pack_awq(q))
+    module.qzeros.copy_(awq_format.pack_awq(z))
+    module.scales.copy_(scales)
+    nbytes = k * n // 2 + (k // group) * (n // 8) * 4 + (k // group) * n * 2 + m * k * 2 + m * n * 2
+    return Workload(f"awq_w4a16_m{m}_n{n}_k{k}_g{group}", module, x, nbytes, 2 * m * n * k,
+                    "hbm" if m <= 64 else "mfma")
+
+
+def gptq_layer(m: int = 16, n: int = 28672, k: int = 4096, group: int = 128, seed: int = 0,
+               device="cuda", x_dtype=torch.float16, act_order: bool = True) -> Workload:
+    """C2: GPTQ W4A16 symmetric (stored zeros 7, z = 8), act-order g_idx =
+    randperm(K) // group, scales ~ U(0.001, 0.01)."""
+
+    g = _gen(device, seed)
+    q = torch.randint(0, 16, (k, n), generator=g, device=device, dtype=torch.int32)
+    groups = -(-k // group)
+    scales = _uniform((groups, n), 0.001, 0.01, g, device, torch.float16)
+    if act_order:
+        g_idx = (torch.randperm(k, generator=g, device=device) // group).to(torch.int32)
+    else:
+        g_idx = (torch.arange(k, device=device) // group).to(torch.int32)
+    x = torch.randn((m, k), generator=g, device=device).to(x_dtype)
+    module = GptqLinear(k, n, bias=False, group_size=group).to(device)
+    module.qweight.copy_(gptq_format.pack_gptq_rows(q))
+    module.qzeros.copy_(
+        gptq_format.pack_gptq_cols(torch.full((groups, n), 7, dtype=torch.int32)).to(device)
+    )
+    module.scales.copy_(scales)
+    module.g_idx.copy_(g_idx)
+    nbytes = (k * n // 2 + groups * (n // 8) * 4 + groups * n * 2 + 4 * k + m * k * 2 + m * n * 2)
+    return Workload(f"gptq_w4a16_actorder_m{m}_n{n}_k{k}_g{group}", module, x, nbytes,
+                    2 * m * n * k, "hbm" if m <= 64 else "mfma")
+
+
+def fp8_layer(m: int = 16, n: int = 4096, k: int = 14336, seed: int = 0, device="cuda",
+              x_dtype=torch.bfloat16) -> Workload:
+    """C3: FP8 e4m3 W8A8, W ~ N(0, 0.02) per-channel; x ~ N(0,1) with exactly
+    floor(0.01*M*K) (at least one) seeded outliers x20; dynamic per-token quant."""
+
+    g = _gen(device, seed)
+    w = torch.randn((n, k), generator=g, device=device) * 0.02
+    qw, ws = quantize_fp8(w, per_channel=True)
+    del w
+    x = torch.randn((m, k), generator=g, device=device)
+    count = max(1, (m * k) // 100)
+    flat_idx = torch.randperm(m * k, generator=g, device=device)[:count]
+    x.view(-1)[flat_idx] *= 20.0
+    module = Fp8Linear(k, n, bias=False).to(device)
+    module.weight.copy_(qw)
+    module.weight_scale.copy_(ws)
+    nbytes = n * k + 4 * n + 2 * m * k + 2 * m * n + 4 * m
+    return Workload(f"fp8_w8a8_m{m}_n{n}_k{k}", module, x.to(x_dtype), nbytes, 2 * m * n * k,
+                    "hbm" if m <= 64 else "mfma")
+
+
+def int8_layer(m: int = 16, n: int = 18944, k: int = 3584, seed: int = 0, device="cuda",
+               x_dtype=torch.bfloat16) -> Workload:
+    """C4: INT8 W8A8 SmoothQuant-style, W ~ N(0, 0.02) per-channel int8; x ~ N(0,1)."""
+
+    g = _gen(device, seed)
+    w = torch.randn((n, k), generator=g, device=device) * 0.02
+    qw, ws = quantize_int8_weight(w)
+    del w
+    x = torch.randn((m, k), generator=g, device=device).to(x_dtype)
+    module = Int8Linear(k, n, bias=False).to(device)
+    module.weight.copy_(qw)
+    module.weight_scale.copy_(ws)
+    nbytes = n * k + 4 * n + 2 * m * k + 2 * m * n + 4 * m
+    return Workload(f"int8_w8a8_m{m}_n{n}_k{k}", module, x, nbytes, 2 * m * n * k,
+                    "hbm" if m <= 64 else "mfma")
+
+
+def replicas(workload: Workload, copies: int) -> list[torch.nn.Module]:
+    """Independent copies of a workload's module (distinct HBM allocations), used
+    to rotate weights so repeated calls cannot be served from the 256 MB MALL."""
+
+    mods = [workload.module]
+    for _ in range(copies - 1):
+        clone = type(workload.module).__new__(type(workload.module))
+        clone.__dict__ = dict(workload.module.__dict__)
+        clone._buffers = {name: t.clone() for name, t in workload.module._buffers.items()}
+        clone._parameters = dict(workload.module._parameters)
+        clone._modules = dict(workload.module._modules)
+        clone.__dict__.pop("_kq_gptq_operands", None)
+        mods.append(clone)
+    return mods

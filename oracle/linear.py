@@ -1,0 +1,119 @@
+"""Reference forwards of the quantized linear formats (numpy, exact accumulation).
+
+The device contract each kernel must meet, per scheme:
+
+* INT8 (kairyu/quant/linear.py:547-553, int8.py:33-41): activation bytes and
+  scales bit-exact; int32 accumulators bit-exact; output
+  ``((fp32(acc) * xs) * ws) + bias`` rounded to the activation dtype, bit-exact.
+* FP8 (linear.py:463-469, fp8.py:48-56): activation bytes and scales
+  bit-exact; ``acc`` is the exact sum of e4m3 products (computed here in fp64,
+  where it is exact: products are multiples of 2^-18 below 2^18); output
+  ``((acc * xs) * ws) + bias``; device output within 1e-2 normwise.
+* W4A16 (quant_gemm_gpu.py:224-407 contract): weights ``fp16((q - z) * s)``,
+  activation ``fp16(x)`` (bf16 saturated to +-65504), fp64 dot, ``+ bias``.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+from . import formats
+from .numerics import e4m3_decode, to_dtype, w4a16_activation
+
+
+def _bias_add(out32: np.ndarray, bias) -> np.ndarray:
+    if bias is None:
+        return out32
+    return (out32 + np.asarray(bias, dtype=np.float32)).astype(np.float32)
+
+
+def int8_accumulate(x_q, w_q) -> np.ndarray:
+    """Exact int32 accumulators.  fp64 BLAS is exact here: every partial sum is
+    an integer below 2^53 (|acc| <= K * 127^2)."""
+
+    acc = np.asarray(x_q, np.float64) @ np.asarray(w_q, np.float64).T
+    return acc.astype(np.int64)
+
+
+def int8_forward(x, w_q, w_scale, bias=None, out_dtype="bfloat16"):
+    """-> (out float32 holding out_dtype values, x_q, x_scale, acc)."""
+
+    x_q, x_scale = formats.int8_quantize_rows(x)
+    acc = int8_accumulate(x_q, w_q)
+    ws = np.asarray(w_scale, np.float32).reshape(1, -1)
+    out = (acc.astype(np.float32) * x_scale).astype(np.float32) * ws
+    out = _bias_add(out.astype(np.float32), bias)
+    return to_dtype(out, out_dtype), x_q, x_scale, acc
+
+
+def fp8_accumulate(x_bits, w_bits) -> np.ndarray:
+    """Exact sum of e4m3 products (fp64; exact for K < 2^14 * 2^18 range)."""
+
+    return e4m3_decode(x_bits).astype(np.float64) @ e4m3_decode(w_bits).astype(np.float64).T
+
+
+def fp8_forward(x, w_bits, w_scale, bias=None, out_dtype="bfloat16", static_scale=None,
+                row_scale=None):
+    """-> (out, x_bits, x_scale, out_fp32_before_cast)."""
+
+    x = np.asarray(x, np.float32)
+    if row_scale is not None:
+        scale = np.asarray(row_scale, np.float32).reshape(-1, 1)
+        from .numerics import e4m3_encode
+
+        x_bits = e4m3_encode(np.clip(x / scale, -448.0, 448.0))
+        x_scale = scale
+    else:
+        x_bits, x_scale = formats.fp8_quantize_rows(x, static_scale)
+    acc = fp8_accumulate(x_bits, w_bits).astype(np.float32)
+    ws = np.asarray(w_scale, np.float32).reshape(-1)
+    ws = ws.reshape(1, -1) if ws.size > 1 else ws.reshape(1, 1)
+    out = ((acc * x_scale).astype(np.float32) * ws).astype(np.float32)
+    out = _bias_add(out, bias)
+    return to_dtype(out, out_dtype), x_bits, x_scale, out
+
+
+def w4a16_forward(x, w_dequant_fp32, x_dtype: str, bias=None) -> np.ndarray:
+    """``w_dequant_fp32`` is ``(q - z) * s`` in fp32, [out, in]."""
+
+    a = w4a16_activation(x, x_dtype).astype(np.float64)
+    w = formats.w4a16_weight_fp16(w_dequant_fp32).astype(np.float64)
+    out = (a @ w.T).astype(np.float32)
+    out = _bias_add(out, bias)
+    return to_dtype(out, x_dtype)
+
+
+def awq_forward(x, qweight, qzeros, scales, group_size, x_dtype, bias=None) -> np.ndarray:
+    w = formats.awq_dequantize(qweight, qzeros, scales, group_size)
+    return w4a16_forward(x, w, x_dtype, bias)
+
+
+def gptq_forward(x, qweight, qzeros, scales, g_idx, x_dtype, bias=None) -> np.ndarray:
+    w = formats.gptq_dequantize(qweight, qzeros, scales, g_idx)
+    return w4a16_forward(x, w, x_dtype, bias)
+
+
+def error_metrics(actual, expected) -> dict[str, float]:
+    """max-abs, rel-RMSE and the normwise max ratio used by every tolerance."""
+
+    a = np.asarray(actual, np.float64)
+    e = np.asarray(expected, np.float64)
+    diff = a - e
+    denom_max = max(float(np.abs(e).max()), 1e-30)
+    denom_rms = max(float(np.sqrt(np.mean(e * e))), 1e-30)
+    return {
+        "max_abs": float(np.abs(diff).max()) if diff.size else 0.0,
+        "rel_rmse": float(np.sqrt(np.mean(diff * diff)) / denom_rms) if diff.size else 0.0,
+        "normwise_max": float(np.abs(diff).max() / denom_max) if diff.size else 0.0,
+    }
+
+
+def gptq_forward_fast(x, qweight, qzeros, scales, g_idx, x_dtype, bias=None) -> np.ndarray:
+    """The reference CPU path's operation order (linear.py:401-404: dequantize to
+    fp32, cast to the activation dtype, matmul) with the matmul in fp32 BLAS.
+    Used only as the timed CPU baseline; parity checks use ``gptq_forward``."""
+
+    w = formats.w4a16_weight_fp16(formats.gptq_dequantize(qweight, qzeros, scales, g_idx))
+    a = w4a16_activation(x, x_dtype)
+    out = a @ w.T
+    return to_dtype(_bias_add(out.astype(np.float32), bias), x_dtype)

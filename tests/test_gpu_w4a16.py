@@ -1,0 +1,227 @@
+"""AWQ / GPTQ W4A16 on gfx950 against the CPU oracle.
+
+Outputs match ``fp64(fp16(x) . fp16((q - z) * s))`` within 1e-2 normwise and
+rel-RMSE; the reference's exactness contracts (fp16 checkpoint-scale
+precision, bf16 saturation to +-65504, non-finite propagation) hold bit for
+bit.  GPTQ covers all three group modes: g_idx == k // g, act-order (load-time
+K permutation) and an arbitrary g_idx (per-element groups).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from gpu_helpers import DTYPE_NAME, assert_close_fp, banner, bits, np32
+from kairyu_amd.kernels import quant_gemm_hip as hip
+from kairyu_amd.quant import awq as awq_format
+from kairyu_amd.quant import gptq as gptq_format
+from kairyu_amd.quant.linear import AwqLinear, GptqLinear
+from oracle import linear as olinear
+
+pytestmark = pytest.mark.gpu
+
+
+def _awq_module(k, n, group=16, seed=0, bias=True, random_packed=False):
+    g = torch.Generator().manual_seed(seed)
+    module = AwqLinear(k, n, bias=bias, group_size=group)
+    if random_packed:
+        groups = module.qzeros.shape[0]
+        module.qweight.copy_(awq_format.pack_awq(torch.randint(0, 16, (k, n), generator=g)))
+        module.qzeros.copy_(awq_format.pack_awq(torch.randint(0, 16, (groups, n), generator=g)))
+        module.scales.copy_((torch.rand(groups, n, generator=g) * 0.018 + 0.002).half())
+    else:
+        qw, qz, sc = awq_format.quantize_awq(torch.randn(n, k, generator=g), group_size=group)
+        module.qweight.copy_(qw)
+        module.qzeros.copy_(qz)
+        module.scales.copy_(sc)
+    if bias:
+        module.bias.data.normal_(generator=g)
+    return module
+
+
+def _gptq_module(k, n, group=16, seed=0, bias=True, g_idx=None, random_packed=False):
+    g = torch.Generator().manual_seed(seed)
+    module = GptqLinear(k, n, bias=bias, group_size=group)
+    groups = module.qzeros.shape[0]
+    if random_packed:
+        module.qweight.copy_(gptq_format.pack_gptq_rows(torch.randint(0, 16, (k, n), generator=g)))
+        module.qzeros.copy_(gptq_format.pack_gptq_cols(torch.randint(0, 16, (groups, n), generator=g)))
+        module.scales.copy_((torch.rand(groups, n, generator=g) * 0.009 + 0.001).half())
+        module.g_idx.copy_((torch.arange(k) // group).to(torch.int32))
+    else:
+        qw, qz, sc, gi = gptq_format.quantize_gptq(torch.randn(n, k, generator=g), group_size=group)
+        module.qweight.copy_(qw)
+        module.qzeros.copy_(qz)
+        module.scales.copy_(sc)
+        module.g_idx.copy_(gi)
+    if g_idx is not None:
+        module.g_idx.copy_(g_idx)
+    if bias:
+        module.bias.data.normal_(generator=g)
+    return module
+
+
+def _oracle(module, x: torch.Tensor, add_bias=True) -> np.ndarray:
+    xd = DTYPE_NAME[x.dtype]
+    bias = np32(module.bias) if (add_bias and module.bias is not None) else None
+    if isinstance(module, AwqLinear):
+        return olinear.awq_forward(np32(x), module.qweight.cpu().numpy(), module.qzeros.cpu().numpy(),
+                                   np32(module.scales), module.group_size, xd, bias)
+    return olinear.gptq_forward(np32(x), module.qweight.cpu().numpy(), module.qzeros.cpu().numpy(),
+                                np32(module.scales), module.g_idx.cpu().numpy(), xd, bias)
+
+
+@pytest.mark.parametrize("factory", [_awq_module, _gptq_module], ids=["awq", "gptq"])
+@pytest.mark.parametrize("shape", [(1, 64, 32), (17, 96, 40), (32, 64, 32)])
+def test_ragged_shapes_match_cpu_path_without_dequantizing(cuda, fixtures, monkeypatch, factory, shape):
+    m, k, n = shape
+    banner(f"ragged {factory.__name__} {shape}")
+    module = factory(k, n)
+    x = torch.randn(m, k, generator=torch.Generator().manual_seed(0))
+    cpu_out = module.forward_reference(x.to(torch.bfloat16).float())
+    expected = _oracle(module, x.to(torch.bfloat16))
+
+    def forbidden(*_a, **_k):
+        raise AssertionError("W4A16 device forward materialized its weight")
+
+    monkeypatch.setattr(type(module), "dequantize", forbidden)
+    gpu_out = module.to(cuda)(x.to(cuda, torch.bfloat16))
+    tol = fixtures["tolerances"]["awq"]
+    torch.testing.assert_close(gpu_out.float().cpu(), cpu_out, rtol=tol["rtol"], atol=tol["atol"])
+    assert_close_fp(np32(gpu_out), expected)
+
+
+@pytest.mark.parametrize("factory", [_awq_module, _gptq_module], ids=["awq", "gptq"])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_fp16_checkpoint_scale_precision_is_bit_exact(cuda, fixtures, factory, dtype):
+    fx = fixtures["w4a16_scale_precision"]
+    module = factory(fx["k"], fx["n"], seed=366)
+    module.bias.data.zero_()
+    module.scales.fill_(fx["scale"])
+    x = torch.ones(fx["rows"], fx["k"], dtype=dtype)
+    expected = _oracle(module, x)
+    weight = module.dequantize()
+    actual = module.to(cuda)(x.to(cuda))
+    assert np.array_equal(np32(actual), expected)
+    if dtype is torch.bfloat16:  # the bf16-rounded-weight path would differ
+        bf16_path = (x.float() @ weight.to(torch.bfloat16).float().T).to(torch.bfloat16)
+        assert not np.array_equal(np32(bf16_path), expected)
+
+
+@pytest.mark.parametrize("factory", [_awq_module, _gptq_module], ids=["awq", "gptq"])
+def test_bf16_activations_saturate_to_fp16_range(cuda, fixtures, factory):
+    fx = fixtures["w4a16_saturation"]
+    module = factory(fx["k"], fx["n"], seed=367)
+    module.bias.data.zero_()
+    module.scales.fill_(fx["scale"])
+    x = torch.full((fx["rows"], fx["k"]), fx["value"], dtype=torch.bfloat16)
+    x[1].neg_()
+    expected = _oracle(module, x)
+    actual = module.to(cuda)(x.to(cuda))
+    assert torch.isfinite(actual).all()
+    assert np.array_equal(np32(actual), expected)
+
+
+@pytest.mark.parametrize("factory", [_awq_module, _gptq_module], ids=["awq", "gptq"])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_infinite_activations_stay_non_finite(cuda, factory, dtype):
+    module = factory(64, 32).to(cuda)
+    out = module(torch.full((1, 64), float("inf"), device=cuda, dtype=dtype))
+    assert not torch.isfinite(out).all()
+
+
+@pytest.mark.parametrize("m", [1, 4, 16, 17, 40, 64, 65, 130])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_awq_all_paths(cuda, m, dtype):
+    banner(f"awq paths m={m} {dtype}")
+    module = _awq_module(2048, 320, group=128, seed=m, random_packed=True).to(cuda)
+    x = torch.randn(m, 2048, generator=torch.Generator().manual_seed(m)).to(dtype)
+    out = module(x.to(cuda))
+    assert_close_fp(np32(out), _oracle(module, x), label=f"m={m}")
+
+
+@pytest.mark.parametrize("mode", ["uniform", "act_order", "arbitrary"])
+@pytest.mark.parametrize("m", [1, 16, 33, 100])
+def test_gptq_group_modes(cuda, mode, m):
+    banner(f"gptq {mode} m={m}")
+    k, n, group = 1024, 192, 64
+    g = torch.Generator().manual_seed(7 + m)
+    if mode == "uniform":
+        g_idx = (torch.arange(k) // group).to(torch.int32)
+    elif mode == "act_order":
+        g_idx = (torch.randperm(k, generator=g) // group).to(torch.int32)
+    else:
+        g_idx = torch.randint(0, k // group, (k,), generator=g).to(torch.int32)
+    module = _gptq_module(k, n, group=group, seed=m, g_idx=g_idx, random_packed=True)
+    module.g_idx.copy_(g_idx)
+    module = module.to(cuda)
+    x = torch.randn(m, k, generator=g).to(torch.float16)
+    out = module(x.to(cuda))
+    expected_mode = {"uniform": hip.GIDX_UNIFORM, "act_order": hip.GIDX_PERMUTED,
+                     "arbitrary": hip.GIDX_PER_K}[mode]
+    assert module._kq_gptq_operands[1][0] == expected_mode
+    assert_close_fp(np32(out), _oracle(module, x), label=f"{mode} m={m}")
+
+
+def test_gptq_derived_operands_follow_g_idx_updates(cuda):
+    module = _gptq_module(256, 64, group=32, seed=1, random_packed=True).to(cuda)
+    x = torch.randn(3, 256, device=cuda, dtype=torch.float16)
+    module(x)
+    assert module._kq_gptq_operands[1][0] == hip.GIDX_UNIFORM
+    module.g_idx.copy_((torch.randperm(256) // 32).to(torch.int32))
+    out = module(x)
+    assert module._kq_gptq_operands[1][0] == hip.GIDX_PERMUTED
+    assert_close_fp(np32(out), _oracle(module, x.cpu()))
+
+
+def test_awq_group_not_multiple_of_8_uses_per_row_groups(cuda):
+    module = _awq_module(60, 16, group=12, seed=4, random_packed=True).to(cuda)
+    x = torch.randn(5, 60, generator=torch.Generator().manual_seed(4)).to(torch.float16)
+    assert_close_fp(np32(module(x.to(cuda))), _oracle(module, x))
+
+
+def test_row_parallel_bias_omission(cuda):
+    module = _awq_module(128, 64, seed=9).to(cuda)
+    module._kairyu_row_parallel_omit_bias = True
+    x = torch.randn(4, 128, generator=torch.Generator().manual_seed(9)).to(torch.float16)
+    assert_close_fp(np32(module(x.to(cuda))), _oracle(module, x, add_bias=False))
+
+
+def test_rejects_non_fp16_scales_and_bad_layout(cuda):
+    module = _awq_module(64, 32).to(cuda)
+    module.scales = module.scales.float()
+    with pytest.raises(RuntimeError, match="fp16 checkpoint scales"):
+        module(torch.randn(2, 64, device=cuda, dtype=torch.float16))
+    module = _gptq_module(64, 32).to(cuda)
+    module.g_idx = module.g_idx[:32]
+    with pytest.raises(ValueError, match="GPTQ packed layout"):
+        module(torch.randn(2, 64, device=cuda, dtype=torch.float16))
+
+
+def test_graph_replays_match_eager(cuda):
+    banner("w4a16 graph replay")
+    awq = _awq_module(4096, 512, group=128, seed=2, random_packed=True).to(cuda)
+    gptq = _gptq_module(4096, 512, group=128, seed=3, random_packed=True,
+                        g_idx=(torch.randperm(4096) // 128).to(torch.int32)).to(cuda)
+    x = torch.randn(16, 4096, device=cuda, dtype=torch.float16)
+    eager = (awq(x).clone(), gptq(x).clone())
+    torch.cuda.synchronize()
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        for _ in range(2):
+            awq(x), gptq(x)
+    torch.cuda.current_stream().wait_stream(stream)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        oa = awq(x)
+        og = gptq(x)
+    for step in range(4):
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(oa, eager[0]), step
+        assert torch.equal(og, eager[1]), step
+        gptq(x * 2)
+        torch.cuda.synchronize()

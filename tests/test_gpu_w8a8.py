@@ -1,0 +1,239 @@
+"""INT8 / FP8 W8A8 on gfx950 against the CPU oracle.
+
+INT8 is bit-exact end to end (activation bytes and scales, int32 accumulators,
+bf16 output).  FP8 activation bytes and scales are bit-exact; outputs match
+the exact-accumulation oracle within 1e-2 normwise and rel-RMSE.  Cases follow
+the reference's tests/gpu/test_quant_kernels.py plus every kernel path of this
+package (skinny MT=1/2/4, split-K, tiled, generic K).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from gpu_helpers import DTYPE_NAME, assert_close_fp, banner, bits, np32
+from kairyu_amd.kernels import quant_gemm_hip as hip
+from kairyu_amd.quant.fp8 import quantize_fp8
+from kairyu_amd.quant.int8 import quantize_int8_weight
+from kairyu_amd.quant.linear import Fp8Linear, Int8Linear
+from oracle import formats, linear as olinear, numerics
+
+pytestmark = pytest.mark.gpu
+
+
+def _int8_module(k, n, seed=0, bias=True):
+    g = torch.Generator().manual_seed(seed)
+    module = Int8Linear(k, n, bias=bias)
+    qw, ws = quantize_int8_weight(torch.randn(n, k, generator=g))
+    module.weight.copy_(qw)
+    module.weight_scale.copy_(ws)
+    if bias:
+        module.bias.data.normal_(generator=g)
+    return module
+
+
+def _fp8_module(k, n, seed=0, bias=True, per_channel=True, dynamic=True):
+    g = torch.Generator().manual_seed(seed)
+    module = Fp8Linear(k, n, bias=bias, activation_dynamic=dynamic)
+    qw, ws = quantize_fp8(torch.randn(n, k, generator=g) * 0.02, per_channel=per_channel)
+    module.weight.copy_(qw)
+    if per_channel:
+        module.weight_scale.copy_(ws)
+    else:
+        module.weight_scale = ws
+    if bias:
+        module.bias.data.normal_(generator=g)
+    return module
+
+
+# ---------------------------------------------------------------- INT8
+@pytest.mark.parametrize("k", [1536, 8960])
+def test_int8_activation_quantization_bit_exact(cuda, fixtures, k):
+    fx = fixtures["int8_act_quant_cases"]
+    banner(f"int8 act quant k={k}")
+    torch.manual_seed(fx["seed"])
+    x = torch.randn(fx["rows"], k, dtype=torch.bfloat16)
+    x[fx["zero_row"]].zero_()
+    q, s = hip._quantize_activation(x.to(cuda), torch.int8, 127.0)
+    eq, es = formats.int8_quantize_rows(np32(x))
+    assert np.array_equal(bits(q), eq)
+    assert np.array_equal(np32(s), es)
+
+
+@pytest.mark.parametrize("case", range(3))
+def test_int8_fused_output_bit_exact_with_bias(cuda, fixtures, case):
+    c = fixtures["int8_bitexact_cases"][case]
+    banner(f"int8 bit-exact {c}")
+    torch.manual_seed(c["seed"])
+    module = _int8_module(c["k"], c["n"], seed=c["seed"])
+    module.bias.data = module.bias.data.to(torch.bfloat16)
+    x = torch.randn(c["m"], c["k"], dtype=torch.bfloat16)
+    expected, _, _, _ = olinear.int8_forward(np32(x), module.weight.numpy(),
+                                             module.weight_scale.numpy(), np32(module.bias))
+    actual = module.to(cuda)(x.to(cuda))
+    assert actual.dtype == torch.bfloat16
+    assert np.array_equal(bits(actual), numerics.bf16_bits(expected).view(np.int16))
+
+
+@pytest.mark.parametrize("m", [1, 5, 16, 17, 33, 64, 65, 200])
+@pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float16])
+def test_int8_accumulators_and_output_bit_exact_all_paths(cuda, m, out_dtype):
+    n, k = 160, 3584  # split-K on the skinny path; 2x2 tiles on the tiled path
+    banner(f"int8 paths m={m} dtype={out_dtype}")
+    module = _int8_module(k, n, seed=m).to(cuda)
+    x = torch.randn(m, k, generator=torch.Generator().manual_seed(100 + m)).to(out_dtype)
+    acc = torch.empty(m, n, dtype=torch.int32, device=cuda)
+    out = hip.int8_linear_forward(x.to(cuda), module, accumulators=acc)
+    expected, xq, xs, eacc = olinear.int8_forward(
+        np32(x), module.weight.cpu().numpy(), module.weight_scale.cpu().numpy(),
+        np32(module.bias), out_dtype=DTYPE_NAME[out_dtype])
+    assert np.array_equal(acc.cpu().numpy().astype(np.int64), eacc)
+    assert np.array_equal(np32(out), expected)
+
+
+def test_int8_generic_k_path(cuda):
+    banner("int8 generic k")
+    module = _int8_module(72, 24, seed=3).to(cuda)
+    x = torch.randn(3, 72, generator=torch.Generator().manual_seed(4)).to(torch.bfloat16)
+    out = module(x.to(cuda))
+    expected, *_ = olinear.int8_forward(np32(x), module.weight.cpu().numpy(),
+                                        module.weight_scale.cpu().numpy(), np32(module.bias))
+    assert np.array_equal(np32(out), expected)
+
+
+# ----------------------------------------------------------------- FP8
+@pytest.mark.parametrize("mode", ["dynamic", "static", "row"])
+def test_fp8_activation_quantization_bit_exact(cuda, mode):
+    banner(f"fp8 act quant {mode}")
+    g = torch.Generator().manual_seed(21)
+    x = (torch.randn(6, 2304, generator=g) * 3).to(torch.bfloat16)
+    x[2].zero_()
+    static = torch.tensor(0.013) if mode == "static" else None
+    row = (torch.rand(6, 1, generator=g) * 0.05 + 1e-3) if mode == "row" else None
+    q, s = hip._quantize_activation(x.to(cuda), torch.float8_e4m3fn, 448.0,
+                                    static_scale=None if static is None else static.to(cuda),
+                                    row_scale=None if row is None else row.to(cuda))
+    if mode == "row":
+        eq = numerics.e4m3_encode(np.clip(np32(x) / row.numpy(), -448, 448))
+        es = row.numpy()
+    else:
+        eq, es = formats.fp8_quantize_rows(np32(x), None if static is None else float(static))
+    assert np.array_equal(bits(q), eq)
+    assert np.array_equal(np32(s), es)
+
+
+@pytest.mark.parametrize("m", [1, 7, 16, 24, 48, 64, 96, 300])
+def test_fp8_output_matches_oracle_all_paths(cuda, m):
+    n, k = 192, 14336 // 4
+    banner(f"fp8 paths m={m}")
+    module = _fp8_module(k, n, seed=m).to(cuda)
+    x = torch.randn(m, k, generator=torch.Generator().manual_seed(m)).to(torch.bfloat16)
+    out = module(x.to(cuda))
+    expected, _, _, pre = olinear.fp8_forward(np32(x), bits(module.weight), np32(module.weight_scale),
+                                              np32(module.bias))
+    assert_close_fp(np32(out), pre, label=f"m={m}")
+
+
+def test_fp8_per_tensor_weight_scale_and_static_input(cuda):
+    banner("fp8 static")
+    module = _fp8_module(64, 32, seed=2, bias=False, per_channel=False, dynamic=False)
+    module.input_scale.copy_(torch.tensor(0.01))
+    x = torch.randn(7, 64, generator=torch.Generator().manual_seed(2)).to(torch.bfloat16)
+    out = module.to(cuda)(x.to(cuda))
+    _, _, _, pre = olinear.fp8_forward(np32(x), bits(module.weight), np32(module.weight_scale),
+                                       static_scale=0.01)
+    assert_close_fp(np32(out), pre)
+
+
+def test_fp8_global_per_token_scale_and_exact_amax(cuda):
+    banner("fp8 global scale")
+    module = _fp8_module(64, 32, seed=19)
+    x = torch.randn(7, 64, generator=torch.Generator().manual_seed(19)).to(torch.bfloat16)
+    amax = np32(x).__abs__().max(axis=-1, keepdims=True)
+    scale = np.maximum(amax * np.float32(1.25) / np.float32(448.0), np.float32(1e-12)).astype(np.float32)
+    module = module.to(cuda)
+    xc = x.to(cuda)
+    assert np.array_equal(np32(module.activation_amax(xc)), amax)
+    out = module.forward_with_activation_scale(xc, torch.from_numpy(scale).to(cuda))
+    _, _, _, pre = olinear.fp8_forward(np32(x), bits(module.weight), np32(module.weight_scale),
+                                       np32(module.bias), row_scale=scale)
+    assert_close_fp(np32(out), pre)
+
+
+# ------------------------------------------------ reference ragged cases
+@pytest.mark.parametrize("scheme", ["int8", "fp8"])
+@pytest.mark.parametrize("shape", [(1, 64, 32), (17, 96, 40), (32, 64, 32)])
+def test_ragged_shapes_match_cpu_path_without_dequantizing(cuda, fixtures, monkeypatch, scheme, shape):
+    m, k, n = shape
+    banner(f"ragged {scheme} {shape}")
+    module = (_int8_module if scheme == "int8" else _fp8_module)(k, n, seed=0)
+    x = torch.randn(m, k, generator=torch.Generator().manual_seed(0))
+    cpu_out = module.forward_reference(x.to(torch.bfloat16).float())
+
+    def forbidden(*_a, **_k):
+        raise AssertionError(f"{scheme} device forward materialized its weight")
+
+    monkeypatch.setattr(type(module), "dequantize", forbidden)
+    gpu_out = module.to(cuda)(x.to(cuda, torch.bfloat16)).float().cpu()
+    tol = fixtures["tolerances"][scheme]
+    if scheme == "fp8":
+        err = gpu_out - cpu_out
+        rel = err.square().mean().sqrt() / cpu_out.square().mean().sqrt()
+        assert rel.item() < tol["rel_rmse"]
+        assert err.abs().max().item() < tol["max_abs_per_sqrt_k"] * k**0.5
+    else:
+        torch.testing.assert_close(gpu_out, cpu_out, rtol=tol["rtol"], atol=tol["atol"])
+
+
+# ------------------------------------------------------------ fail closed
+def test_rejects_unsupported_activation_dtype(cuda):
+    module = _int8_module(64, 32).to(cuda)
+    with pytest.raises(RuntimeError, match="float16/bfloat16"):
+        module(torch.randn(2, 64, device=cuda))
+
+
+@pytest.mark.parametrize("factory", [_int8_module, _fp8_module], ids=["int8", "fp8"])
+def test_rejects_other_architectures(cuda, monkeypatch, factory):
+    module = factory(64, 32).to(cuda)
+    monkeypatch.setattr(hip, "_device_arch", lambda _d: "gfx942")
+    with pytest.raises(RuntimeError, match="requires gfx950"):
+        module(torch.randn(2, 64, device=cuda, dtype=torch.bfloat16))
+
+
+def test_rejects_k_mismatch_and_misplaced_payload(cuda):
+    module = _int8_module(64, 32).to(cuda)
+    with pytest.raises(ValueError, match="expected K=64"):
+        module(torch.randn(2, 48, device=cuda, dtype=torch.bfloat16))
+    cpu_module = _int8_module(64, 32)
+    with pytest.raises(RuntimeError, match="payloads"):
+        hip.int8_linear_forward(torch.randn(2, 64, device=cuda, dtype=torch.bfloat16), cpu_module)
+
+
+# ------------------------------------------------------------- graphs
+def test_graph_replays_match_eager(cuda):
+    banner("w8a8 graph replay")
+    int8_mod = _int8_module(3584, 160, seed=5).to(cuda)
+    fp8_mod = _fp8_module(3584, 160, seed=6).to(cuda)
+    x = torch.randn(16, 3584, device=cuda, dtype=torch.bfloat16)
+    eager = (int8_mod(x).clone(), fp8_mod(x).clone())
+    torch.cuda.synchronize()
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        for _ in range(2):
+            int8_mod(x), fp8_mod(x)
+    torch.cuda.current_stream().wait_stream(stream)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out_i8 = int8_mod(x)
+        out_f8 = fp8_mod(x)
+    for step in range(4):
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out_i8, eager[0]), step
+        assert torch.equal(out_f8, eager[1]), step
+        # eager work between replays must not disturb the shared workspace
+        int8_mod(x * 0.5)
+        torch.cuda.synchronize()
