@@ -35,15 +35,20 @@
 namespace kq {
 
 enum { kAwq = 0, kGptq = 1 };
+// Host-side group modes (ABI gidx_mode) ...
 enum { kGroupsUniform = 0, kGroupsPermuted = 1, kGroupsPerK = 2 };
+// ... and the kernel's group addressing: one group per step for the whole
+// wave (group_size % 32 == 0, computed on the scalar unit), one group per
+// lane's 8-k chunk (group_size % 8 == 0), or a group per element (g_idx).
+enum { kGStep = 0, kGLane = 1, kGElem = 2 };
+enum { kXF16 = 0, kXBF16 = 1 };
 
 constexpr int kW4Cols = 64;   // columns per workgroup tile
 
 struct W4Args {
-  const uint16_t* x;
-  int x_dtype;
+  const uint16_t* x;     // activation rows (fp16 or bf16 per kernel template)
   int ldx;
-  bool x_vec;
+  int x_dtype;           // caller's activation dtype
   const uint32_t* qw;
   const uint32_t* qz;
   const uint16_t* sc;
@@ -54,10 +59,15 @@ struct W4Args {
   uint16_t* out;
   int out_dtype;
   int M, N, K, G;
+  uint64_t gmagic;       // floor(k / G) == (k * gmagic) >> 40 for k < 2^24
   int steps_per_split;
   int splits;
-  float* partials;  // [splits][M][N] when splits > 1
+  float* partials;       // [splits][M][N] when splits > 1
 };
+
+KQ_DEV int group_of(const W4Args& a, int k) {
+  return (int)(((uint64_t)(uint32_t)k * a.gmagic) >> 40);
+}
 
 KQ_DEV uint32_t pk_sub_mul(uint32_t q, uint32_t z, uint32_t s) {
   f16x2 r = (__builtin_bit_cast(f16x2, q) - __builtin_bit_cast(f16x2, z)) *
@@ -76,30 +86,25 @@ KQ_DEV uint16_t act_bits(uint16_t b, int dtype) {
   return __builtin_bit_cast(uint16_t, act_to_f16(b, dtype));
 }
 
-KQ_DEV uint32_t act_pair(uint32_t raw, int dtype) {
-  if (dtype == KQ_DTYPE_F16) return raw;
-  return (uint32_t)act_bits((uint16_t)(raw & 0xffffu), dtype) |
-         ((uint32_t)act_bits((uint16_t)(raw >> 16), dtype) << 16);
+// bf16 -> fp16 with finite saturation to +-65504, inf/nan kept (see act_to_f16)
+KQ_DEV _Float16 bf16f_to_f16_sat(float f) {
+  const float c = __builtin_amdgcn_fmed3f(f, -65504.0f, 65504.0f);
+  // class mask: signaling/quiet nan (0x3) | -inf (0x4) | +inf (0x200)
+  const bool keep = __builtin_amdgcn_class(f, 0x207);
+  return (_Float16)(keep ? f : c);
 }
 
-// Eight fp16 activation values x[m][k..k+7] (natural k order), zero beyond
-// the matrix.
-KQ_DEV u32x4 load_x8(const W4Args& a, int m, int k) {
-  u32x4 v = {0u, 0u, 0u, 0u};
-  if (m >= a.M) return v;
-  const uint16_t* row = a.x + (int64_t)m * a.ldx;
-  if (a.x_vec && k + 8 <= a.K) {
-    u32x4 raw = *(const u32x4*)(row + k);
-#pragma unroll
-    for (int d = 0; d < 4; ++d) v[d] = act_pair(raw[d], a.x_dtype);
-    return v;
-  }
-  uint16_t h[8];
-#pragma unroll
-  for (int e = 0; e < 8; ++e) h[e] = (k + e < a.K) ? act_bits(row[k + e], a.x_dtype) : 0;
-#pragma unroll
-  for (int d = 0; d < 4; ++d) v[d] = (uint32_t)h[2 * d] | ((uint32_t)h[2 * d + 1] << 16);
-  return v;
+KQ_DEV uint32_t bf16x2_to_f16x2(uint32_t raw) {
+  const _Float16 lo = bf16f_to_f16_sat(__uint_as_float(raw << 16));
+  const _Float16 hi = bf16f_to_f16_sat(__uint_as_float(raw & 0xffff0000u));
+  return (uint32_t)__builtin_bit_cast(uint16_t, lo) | ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
+}
+
+template <int XDT>
+KQ_DEV u32x4 x_to_f16(u32x4 raw) {
+  if constexpr (XDT == kXF16) return raw;
+  return u32x4{bf16x2_to_f16x2(raw[0]), bf16x2_to_f16x2(raw[1]), bf16x2_to_f16x2(raw[2]),
+               bf16x2_to_f16x2(raw[3])};
 }
 
 // GPTQ A operand order [0,4,1,5,2,6,3,7] from natural pairs.
@@ -117,11 +122,53 @@ KQ_DEV uint16_t dq1(uint32_t q, uint32_t z, uint16_t s) {
   return __builtin_bit_cast(uint16_t, r);
 }
 
-template <int FMT, int MT, int GMODE, int WAVES>
+// Register batch of U consecutive 32-k steps for one lane: packed weights,
+// the group's scale/zero words and the raw activation chunks.
+template <int FMT, int MT, int U>
+struct W4Batch {
+  u32x4 wq[FMT == kGptq ? U : 1];      // GPTQ: 4 columns' words of packed row
+  uint32_t wd[FMT == kAwq ? U : 1][8]; // AWQ: octet word of rows k..k+7
+  u32x2 sv[U];                         // fp16 scales of the lane's 4 columns
+  uint32_t zw[U];                      // zero word holding those columns
+  u32x4 xv[U][MT];                     // raw x[m][k..k+7]
+};
+
+// Load through a base pointer plus a 32-bit byte offset; with a wave-uniform
+// base this is the global_load "saddr" form (no per-lane 64-bit addressing).
+template <typename T>
+KQ_DEV T ldb(const void* base, uint32_t byte_off) {
+  return *(const T*)((const char*)base + byte_off);
+}
+
+// (x & mask) | magic in one VOP3 (gfx9 allows a single SGPR/literal operand,
+// so the magic constant lives in a VGPR).
+KQ_DEV uint32_t and_or(uint32_t x, uint32_t mask, uint32_t magic) {
+  uint32_t r;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(x), "s"(mask), "v"(magic));
+  return r;
+}
+
+// Nibble pairs of a 32-bit word as fp16 (base + q) pairs: OR-ing the nibble at
+// bits 0-3 of each half into 0x6400 gives 1024+q; the nibble at bits 4-7 into
+// 0x5400 gives 64+q (the nibble lands on the mantissa's unit place in both
+// binades).  Bits 8-15 would reach the exponent field, so the upper byte of
+// each half is shifted down first.
+struct NibbleConsts {
+  uint32_t m0, m1;  // SGPR masks 0x000f000f, 0x00f000f0
+  uint32_t c0, c1;  // VGPR magics: fp16 pairs (1024, 1024), (64, 64)
+};
+
+// PRED = false: every step of the kernel is a full 32-k step and x rows are
+// 16-byte aligned; loads carry no predicates (columns and rows are clamped to
+// valid addresses and the surplus results are never stored).  PRED = true
+// guards every load (K tails, unaligned x).
+template <int FMT, int MT, int GM, int XDT, bool PRED, int WAVES>
 __global__ void __launch_bounds__(64 * WAVES)
 w4a16_skinny_kernel(W4Args a) {
+  constexpr int U = 4;
   __shared__ float red[(WAVES - 1) * MT * 16 * 64];
-  const int lane = lane_id(), wave = wave_id();
+  const int lane = lane_id();
+  const int wave = __builtin_amdgcn_readfirstlane(wave_id());
   const int j = lane & 15, kb = lane >> 4;
   const int tile = blockIdx.x / a.splits, split = blockIdx.x % a.splits;
   const int colbase = tile * kW4Cols;
@@ -129,16 +176,34 @@ w4a16_skinny_kernel(W4Args a) {
   const int nsteps = (a.K + 31) / 32;
   const int sbeg = split * a.steps_per_split;
   const int send = min(nsteps, sbeg + a.steps_per_split);
-  const int per_wave = (send - sbeg + WAVES - 1) / WAVES;
+  // waves take contiguous, batch-aligned step ranges
+  const int per_wave = ((send - sbeg + WAVES - 1) / WAVES + U - 1) / U * U;
   const int wbeg = sbeg + wave * per_wave;
   const int wend = min(send, wbeg + per_wave);
 
-  // columns handled by this lane
-  const int o = j & 7, h = j >> 3;                    // AWQ octet / half
-  const int gcol = colbase + 4 * j;                   // GPTQ first column
-  const int acol = colbase + 8 * o + 4 * h;           // AWQ first column
-  const bool col_ok = (FMT == kGptq ? gcol : acol) < a.N;
+  // the lane's 4 columns, clamped to valid memory
+  const int o = j & 7, h = j >> 3;                        // AWQ octet / half
+  const int lcol = FMT == kGptq ? colbase + 4 * j : colbase + 8 * o + 4 * h;
+  const bool col_ok = lcol < a.N;
+  const int lcol_c = col_ok ? lcol : a.N - 4;
   const int n8 = a.N / 8;
+  const int zword = lcol_c >> 3;
+  const int zsh = FMT == kGptq ? 4 * (lcol_c & 7) : 8 * h;
+  NibbleConsts nc;
+  nc.m0 = __builtin_amdgcn_readfirstlane(0x000f000fu);
+  nc.m1 = __builtin_amdgcn_readfirstlane(0x00f000f0u);
+  nc.c0 = 0x64006400u + (uint32_t)(lane & 0);  // keep the magics in VGPRs
+  nc.c1 = 0x54005400u + (uint32_t)(lane & 0);
+
+  // loop-invariant 32-bit byte offsets of this lane
+  const uint32_t w_boff = FMT == kGptq ? (uint32_t)(kb * a.N + lcol_c) * 4u
+                                       : (uint32_t)(8 * kb * n8 + zword) * 4u;
+  const uint32_t s_boff = (uint32_t)lcol_c * 2u;
+  const uint32_t z_boff = (uint32_t)zword * 4u;
+  uint32_t x_boff[MT];
+#pragma unroll
+  for (int t = 0; t < MT; ++t)
+    x_boff[t] = (uint32_t)(min(mbase + t * 16 + j, a.M - 1) * a.ldx + 8 * kb) * 2u;
 
   f32x4 acc[MT][4];
 #pragma unroll
@@ -146,111 +211,173 @@ w4a16_skinny_kernel(W4Args a) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) acc[t][i] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  constexpr int U = FMT == kGptq ? 4 : 2;
-  for (int st0 = wbeg; st0 < wend; st0 += U) {
-    // ---- issue all weight loads of U steps first
-    u32x4 wq[U];
-    uint32_t wd[U][8];
+  auto step_group = [&](int st, int k) -> int {
+    if constexpr (GM == kGStep) return __builtin_amdgcn_readfirstlane(group_of(a, st * 32));
+    else return group_of(a, PRED ? min(k, a.K - 1) : k);
+  };
+
+  auto load_step = [&](W4Batch<FMT, MT, U>& b, int u, int st) {
+    const int k = st * 32 + 8 * kb;
+    const bool ok = !PRED || (k < a.K && col_ok);
+    if constexpr (FMT == kGptq) {
+      const uint32_t* base = a.qw + (int64_t)st * 4 * a.N;
+      b.wq[u] = ok ? ldb<u32x4>(base, w_boff) : u32x4{0u, 0u, 0u, 0u};
+    } else {
+      const uint32_t* base = a.qw + (int64_t)st * 32 * n8;
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int k = (st0 + u) * 32 + 8 * kb;
-      const bool step_ok = (st0 + u) < wend;
-      if constexpr (FMT == kGptq) {
-        wq[u] = (step_ok && col_ok && k < a.K)
-                    ? *(const u32x4*)(a.qw + (int64_t)(k >> 3) * a.N + gcol)
-                    : u32x4{0u, 0u, 0u, 0u};
+      for (int t = 0; t < 8; ++t)
+        b.wd[u][t] = (!PRED || (ok && k + t < a.K)) ? ldb<uint32_t>(base, w_boff + (uint32_t)(t * n8 * 4)) : 0u;
+    }
+    if constexpr (GM != kGElem) {
+      const int g = step_group(st, k);
+      b.sv[u] = ldb<u32x2>(a.sc + (int64_t)g * a.N, s_boff);
+      b.zw[u] = ldb<uint32_t>(a.qz + (int64_t)g * n8, z_boff);
+    }
+    const uint16_t* xb = a.x + (int64_t)st * 32;
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+      if constexpr (!PRED) {
+        b.xv[u][t] = ldb<u32x4>(xb, x_boff[t]);
       } else {
+        uint32_t hv[8];
 #pragma unroll
-        for (int t = 0; t < 8; ++t)
-          wd[u][t] = (step_ok && col_ok && k + t < a.K)
-                         ? a.qw[(int64_t)(k + t) * n8 + (colbase >> 3) + o]
-                         : 0u;
+        for (int e = 0; e < 8; ++e)
+          hv[e] = (k + e < a.K) ? (uint32_t)ldb<uint16_t>(xb, x_boff[t] + 2u * e) : 0u;
+#pragma unroll
+        for (int d = 0; d < 4; ++d) b.xv[u][t][d] = hv[2 * d] | (hv[2 * d + 1] << 16);
+      }
+    }
+  };
+
+  // derived per-group operands: zero pairs for the two magics and the
+  // broadcast scale pair of each of the lane's 4 columns (GPTQ), or the zero
+  // / scale pairs of its 4 columns (AWQ)
+  uint32_t zq[4][2], sq[4];
+  int gcur = -1;
+  auto derive = [&](const W4Batch<FMT, MT, U>& b, int u) {
+    if constexpr (FMT == kGptq) {
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const uint32_t z = ((b.zw[u] >> (zsh + 4 * t)) & 0xfu) + 1u;
+        zq[t][0] = nc.c0 + z * 0x00010001u;   // (1024 + z) pair
+        zq[t][1] = nc.c1 + z * 0x00100010u;   // (64 + z) pair: z on the nibble's bit place
+        const uint32_t s16 = (t & 1) ? (b.sv[u][t >> 1] >> 16) : (b.sv[u][t >> 1] & 0xffffu);
+        sq[t] = s16 * 0x00010001u;
+      }
+    } else {
+      const uint32_t x = b.zw[u] >> zsh;
+      zq[0][0] = and_or(x, nc.m0, nc.c0);   // zero pair of columns 4h, 4h+1 as 1024+z
+      zq[1][0] = and_or(x, nc.m1, nc.c1);   // columns 4h+2, 4h+3 as 64+z
+      sq[0] = b.sv[u][0];
+      sq[1] = b.sv[u][1];
+    }
+  };
+
+  auto compute_step = [&](const W4Batch<FMT, MT, U>& b, int u, int st) {
+    const int k = st * 32 + 8 * kb;
+    u32x4 B[4];
+    if constexpr (GM == kGStep) {
+      const int g = __builtin_amdgcn_readfirstlane(group_of(a, st * 32));
+      if (g != gcur) {
+        derive(b, u);
+        gcur = g;
+      }
+    } else if constexpr (GM == kGLane) {
+      derive(b, u);
+    }
+    if constexpr (FMT == kGptq) {
+      if constexpr (GM != kGElem) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const uint32_t w = b.wq[u][t], y = w >> 8;
+          B[t] = u32x4{pk_sub_mul(and_or(w, nc.m0, nc.c0), zq[t][0], sq[t]),   // k+0, k+4
+                       pk_sub_mul(and_or(w, nc.m1, nc.c1), zq[t][1], sq[t]),   // k+1, k+5
+                       pk_sub_mul(and_or(y, nc.m0, nc.c0), zq[t][0], sq[t]),   // k+2, k+6
+                       pk_sub_mul(and_or(y, nc.m1, nc.c1), zq[t][1], sq[t])};  // k+3, k+7
+        }
+      } else {
+        // arbitrary g_idx: per-element group; natural -> [0,4,1,5,...] order
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          uint16_t hv[8];
+          const uint32_t w = b.wq[u][t];
+          const int col = lcol_c + t;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const int g = a.gidx[min(k + e, a.K - 1)];
+            const uint32_t z = ((a.qz[(int64_t)g * n8 + (col >> 3)] >> (4 * (col & 7))) & 0xfu) + 1u;
+            hv[e] = dq1((w >> (4 * e)) & 0xfu, z, a.sc[(int64_t)g * a.N + col]);
+          }
+          B[t] = u32x4{(uint32_t)hv[0] | ((uint32_t)hv[4] << 16),
+                       (uint32_t)hv[1] | ((uint32_t)hv[5] << 16),
+                       (uint32_t)hv[2] | ((uint32_t)hv[6] << 16),
+                       (uint32_t)hv[3] | ((uint32_t)hv[7] << 16)};
+        }
+      }
+    } else {
+      uint32_t wa[8], wb[8];
+#pragma unroll
+      for (int t = 0; t < 8; ++t) {
+        if constexpr (GM == kGElem) {
+          // a group boundary inside the 8-row chunk: per-row parameters
+          W4Batch<FMT, MT, U> tmp;
+          const int g = group_of(a, min(k + t, a.K - 1));
+          tmp.sv[0] = ldb<u32x2>(a.sc + (int64_t)g * a.N, s_boff);
+          tmp.zw[0] = ldb<uint32_t>(a.qz + (int64_t)g * n8, z_boff);
+          derive(tmp, 0);
+        }
+        const uint32_t x = b.wd[u][t] >> zsh;
+        wa[t] = pk_sub_mul(and_or(x, nc.m0, nc.c0), zq[0][0], sq[0]);
+        wb[t] = pk_sub_mul(and_or(x, nc.m1, nc.c1), zq[1][0], sq[1]);
+      }
+#pragma unroll
+      for (int p = 0; p < 4; ++p) {
+        B[0][p] = perm_lo(wa[2 * p + 1], wa[2 * p]);
+        B[1][p] = perm_hi(wa[2 * p + 1], wa[2 * p]);
+        B[2][p] = perm_lo(wb[2 * p + 1], wb[2 * p]);
+        B[3][p] = perm_hi(wb[2 * p + 1], wb[2 * p]);
       }
     }
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      if ((st0 + u) >= wend) break;
-      const int k = (st0 + u) * 32 + 8 * kb;
-      u32x4 B[4];
-      if constexpr (FMT == kGptq) {
-        if constexpr (GMODE != kGroupsPerK) {
-          const int g = min(k, a.K - 1) / a.G;
-          const u32x2 sv = col_ok ? *(const u32x2*)(a.sc + (int64_t)g * a.N + gcol) : u32x2{0u, 0u};
-          const uint32_t zw = col_ok ? a.qz[(int64_t)g * n8 + (gcol >> 3)] : 0u;
-          const int zsh = 4 * (gcol & 7);
+    for (int t = 0; t < MT; ++t) {
+      u32x4 xv = x_to_f16<XDT>(b.xv[u][t]);
+      if constexpr (FMT == kGptq) xv = gptq_order(xv);
+      const f16x8 A = as_f16x8(xv);
 #pragma unroll
-          for (int t = 0; t < 4; ++t) {
-            const uint32_t z = ((zw >> (zsh + 4 * t)) & 0xfu) + 1u;
-            const uint32_t zz = 0x64006400u + (z | (z << 16));
-            const uint32_t s16 = (t & 1) ? (sv[t >> 1] >> 16) : (sv[t >> 1] & 0xffffu);
-            const uint32_t ss = s16 | (s16 << 16);
-            const uint32_t w = wq[u][t];
-            B[t] = u32x4{pk_sub_mul((w & 0x000f000fu) | 0x64006400u, zz, ss),
-                         pk_sub_mul(((w >> 4) & 0x000f000fu) | 0x64006400u, zz, ss),
-                         pk_sub_mul(((w >> 8) & 0x000f000fu) | 0x64006400u, zz, ss),
-                         pk_sub_mul(((w >> 12) & 0x000f000fu) | 0x64006400u, zz, ss)};
-          }
-        } else {
-          // arbitrary g_idx: per element group, natural -> [0,4,1,5,...] order
-#pragma unroll
-          for (int t = 0; t < 4; ++t) {
-            uint16_t hv[8];
-            const uint32_t w = wq[u][t];
-            const int col = gcol + t;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-              const int kk = min(k + e, a.K - 1);
-              const int g = a.gidx[kk];
-              const uint32_t z = col_ok ? ((a.qz[(int64_t)g * n8 + (col >> 3)] >> (4 * (col & 7))) & 0xfu) + 1u : 0u;
-              const uint16_t s = col_ok ? a.sc[(int64_t)g * a.N + col] : 0;
-              hv[e] = dq1((w >> (4 * e)) & 0xfu, z, s);
-            }
-            B[t] = u32x4{(uint32_t)hv[0] | ((uint32_t)hv[4] << 16),
-                         (uint32_t)hv[1] | ((uint32_t)hv[5] << 16),
-                         (uint32_t)hv[2] | ((uint32_t)hv[6] << 16),
-                         (uint32_t)hv[3] | ((uint32_t)hv[7] << 16)};
-          }
-        }
-      } else {
-        uint32_t wa[8], wb[8];
-        const int zsh = 8 * h;
-        // group parameters: (zero pair, scale pair) for columns 4h..4h+1 and
-        // 4h+2..4h+3 of the octet; one group per 8-row chunk unless the
-        // per-k path re-reads them for every row.
-        u32x2 sv = {0u, 0u};
-        uint32_t zp0 = 0u, zp1 = 0u;
-        auto group_params = [&](int row) {
-          const int g = min(row, a.K - 1) / a.G;
-          sv = col_ok ? *(const u32x2*)(a.sc + (int64_t)g * a.N + acol) : u32x2{0u, 0u};
-          const uint32_t zw = col_ok ? a.qz[(int64_t)g * n8 + (colbase >> 3) + o] : 0u;
-          zp0 = ((zw >> zsh) & 0x000f000fu) | 0x64006400u;
-          zp1 = ((zw >> (zsh + 4)) & 0x000f000fu) | 0x64006400u;
-        };
-        if constexpr (GMODE != kGroupsPerK) group_params(k);
-#pragma unroll
-        for (int t = 0; t < 8; ++t) {
-          if constexpr (GMODE == kGroupsPerK) group_params(k + t);
-          const uint32_t x = wd[u][t] >> zsh;
-          wa[t] = pk_sub_mul((x & 0x000f000fu) | 0x64006400u, zp0, sv[0]);
-          wb[t] = pk_sub_mul(((x >> 4) & 0x000f000fu) | 0x64006400u, zp1, sv[1]);
-        }
-#pragma unroll
-        for (int p = 0; p < 4; ++p) {
-          B[0][p] = perm_lo(wa[2 * p + 1], wa[2 * p]);
-          B[1][p] = perm_hi(wa[2 * p + 1], wa[2 * p]);
-          B[2][p] = perm_lo(wb[2 * p + 1], wb[2 * p]);
-          B[3][p] = perm_hi(wb[2 * p + 1], wb[2 * p]);
-        }
-      }
-#pragma unroll
-      for (int t = 0; t < MT; ++t) {
-        u32x4 xv = load_x8(a, mbase + t * 16 + j, k);
-        if constexpr (FMT == kGptq) xv = gptq_order(xv);
-        const f16x8 A = as_f16x8(xv);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) acc[t][i] = mfma_f16(A, as_f16x8(B[i]), acc[t][i]);
-      }
+      for (int i = 0; i < 4; ++i) acc[t][i] = mfma_f16(A, as_f16x8(B[i]), acc[t][i]);
     }
+  };
+
+  auto load = [&](W4Batch<FMT, MT, U>& b, int st0) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) load_step(b, u, st0 + u);
+  };
+  auto compute = [&](const W4Batch<FMT, MT, U>& b, int st0) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) compute_step(b, u, st0 + u);
+  };
+
+  // full batches: two register batches in flight (load b+1 while computing b)
+  const int nfull = max(0, wend - wbeg) / U;
+  W4Batch<FMT, MT, U> b0, b1;
+  int st = wbeg;
+  if (nfull > 0) load(b0, st);
+  int bi = 0;
+  for (; bi + 2 <= nfull; bi += 2, st += 2 * U) {
+    load(b1, st + U);
+    compute(b0, st);
+    if (bi + 2 < nfull) load(b0, st + 2 * U);
+    compute(b1, st + U);
+  }
+  if (bi < nfull) {
+    compute(b0, st);
+    st += U;
+  }
+  // remaining single steps
+  for (; st < wend; ++st) {
+    load_step(b0, 0, st);
+    gcur = -1;
+    compute_step(b0, 0, st);
   }
 
   // ---- reduce the waves' K ranges in fixed order through LDS
@@ -301,18 +428,33 @@ w4a16_skinny_kernel(W4Args a) {
 }
 
 // x16[m][j] = fp16(x[m][perm[j]]) (act-order gather + W4A16 activation
-// conversion), 8 elements per thread.
-__global__ void w4a16_prep_x_kernel(const uint16_t* __restrict__ x, int dtype, int ldx,
-                                    const int32_t* __restrict__ perm, int M, int K,
-                                    uint16_t* __restrict__ x16) {
+// conversion); each thread writes 8 consecutive outputs with one 16-byte store.
+__global__ void __launch_bounds__(64)
+w4a16_prep_x_kernel(const uint16_t* __restrict__ x, int dtype, int ldx,
+                    const int32_t* __restrict__ perm, int M, int K, uint16_t* __restrict__ x16) {
   const int64_t idx = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 8;
   if (idx >= (int64_t)M * K) return;
   const int m = (int)(idx / K), k0 = (int)(idx % K);
   const uint16_t* row = x + (int64_t)m * ldx;
+  if (k0 + 8 <= K && (K % 8) == 0) {
+    const i32x4 p0 = *(const i32x4*)(perm + k0);
+    const i32x4 p1 = *(const i32x4*)(perm + k0 + 4);
+    uint16_t h[8];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      h[e] = act_bits(row[p0[e]], dtype);
+      h[e + 4] = act_bits(row[p1[e]], dtype);
+    }
+    u32x4 v;
+#pragma unroll
+    for (int d = 0; d < 4; ++d) v[d] = (uint32_t)h[2 * d] | ((uint32_t)h[2 * d + 1] << 16);
+    *(u32x4*)(x16 + (int64_t)m * K + k0) = v;
+    return;
+  }
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
     const int k = k0 + e;
-    if (k < K) x16[(int64_t)m * K + k] = act_bits(row[perm ? perm[k] : k], dtype);
+    if (k < K) x16[(int64_t)m * K + k] = act_bits(row[perm[k]], dtype);
   }
 }
 
@@ -343,7 +485,7 @@ static W4Plan plan_w4(int M, int N, int K, bool needs_x16, size_t ws_bytes, bool
   W4Plan p{};
   const int mt_needed = M >= 64 ? 4 : (M + 15) / 16;
   p.mt = mt_needed <= 1 ? 1 : (mt_needed <= 2 ? 2 : 4);
-  p.waves = p.mt == 1 ? 8 : 4;
+  p.waves = 4;
   p.mblocks = (M + p.mt * 16 - 1) / (p.mt * 16);
   p.tiles = (N + kW4Cols - 1) / kW4Cols;
   p.x16_bytes = needs_x16 ? ((size_t)M * K * 2 + 255) / 256 * 256 : 0;
@@ -359,15 +501,26 @@ static W4Plan plan_w4(int M, int N, int K, bool needs_x16, size_t ws_bytes, bool
   return p;
 }
 
-template <int FMT, int GMODE>
-static void launch_w4(const W4Args& a, const W4Plan& p, hipStream_t stream) {
+template <int FMT, int GM, int XDT, bool PRED>
+static void launch_w4_mt(const W4Args& a, const W4Plan& p, hipStream_t stream) {
   dim3 grid(p.tiles * p.splits, p.mblocks);
   if (p.mt == 1)
-    hipLaunchKernelGGL((w4a16_skinny_kernel<FMT, 1, GMODE, 8>), grid, dim3(512), 0, stream, a);
+    hipLaunchKernelGGL((w4a16_skinny_kernel<FMT, 1, GM, XDT, PRED, 4>), grid, dim3(256), 0, stream, a);
   else if (p.mt == 2)
-    hipLaunchKernelGGL((w4a16_skinny_kernel<FMT, 2, GMODE, 4>), grid, dim3(256), 0, stream, a);
+    hipLaunchKernelGGL((w4a16_skinny_kernel<FMT, 2, GM, XDT, PRED, 4>), grid, dim3(256), 0, stream, a);
   else
-    hipLaunchKernelGGL((w4a16_skinny_kernel<FMT, 4, GMODE, 4>), grid, dim3(256), 0, stream, a);
+    hipLaunchKernelGGL((w4a16_skinny_kernel<FMT, 4, GM, XDT, PRED, 4>), grid, dim3(256), 0, stream, a);
+}
+
+template <int FMT, int GM>
+static void launch_w4(const W4Args& a, const W4Plan& p, int xdt, bool pred, hipStream_t stream) {
+  if (pred) {
+    if (xdt == kXF16) launch_w4_mt<FMT, GM, kXF16, true>(a, p, stream);
+    else launch_w4_mt<FMT, GM, kXBF16, true>(a, p, stream);
+  } else {
+    if (xdt == kXF16) launch_w4_mt<FMT, GM, kXF16, false>(a, p, stream);
+    else launch_w4_mt<FMT, GM, kXBF16, false>(a, p, stream);
+  }
 }
 
 static int run_w4(const char* what, int fmt, W4Args a, int gmode, void* workspace,
@@ -376,7 +529,8 @@ static int run_w4(const char* what, int fmt, W4Args a, int gmode, void* workspac
     set_error("%s: activation dtype must be fp16 or bf16", what);
     return KQ_EUNSUPPORTED;
   }
-  if (a.M < 0 || a.N < 8 || a.K < 1 || (a.N % 8) != 0 || a.G < 1 || a.ldx < a.K) {
+  if (a.M < 0 || a.N < 8 || a.K < 1 || (a.N % 8) != 0 || a.G < 1 || a.ldx < a.K ||
+      a.K >= (1 << 24) || a.G >= (1 << 16)) {
     set_error("%s: bad shape m=%d n=%d k=%d group=%d", what, a.M, a.N, a.K, a.G);
     return KQ_EINVAL;
   }
@@ -389,6 +543,8 @@ static int run_w4(const char* what, int fmt, W4Args a, int gmode, void* workspac
     return KQ_EINVAL;
   }
   if (a.M == 0) return KQ_OK;
+  // floor(k / G) = (k * ceil(2^40 / G)) >> 40, exact for k < 2^24, G < 2^16
+  a.gmagic = (((uint64_t)1 << 40) + (uint64_t)a.G - 1) / (uint64_t)a.G;
   const bool needs_x16 = gmode == kGroupsPermuted;
   W4Plan p = plan_w4(a.M, a.N, a.K, needs_x16, ws_bytes, workspace != nullptr);
   if (p.x16_bytes + p.partial_bytes > (workspace ? ws_bytes : 0)) {
@@ -396,25 +552,31 @@ static int run_w4(const char* what, int fmt, W4Args a, int gmode, void* workspac
               workspace ? ws_bytes : (size_t)0, p.x16_bytes + p.partial_bytes);
     return KQ_EWORKSPACE;
   }
+  int xdt = a.x_dtype == KQ_DTYPE_F16 ? kXF16 : kXBF16;
   if (needs_x16) {
     uint16_t* x16 = (uint16_t*)workspace;
     const int64_t threads = ((int64_t)a.M * a.K + 7) / 8;
-    hipLaunchKernelGGL(w4a16_prep_x_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0,
+    hipLaunchKernelGGL(w4a16_prep_x_kernel, dim3((unsigned)((threads + 63) / 64)), dim3(64), 0,
                        stream, a.x, a.x_dtype, a.ldx, a.perm, a.M, a.K, x16);
     a.x = x16;
-    a.x_dtype = KQ_DTYPE_F16;
     a.ldx = a.K;
+    xdt = kXF16;
   }
-  a.x_vec = ((uintptr_t)a.x % 16) == 0 && (a.ldx % 8) == 0;
+  const bool pred = (a.K % 32) != 0 || ((uintptr_t)a.x % 16) != 0 || (a.ldx % 8) != 0;
   a.splits = p.splits;
   a.steps_per_split = p.steps_per_split;
   a.partials = p.splits > 1 ? (float*)((uint8_t*)workspace + p.x16_bytes) : nullptr;
+  // kernel group addressing: per element (g_idx, or a group boundary inside
+  // an 8-row chunk), per lane chunk, or per step for the whole wave
+  const int gm = gmode == kGroupsPerK ? kGElem : ((a.G % 32) == 0 ? kGStep : kGLane);
   if (fmt == kGptq) {
-    if (gmode == kGroupsPerK) launch_w4<kGptq, kGroupsPerK>(a, p, stream);
-    else launch_w4<kGptq, kGroupsUniform>(a, p, stream);
+    if (gm == kGElem) launch_w4<kGptq, kGElem>(a, p, xdt, pred, stream);
+    else if (gm == kGStep) launch_w4<kGptq, kGStep>(a, p, xdt, pred, stream);
+    else launch_w4<kGptq, kGLane>(a, p, xdt, pred, stream);
   } else {
-    if (gmode == kGroupsPerK) launch_w4<kAwq, kGroupsPerK>(a, p, stream);
-    else launch_w4<kAwq, kGroupsUniform>(a, p, stream);
+    if (gm == kGElem) launch_w4<kAwq, kGElem>(a, p, xdt, pred, stream);
+    else if (gm == kGStep) launch_w4<kAwq, kGStep>(a, p, xdt, pred, stream);
+    else launch_w4<kAwq, kGLane>(a, p, xdt, pred, stream);
   }
   if (p.splits > 1) {
     ReduceArgs r{a.partials, p.splits, a.M, a.N, nullptr, nullptr, 0, a.bias, a.bias_dtype,

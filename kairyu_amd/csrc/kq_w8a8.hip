@@ -99,7 +99,14 @@ KQ_DEV typename W8Traits<FMT>::Acc mfma_w8(typename W8Traits<FMT>::Frag a,
 constexpr int kSkinnyWaves = 8;
 constexpr int kSkinnyCols = 16;
 
-template <int FMT, int MT, int U>
+template <typename T>
+KQ_DEV T ldb(const void* base, uint32_t byte_off) {
+  return *(const T*)((const char*)base + byte_off);
+}
+
+// PRED = false: K is a multiple of the MFMA step, so loads need no guards
+// (rows beyond M / N are clamped to valid memory and never stored).
+template <int FMT, int MT, int U, bool PRED>
 __global__ void __launch_bounds__(64 * kSkinnyWaves)
 w8a8_skinny_kernel(const uint8_t* __restrict__ xq, const uint8_t* __restrict__ w, int K,
                    int steps_per_split, int splits, Epi ep, void* __restrict__ partials) {
@@ -107,7 +114,8 @@ w8a8_skinny_kernel(const uint8_t* __restrict__ xq, const uint8_t* __restrict__ w
   using Acc = typename T::Acc;
   using Frag = typename T::Frag;
   __shared__ uint32_t red[(kSkinnyWaves - 1) * MT * 4 * 64];
-  const int lane = lane_id(), wave = wave_id();
+  const int lane = lane_id();
+  const int wave = __builtin_amdgcn_readfirstlane(wave_id());
   const int j = lane & 15, kg = lane >> 4;
   const int tile = blockIdx.x / splits, split = blockIdx.x % splits;
   const int n = tile * kSkinnyCols + j;
@@ -118,32 +126,58 @@ w8a8_skinny_kernel(const uint8_t* __restrict__ xq, const uint8_t* __restrict__ w
   const int per_wave = (send - sbeg + kSkinnyWaves - 1) / kSkinnyWaves;
   const int wbeg = sbeg + wave * per_wave;
   const int wend = min(send, wbeg + per_wave);
-  const uint8_t* wrow = w + (int64_t)(n_ok ? n : 0) * K;
+  // loop-invariant 32-bit byte offsets (rows clamped to valid memory)
+  const uint32_t w_boff = (uint32_t)((n_ok ? n : ep.N - 1) * K + kg * T::kLane);
+  uint32_t x_boff[MT];
+#pragma unroll
+  for (int t = 0; t < MT; ++t) x_boff[t] = (uint32_t)(min(t * 16 + j, ep.M - 1) * K + kg * T::kLane);
 
   Acc acc[MT];
 #pragma unroll
   for (int t = 0; t < MT; ++t) acc[t] = Acc{0, 0, 0, 0};
 
-  for (int st = wbeg; st < wend; st += U) {
+  auto frag = [&](const uint8_t* base, uint32_t off, int k) -> Frag {
+    if constexpr (!PRED) {
+      if constexpr (FMT == kFmtI8) {
+        return ldb<i32x4>(base, off);
+      } else {
+        const i32x4 lo = ldb<i32x4>(base, off), hi = ldb<i32x4>(base, off + 16);
+        return i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+      }
+    } else {
+      return load_frag<FMT>(base + off, k < K, k + 16 < K);
+    }
+  };
+  // two register batches of U steps: load batch b+1 while computing batch b
+  struct Batch {
     Frag b[U];
     Frag a[U][MT];
+  };
+  auto load = [&](Batch& bt, int st0) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const bool s_ok = st + u < wend;
-      const int k = (st + u) * T::kStep + kg * T::kLane;
-      b[u] = load_frag<FMT>(wrow + k, s_ok && n_ok && k < K, s_ok && n_ok && k + 16 < K);
+      const int st = min(st0 + u, wend - 1);  // surplus steps reload; never computed
+      const int k = st * T::kStep + kg * T::kLane;
+      bt.b[u] = frag(w + (int64_t)st * T::kStep, w_boff, k);
 #pragma unroll
-      for (int t = 0; t < MT; ++t) {
-        const int m = t * 16 + j;
-        const bool m_ok = s_ok && m < ep.M;
-        a[u][t] = load_frag<FMT>(xq + (int64_t)(m < ep.M ? m : 0) * K + k, m_ok && k < K,
-                                 m_ok && k + 16 < K);
-      }
+      for (int t = 0; t < MT; ++t) bt.a[u][t] = frag(xq + (int64_t)st * T::kStep, x_boff[t], k);
     }
+  };
+  auto compute = [&](const Batch& bt, int st0) {
 #pragma unroll
-    for (int u = 0; u < U; ++u)
+    for (int u = 0; u < U; ++u) {
+      if (st0 + u >= wend) break;
 #pragma unroll
-      for (int t = 0; t < MT; ++t) acc[t] = mfma_w8<FMT>(a[u][t], b[u], acc[t]);
+      for (int t = 0; t < MT; ++t) acc[t] = mfma_w8<FMT>(bt.a[u][t], bt.b[u], acc[t]);
+    }
+  };
+  Batch b0, b1;
+  if (wbeg < wend) load(b0, wbeg);
+  for (int st = wbeg; st < wend; st += 2 * U) {
+    if (st + U < wend) load(b1, st + U);
+    compute(b0, st);
+    if (st + 2 * U < wend) load(b0, st + 2 * U);
+    compute(b1, st + U);
   }
 
   // fixed-order reduction of the waves' K ranges
@@ -327,10 +361,15 @@ static void launch_skinny(const uint8_t* xq, const uint8_t* w, int K, const Epi&
          plane * splits * 2 <= ws_bytes)
     splits *= 2;
   const int steps_per_split = (nsteps + splits - 1) / splits;
-  constexpr int U = FMT == kFmtI8 ? 4 : 2;
-  hipLaunchKernelGGL((w8a8_skinny_kernel<FMT, MT, U>), dim3(tiles * splits),
-                     dim3(64 * kSkinnyWaves), 0, stream, xq, w, K, steps_per_split, splits, ep,
-                     workspace);
+  constexpr int U = MT == 4 ? (FMT == kFmtI8 ? 2 : 1) : (FMT == kFmtI8 ? 4 : 2);
+  if (K % T::kStep == 0)
+    hipLaunchKernelGGL((w8a8_skinny_kernel<FMT, MT, U, false>), dim3(tiles * splits),
+                       dim3(64 * kSkinnyWaves), 0, stream, xq, w, K, steps_per_split, splits, ep,
+                       workspace);
+  else
+    hipLaunchKernelGGL((w8a8_skinny_kernel<FMT, MT, U, true>), dim3(tiles * splits),
+                       dim3(64 * kSkinnyWaves), 0, stream, xq, w, K, steps_per_split, splits, ep,
+                       workspace);
   if (splits > 1) {
     ReduceArgs r{workspace, splits, ep.M, ep.N, ep.xscale, ep.wscale, ep.ws_per_channel,
                  ep.bias, ep.bias_dtype, ep.out, ep.out_dtype, ep.acc_out};
@@ -359,6 +398,10 @@ static int run_w8a8(const char* what, const uint8_t* xq, const uint8_t* w, int64
     hipLaunchKernelGGL(w8a8_generic_kernel<FMT>, dim3((unsigned)((total + 255) / 256)),
                        dim3(256), 0, stream, xq, w, K, ep);
     return check_launch(what);
+  }
+  if (m <= 64 && (n * k >= ((int64_t)1 << 32) || m * k >= ((int64_t)1 << 32))) {
+    set_error("%s: weight or activation exceeds the 4 GiB addressing of the skinny kernel", what);
+    return KQ_EINVAL;
   }
   if (m <= 16) launch_skinny<FMT, 1>(xq, w, K, ep, workspace, ws_bytes, stream);
   else if (m <= 32) launch_skinny<FMT, 2>(xq, w, K, ep, workspace, ws_bytes, stream);
