@@ -122,6 +122,39 @@ int kq_w4a16_gptq_gemm(const void* x, int x_dtype, const int32_t* qweight,
                        int group_size, void* workspace, size_t workspace_bytes,
                        void* stream);
 
+/* Load-time tiling of a W4A16 weight for the tiled kernels: tiles int32
+ * [ceil(n/16)][k/8][16], word (u, r, c) holding q[row(8r + e)][16u + c] in
+ * nibble e, row(k) = perm[k] when perm is given (GPTQ act-order: the stable
+ * argsort of g_idx, so permuted row j has group j / group_size), else k;
+ * columns past n are 0.  src_format 0: AWQ qweight [k, n/8]; 1: GPTQ qweight
+ * [k/8, n].  Derived operand only; checkpoint buffers are untouched (the
+ * reference caches derived runtime operands the same way,
+ * quant_gemm_gpu.py:802-850; formats kairyu/quant/awq.py:14-36,
+ * kairyu/quant/gptq.py:15-46). */
+int kq_w4a16_tile_weights(const int32_t* qweight, int src_format, const int32_t* perm,
+                          int32_t* tiles, int64_t n, int64_t k, void* stream);
+
+/* AWQ qzeros [groups, n/8] (AWQ nibble order) -> natural nibble order
+ * (column 8w + i in nibble i), values unchanged: the zero operand of
+ * kq_w4a16_tiled_gemm with zero_offset 0 (kairyu/quant/awq.py:14-36). */
+int kq_awq_natural_zeros(const int32_t* qzeros, int32_t* qzeros_n, int64_t n, int64_t groups,
+                         void* stream);
+
+/* W4A16 on kq_w4a16_tile_weights' tiles: w = fp16((q - z) * s[group]) with
+ * z = stored nibble + zero_offset (GPTQ qzeros: 1; AWQ natural zeros: 0),
+ * qzeros [groups, n/8] natural nibble order, scales fp16 [groups, n],
+ * group = row / group_size of the (permuted) row; x fed to the dot as fp16
+ * (bf16 saturated to +-65504), fp32 accumulation, out in x_dtype.  perm
+ * (nullable) is the act-order permutation the tiles were built with: x is
+ * gathered through it (workspace: m*k*2 bytes).  M <= 16 with k in
+ * {1024, 2048, 4096} runs the persistent decode GEMV.
+ * Replaces _awq_w4a16_kernel / _gptq_w4a16_kernel and awq_linear_forward /
+ * gptq_linear_forward (quant_gemm_gpu.py:224-407,690-761). */
+int kq_w4a16_tiled_gemm(const void* x, int x_dtype, const int32_t* tiles, const int32_t* qzeros,
+                        int zero_offset, const void* scales, const int32_t* perm, const void* bias,
+                        int bias_dtype, void* out, int64_t m, int64_t n, int64_t k, int group_size,
+                        void* workspace, size_t workspace_bytes, void* stream);
+
 /* Bytes of `workspace` a W4A16 call of this shape needs (gidx_mode as for
  * kq_w4a16_gptq_gemm; AWQ uses 0).  No reference counterpart: sizing helper
  * for the caller-owned scratch buffer. */

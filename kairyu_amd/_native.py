@@ -52,6 +52,11 @@ _SIGNATURES: dict[str, list] = {
         _P, _I, _P, _P, _P, _P, _P, _I, _P, _I, _P, _I64, _I64, _I64, _I, _P, _SZ, _P,
     ],
     "kq_gptq_permute_qweight": [_P, _P, _P, _I64, _I64, _P],
+    "kq_w4a16_tile_weights": [_P, _I, _P, _P, _I64, _I64, _P],
+    "kq_awq_natural_zeros": [_P, _P, _I64, _I64, _P],
+    "kq_w4a16_tiled_gemm": [
+        _P, _I, _P, _P, _I, _P, _P, _P, _I, _P, _I64, _I64, _I64, _I, _P, _SZ, _P,
+    ],
     "kq_w4a16_workspace_size": [_I64, _I64, _I64, _I],
 }
 

@@ -115,6 +115,32 @@ KQ_DEV f32x4 mfma_fp8(i32x8 a, i32x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 127, 0, 127);
 }
 
+// ------------------------------------------------------------- buffer loads
+// Raw buffer loads: a 128-bit resource held in SGPRs (base, byte size, gfx9
+// format word) plus a 32-bit per-lane byte offset and a uniform SGPR offset.
+// No per-lane 64-bit address arithmetic; offsets at or beyond the resource's
+// byte size read as 0.  `aux` bit 1 marks the access non-temporal.
+}  // namespace kq
+__device__ int32_t kq_rbl_i32(i32x4 rsrc, int32_t voff, int32_t soff, int32_t aux)
+    __asm("llvm.amdgcn.raw.buffer.load.i32");
+__device__ short kq_rbl_i16(i32x4 rsrc, int32_t voff, int32_t soff, int32_t aux)
+    __asm("llvm.amdgcn.raw.buffer.load.i16");
+__device__ i32x4 kq_rbl_v4i32(i32x4 rsrc, int32_t voff, int32_t soff, int32_t aux)
+    __asm("llvm.amdgcn.raw.buffer.load.v4i32");
+namespace kq {
+
+constexpr int32_t kAuxNT = 2;
+
+KQ_DEV i32x4 make_rsrc(const void* base, uint32_t bytes) {
+  const uint64_t a = (uint64_t)(uintptr_t)base;
+  i32x4 r;
+  r[0] = __builtin_amdgcn_readfirstlane((int32_t)(uint32_t)a);
+  r[1] = __builtin_amdgcn_readfirstlane((int32_t)(uint32_t)(a >> 32));  // stride 0
+  r[2] = __builtin_amdgcn_readfirstlane((int32_t)bytes);
+  r[3] = 0x00020000;  // gfx9 buffer format word (32-bit data, no swizzle)
+  return r;
+}
+
 // ------------------------------------------------------------- wave helpers
 KQ_DEV int lane_id() { return (int)(threadIdx.x & 63); }
 KQ_DEV int wave_id() { return (int)(threadIdx.x >> 6); }

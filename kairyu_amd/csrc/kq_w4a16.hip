@@ -10,7 +10,13 @@
 // exact and one packed fp16 multiply yields the same correctly rounded
 // fp16((q-z)*s) as the reference's fp32 product rounded to fp16.
 //
-// Kernel (M <= 64 per row block): a workgroup owns 64 output columns; its
+// Kernels:
+//   * decode GEMV (M <= 16, K in {1024, 2048, 4096}, load-time tiled weights):
+//     one 16-wave workgroup per CU, x held in registers, weights streamed
+//     through buffer loads with three 16-column blocks in flight (below);
+//   * skinny kernel (every other shape, checkpoint or tiled layout), next.
+//
+// Skinny kernel (M <= 64 per row block): a workgroup owns 64 output columns; its
 // waves take contiguous K ranges and each lane dequantizes straight into the
 // B operand of v_mfma_f32_16x16x32_f16 (no LDS for weights); the waves reduce
 // through LDS in fixed order.  Shapes with too few column tiles also split K
@@ -42,6 +48,10 @@ enum { kGroupsUniform = 0, kGroupsPermuted = 1, kGroupsPerK = 2 };
 // lane's 8-k chunk (group_size % 8 == 0), or a group per element (g_idx).
 enum { kGStep = 0, kGLane = 1, kGElem = 2 };
 enum { kXF16 = 0, kXBF16 = 1 };
+// qweight layouts (8 consecutive k per word, LSB first): [K/8][N] words
+// (checkpoint GPTQ order) or 16-column tiles [ceil(N/16)][K/8][16] (each
+// tile's words contiguous, built at load time by kq_w4a16_tile_weights)
+enum { kLayoutRows = 0, kLayoutTiles = 1 };
 
 constexpr int kW4Cols = 64;   // columns per workgroup tile
 
@@ -63,6 +73,8 @@ struct W4Args {
   int steps_per_split;
   int splits;
   float* partials;       // [splits][M][N] when splits > 1
+  uint32_t zoff;         // added to stored zero nibbles (GPTQ 1, natural-order AWQ 0)
+  int layout;            // kLayoutRows (qweight [K/8][N]) or kLayoutTiles
 };
 
 KQ_DEV int group_of(const W4Args& a, int k) {
@@ -139,6 +151,11 @@ template <typename T>
 KQ_DEV T ldb(const void* base, uint32_t byte_off) {
   return *(const T*)((const char*)base + byte_off);
 }
+template <typename T, bool NT>
+KQ_DEV T ldw(const void* base, uint32_t byte_off) {
+  if constexpr (NT) return __builtin_nontemporal_load((const T*)((const char*)base + byte_off));
+  else return *(const T*)((const char*)base + byte_off);
+}
 
 // (x & mask) | magic in one VOP3 (gfx9 allows a single SGPR/literal operand,
 // so the magic constant lives in a VGPR).
@@ -161,11 +178,11 @@ struct NibbleConsts {
 // PRED = false: every step of the kernel is a full 32-k step and x rows are
 // 16-byte aligned; loads carry no predicates (columns and rows are clamped to
 // valid addresses and the surplus results are never stored).  PRED = true
-// guards every load (K tails, unaligned x).
-template <int FMT, int MT, int GM, int XDT, bool PRED, int WAVES>
+// guards every load (K tails, unaligned x).  U = steps per register batch
+// (two batches in flight), NT = weights streamed with non-temporal loads.
+template <int FMT, int MT, int GM, int XDT, bool PRED, int WAVES, int U, bool NT, bool TILED = false>
 __global__ void __launch_bounds__(64 * WAVES)
 w4a16_skinny_kernel(W4Args a) {
-  constexpr int U = 4;
   __shared__ float red[(WAVES - 1) * MT * 16 * 64];
   const int lane = lane_id();
   const int wave = __builtin_amdgcn_readfirstlane(wave_id());
@@ -196,7 +213,9 @@ w4a16_skinny_kernel(W4Args a) {
   nc.c1 = 0x54005400u + (uint32_t)(lane & 0);
 
   // loop-invariant 32-bit byte offsets of this lane
-  const uint32_t w_boff = FMT == kGptq ? (uint32_t)(kb * a.N + lcol_c) * 4u
+  const uint32_t w_boff = (FMT == kGptq && a.layout == kLayoutTiles)
+                             ? (uint32_t)(((lcol_c >> 4) * (a.K / 8) + kb) * 64 + (lcol_c & 15) * 4)
+                         : FMT == kGptq ? (uint32_t)(kb * a.N + lcol_c) * 4u
                                        : (uint32_t)(8 * kb * n8 + zword) * 4u;
   const uint32_t s_boff = (uint32_t)lcol_c * 2u;
   const uint32_t z_boff = (uint32_t)zword * 4u;
@@ -219,19 +238,33 @@ w4a16_skinny_kernel(W4Args a) {
   auto load_step = [&](W4Batch<FMT, MT, U>& b, int u, int st) {
     const int k = st * 32 + 8 * kb;
     const bool ok = !PRED || (k < a.K && col_ok);
-    if constexpr (FMT == kGptq) {
-      const uint32_t* base = a.qw + (int64_t)st * 4 * a.N;
-      b.wq[u] = ok ? ldb<u32x4>(base, w_boff) : u32x4{0u, 0u, 0u, 0u};
+    if constexpr (FMT == kGptq && TILED) {
+      // tile-contiguous layout: [N/64][K/8][64] words
+      const uint32_t* base = a.qw + ((int64_t)tile * (a.K / 8) + (int64_t)st * 4) * 64;
+      b.wq[u] = ldw<u32x4, NT>(base, (uint32_t)(kb * 64 + 4 * j) * 4u);
+    } else if constexpr (FMT == kGptq) {
+      // rows: word row st*4 + kb starts at (st*4)*N; tiles: at (st*4)*16
+      const uint32_t* base = a.qw + (int64_t)st * 4 * (a.layout == kLayoutTiles ? 16 : a.N);
+      b.wq[u] = ok ? ldw<u32x4, NT>(base, w_boff) : u32x4{0u, 0u, 0u, 0u};
     } else {
       const uint32_t* base = a.qw + (int64_t)st * 32 * n8;
 #pragma unroll
       for (int t = 0; t < 8; ++t)
-        b.wd[u][t] = (!PRED || (ok && k + t < a.K)) ? ldb<uint32_t>(base, w_boff + (uint32_t)(t * n8 * 4)) : 0u;
+        b.wd[u][t] = (!PRED || (ok && k + t < a.K)) ? ldw<uint32_t, NT>(base, w_boff + (uint32_t)(t * n8 * 4)) : 0u;
     }
-    if constexpr (GM != kGElem) {
+    if constexpr (GM == kGLane) {
       const int g = step_group(st, k);
       b.sv[u] = ldb<u32x2>(a.sc + (int64_t)g * a.N, s_boff);
       b.zw[u] = ldb<uint32_t>(a.qz + (int64_t)g * n8, z_boff);
+    } else if constexpr (GM == kGStep) {
+      // derive() reads a step's scale/zero words only where the group changes:
+      // at a batch's first step (the previous batch may have ended a group or
+      // this is the wave's first step) and at a group's first step
+      const int g = step_group(st, k);
+      if (u == 0 || group_of(a, st * 32) != group_of(a, st * 32 - 32)) {
+        b.sv[u] = ldb<u32x2>(a.sc + (int64_t)g * a.N, s_boff);
+        b.zw[u] = ldb<uint32_t>(a.qz + (int64_t)g * n8, z_boff);
+      }
     }
     const uint16_t* xb = a.x + (int64_t)st * 32;
 #pragma unroll
@@ -258,7 +291,7 @@ w4a16_skinny_kernel(W4Args a) {
     if constexpr (FMT == kGptq) {
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
-        const uint32_t z = ((b.zw[u] >> (zsh + 4 * t)) & 0xfu) + 1u;
+        const uint32_t z = ((b.zw[u] >> (zsh + 4 * t)) & 0xfu) + a.zoff;
         zq[t][0] = nc.c0 + z * 0x00010001u;   // (1024 + z) pair
         zq[t][1] = nc.c1 + z * 0x00100010u;   // (64 + z) pair: z on the nibble's bit place
         const uint32_t s16 = (t & 1) ? (b.sv[u][t >> 1] >> 16) : (b.sv[u][t >> 1] & 0xffffu);
@@ -305,7 +338,7 @@ w4a16_skinny_kernel(W4Args a) {
 #pragma unroll
           for (int e = 0; e < 8; ++e) {
             const int g = a.gidx[min(k + e, a.K - 1)];
-            const uint32_t z = ((a.qz[(int64_t)g * n8 + (col >> 3)] >> (4 * (col & 7))) & 0xfu) + 1u;
+            const uint32_t z = ((a.qz[(int64_t)g * n8 + (col >> 3)] >> (4 * (col & 7))) & 0xfu) + a.zoff;
             hv[e] = dq1((w >> (4 * e)) & 0xfu, z, a.sc[(int64_t)g * a.N + col]);
           }
           B[t] = u32x4{(uint32_t)hv[0] | ((uint32_t)hv[4] << 16),
@@ -427,6 +460,176 @@ w4a16_skinny_kernel(W4Args a) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// Decode GEMV (M <= 16, K = 16 waves x S steps x 32 with S in {2, 4, 8},
+// group_size a multiple of 32 whose boundaries fall at fixed steps of every
+// wave's window).
+//
+// One 16-wave workgroup per CU owns a balanced run of 16-column blocks.  Wave
+// w owns steps [w*S, w*S + S): it loads those x chunks once as MFMA A
+// operands and keeps them in registers while it streams the weights of every
+// column block of the workgroup with D blocks in flight, so x is read once
+// per wave rather than once per column block.  Lane (j = l%16, kb = l/16)
+// dequantizes the packed word of column block*16 + j, packed row step*4 + kb:
+// the B operand of one v_mfma_f32_16x16x32_f16 (k order [0,4,1,5,2,6,3,7],
+// matched in A).  The 16 waves' partial sums meet in LDS and are added in
+// wave order, so results do not depend on timing.  Weights, scales and zeros
+// are read through buffer resources: every address is a scalar base and
+// offset plus one fixed 32-bit lane offset; reads past a buffer return 0 and
+// columns past N are computed but never stored.
+//
+// Weight layouts: LAYOUT_ROWS = qweight [K/8][N] (checkpoint GPTQ order);
+// LAYOUT_TILES = [ceil(N/16)][K/8][16] (each block's words contiguous).
+constexpr int kGvWaves = 16;
+
+struct GvPlan {
+  int wgs, units;
+};
+
+template <int S, int SPG>
+struct GvShape {
+  static constexpr int kGroups = SPG >= S ? 1 : S / SPG;        // group slots per window
+  static constexpr int kDepth = (S + 2 * kGroups) > 16 ? 2 : 3;  // blocks in flight
+};
+
+template <int S, int SPG>
+struct GvBlock {
+  uint32_t w[S];
+  uint32_t sv[GvShape<S, SPG>::kGroups];
+  uint32_t zw[GvShape<S, SPG>::kGroups];
+};
+
+struct GvCtx {
+  i32x4 rw, rs, rz;      // buffer resources: qweight, scales, qzeros
+  int32_t wlane;         // lane byte offset inside a step (layout dependent)
+  int32_t slane, zlane;  // lane byte offsets of its scale / zero word
+  int st0;               // first step of this wave
+  int g0;                // group of the first step
+};
+
+template <int S, int SPG, int LAYOUT>
+KQ_DEV void gv_load(const W4Args& a, const GvCtx& c, int unit, GvBlock<S, SPG>& b) {
+#pragma unroll
+  for (int s = 0; s < S; ++s) {
+    const int32_t so = LAYOUT == kLayoutTiles
+                           ? (unit * (a.K / 8) + (c.st0 + s) * 4) * 64
+                           : (c.st0 + s) * 16 * a.N + unit * 64;
+    b.w[s] = (uint32_t)kq_rbl_i32(c.rw, c.wlane, so, kAuxNT);
+  }
+#pragma unroll
+  for (int i = 0; i < GvShape<S, SPG>::kGroups; ++i) {
+    const int g = c.g0 + i;
+    b.sv[i] = (uint16_t)kq_rbl_i16(c.rs, c.slane, (g * a.N + unit * 16) * 2, 0);
+    b.zw[i] = (uint32_t)kq_rbl_i32(c.rz, c.zlane, (g * (a.N / 8) + unit * 2) * 4, 0);
+  }
+}
+
+template <int S, int SPG>
+KQ_DEV f32x4 gv_compute(const W4Args& a, const NibbleConsts& nc, uint32_t zsh,
+                        const GvBlock<S, SPG>& b, const u32x4 (&A)[S]) {
+  f32x4 acc{0.f, 0.f, 0.f, 0.f};
+  uint32_t zq0 = 0, zq1 = 0, sq = 0;
+#pragma unroll
+  for (int s = 0; s < S; ++s) {
+    if (SPG >= S ? s == 0 : (s % SPG) == 0) {
+      const int i = SPG >= S ? 0 : s / SPG;
+      const uint32_t z = ((b.zw[i] >> zsh) & 0xfu) + a.zoff;
+      zq0 = nc.c0 + z * 0x00010001u;   // (1024 + z) pair
+      zq1 = nc.c1 + z * 0x00100010u;   // (64 + z) pair
+      sq = b.sv[i] * 0x00010001u;
+    }
+    const uint32_t w = b.w[s], y = w >> 8;
+    const u32x4 B{pk_sub_mul(and_or(w, nc.m0, nc.c0), zq0, sq),   // k+0, k+4
+                  pk_sub_mul(and_or(w, nc.m1, nc.c1), zq1, sq),   // k+1, k+5
+                  pk_sub_mul(and_or(y, nc.m0, nc.c0), zq0, sq),   // k+2, k+6
+                  pk_sub_mul(and_or(y, nc.m1, nc.c1), zq1, sq)};  // k+3, k+7
+    acc = mfma_f16(as_f16x8(A[s]), as_f16x8(B), acc);
+  }
+  return acc;
+}
+
+template <int XDT, int S, int SPG, int LAYOUT>
+__global__ void __launch_bounds__(64 * kGvWaves)
+w4a16_gemv_kernel(W4Args a, GvPlan p) {
+  constexpr int D = GvShape<S, SPG>::kDepth;
+  __shared__ float red[kGvWaves][D * 4][64];
+  const int lane = lane_id();
+  const int wave = __builtin_amdgcn_readfirstlane(wave_id());
+  const int j = lane & 15, kb = lane >> 4;
+  // balanced unit range of this workgroup
+  const int base = p.units / p.wgs, rem = p.units % p.wgs;
+  const int bid = blockIdx.x;
+  const int u0 = bid * base + min(bid, rem);
+  const int ncb = base + (bid < rem ? 1 : 0);
+
+  NibbleConsts nc;
+  nc.m0 = __builtin_amdgcn_readfirstlane(0x000f000fu);
+  nc.m1 = __builtin_amdgcn_readfirstlane(0x00f000f0u);
+  nc.c0 = 0x64006400u + (uint32_t)(lane & 0);
+  nc.c1 = 0x54005400u + (uint32_t)(lane & 0);
+
+  GvCtx c;
+  const int ngroups = (a.K + a.G - 1) / a.G;
+  const int npad = (a.N + 15) / 16 * 16;
+  c.rw = make_rsrc(a.qw, (uint32_t)((a.K / 8) * (LAYOUT == kLayoutTiles ? npad : a.N) * 4));
+  c.rs = make_rsrc(a.sc, (uint32_t)(ngroups * a.N * 2));
+  c.rz = make_rsrc(a.qz, (uint32_t)(ngroups * (a.N / 8) * 4));
+  c.wlane = LAYOUT == kLayoutTiles ? (kb * 16 + j) * 4 : (kb * a.N + j) * 4;
+  c.slane = j * 2;
+  c.zlane = (j >> 3) * 4;
+  c.st0 = wave * S;
+  c.g0 = __builtin_amdgcn_readfirstlane(group_of(a, c.st0 * 32));
+  const uint32_t zsh = 4u * (uint32_t)(j & 7);
+
+  // x chunks of this wave's steps, loaded once and kept for every block
+  u32x4 A[S];
+  {
+    const uint16_t* xr = a.x + (int64_t)min(j, a.M - 1) * a.ldx + c.st0 * 32 + 8 * kb;
+#pragma unroll
+    for (int s = 0; s < S; ++s) A[s] = gptq_order(x_to_f16<XDT>(*(const u32x4*)(xr + s * 32)));
+  }
+
+  // rolling window: block q's weights were requested D blocks earlier
+  GvBlock<S, SPG> buf[D];
+#pragma unroll
+  for (int d = 0; d < D; ++d)
+    if (d < ncb) gv_load<S, SPG, LAYOUT>(a, c, u0 + d, buf[d]);
+
+  for (int q0 = 0; q0 < ncb; q0 += D) {
+    f32x4 acc[D];
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+      acc[d] = f32x4{0.f, 0.f, 0.f, 0.f};
+      if (q0 + d < ncb) {
+        acc[d] = gv_compute<S, SPG>(a, nc, zsh, buf[d], A);
+        if (q0 + d + D < ncb) gv_load<S, SPG, LAYOUT>(a, c, u0 + q0 + d + D, buf[d]);
+      }
+    }
+    // fixed-order reduction of the 16 waves' partial sums (the next blocks'
+    // loads stay in flight across the barriers)
+#pragma unroll
+    for (int d = 0; d < D; ++d)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) red[wave][d * 4 + r][lane] = acc[d][r];
+    __syncthreads();
+    if (wave < D * 4) {
+      const int i = wave, d = i >> 2, r = i & 3;   // one output per thread
+      if (q0 + d < ncb) {
+        float v = red[0][i][lane];
+#pragma unroll
+        for (int w = 1; w < kGvWaves; ++w) v = __fadd_rn(v, red[w][i][lane]);
+        const int m = 4 * kb + r;
+        const int n = (u0 + q0 + d) * 16 + j;
+        if (m < a.M && n < a.N) {
+          if (a.bias_dtype != KQ_DTYPE_NONE) v = __fadd_rn(v, load_as_f32(a.bias, a.bias_dtype, n));
+          a.out[(int64_t)m * a.N + n] = f32_to_out(v, a.out_dtype);
+        }
+      }
+    }
+    __syncthreads();
+  }
+}
+
 // x16[m][j] = fp16(x[m][perm[j]]) (act-order gather + W4A16 activation
 // conversion); each thread writes 8 consecutive outputs with one 16-byte store.
 __global__ void __launch_bounds__(64)
@@ -456,6 +659,49 @@ w4a16_prep_x_kernel(const uint16_t* __restrict__ x, int dtype, int ldx,
     const int k = k0 + e;
     if (k < K) x16[(int64_t)m * K + k] = act_bits(row[perm[k]], dtype);
   }
+}
+
+// AWQ word (k, c) holds column 8c + [0,2,4,6,1,3,5,7][i] in nibble i, so
+// column offset o sits at nibble (o % 2) * 4 + o / 2 (kairyu/quant/awq.py:14-36).
+KQ_DEV uint32_t awq_shift(int o) { return 4u * (uint32_t)((o & 1) * 4 + (o >> 1)); }
+
+// Load-time tiling: out word (u, r, c) of [ceil(N/16)][K/8][16] holds
+// q[row(8r + e)][16u + c] in nibble e, with row(k) = perm[k] (act-order) or k;
+// columns past N are 0.  Source: GPTQ qweight [K/8][N] (LSB-first along k) or
+// AWQ qweight [K][N/8].
+__global__ void w4_tile_kernel(const uint32_t* __restrict__ src, int awq, const int32_t* __restrict__ perm,
+                               uint32_t* __restrict__ out, int N, int K) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int kw8 = K / 8;
+  const int units = (N + 15) / 16;
+  if (idx >= (int64_t)units * kw8 * 16) return;
+  const int c = (int)(idx & 15);
+  const int r = (int)((idx >> 4) % kw8);
+  const int u = (int)((idx >> 4) / kw8);
+  const int n = u * 16 + c;
+  uint32_t word = 0;
+  if (n < N) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int k = perm ? perm[8 * r + e] : 8 * r + e;
+      const uint32_t q = awq ? (src[(int64_t)k * (N / 8) + (n >> 3)] >> awq_shift(n & 7)) & 0xfu
+                             : (src[(int64_t)(k >> 3) * N + n] >> (4 * (k & 7))) & 0xfu;
+      word |= q << (4 * e);
+    }
+  }
+  out[idx] = word;
+}
+
+// AWQ zeros -> natural nibble order (column 8c + i in nibble i), values kept.
+__global__ void awq_natural_zeros_kernel(const uint32_t* __restrict__ qz, uint32_t* __restrict__ out,
+                                         int64_t words) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= words) return;
+  const uint32_t w = qz[idx];
+  uint32_t r = 0;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) r |= ((w >> awq_shift(i)) & 0xfu) << (4 * i);
+  out[idx] = r;
 }
 
 // Act-order repack: unpacked row j of the output = unpacked row perm[j].
@@ -505,11 +751,11 @@ template <int FMT, int GM, int XDT, bool PRED>
 static void launch_w4_mt(const W4Args& a, const W4Plan& p, hipStream_t stream) {
   dim3 grid(p.tiles * p.splits, p.mblocks);
   if (p.mt == 1)
-    hipLaunchKernelGGL((w4a16_skinny_kernel<FMT, 1, GM, XDT, PRED, 4>), grid, dim3(256), 0, stream, a);
+    hipLaunchKernelGGL((w4a16_skinny_kernel<FMT, 1, GM, XDT, PRED, 4, 4, false>), grid, dim3(256), 0, stream, a);
   else if (p.mt == 2)
-    hipLaunchKernelGGL((w4a16_skinny_kernel<FMT, 2, GM, XDT, PRED, 4>), grid, dim3(256), 0, stream, a);
+    hipLaunchKernelGGL((w4a16_skinny_kernel<FMT, 2, GM, XDT, PRED, 4, 4, false>), grid, dim3(256), 0, stream, a);
   else
-    hipLaunchKernelGGL((w4a16_skinny_kernel<FMT, 4, GM, XDT, PRED, 4>), grid, dim3(256), 0, stream, a);
+    hipLaunchKernelGGL((w4a16_skinny_kernel<FMT, 4, GM, XDT, PRED, 4, 4, false>), grid, dim3(256), 0, stream, a);
 }
 
 template <int FMT, int GM>
@@ -521,6 +767,81 @@ static void launch_w4(const W4Args& a, const W4Plan& p, int xdt, bool pred, hipS
     if (xdt == kXF16) launch_w4_mt<FMT, GM, kXF16, false>(a, p, stream);
     else launch_w4_mt<FMT, GM, kXBF16, false>(a, p, stream);
   }
+}
+
+static int device_cus() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) dev = 0;
+  const int slot = dev & 63;
+  if (cached[slot] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      n = 256;
+    cached[slot] = n;
+  }
+  return cached[slot];
+}
+
+// The decode GEMV covers M <= 16 with K in {1024, 2048, 4096} (16 waves x S
+// steps of 32), 16-byte aligned x rows, and group boundaries at fixed steps
+// of every wave window, when there are enough 16-column blocks to give every
+// CU work.  *S and *SPG receive the kernel's template values.
+static bool gv_plan(const W4Args& a, int fmt, int gmode, GvPlan* p, int* S, int* SPG) {
+  if (fmt != kGptq || a.M > 16 || gmode == kGroupsPerK) return false;
+  if (a.K % 512 != 0) return false;
+  const int s = a.K / 512;
+  if (s != 2 && s != 4 && s != 8) return false;
+  if (a.G % 32 != 0) return false;
+  const int spg = a.G / 32;
+  int tspg;
+  if (spg >= s) {
+    if (spg % s != 0) return false;
+    tspg = 8;  // one group per window
+  } else {
+    if (s % spg != 0) return false;
+    tspg = spg;
+  }
+  if (((uintptr_t)a.x % 16) != 0 || (a.ldx % 8) != 0) return false;
+  if ((uint64_t)(a.K / 8) * (uint64_t)((a.N + 15) / 16 * 16) * 4u >= ((uint64_t)1 << 31)) return false;
+  const int cus = device_cus();
+  p->units = (a.N + 15) / 16;
+  if (p->units * 2 < cus) return false;
+  p->wgs = std::min(cus, p->units);
+  *S = s;
+  *SPG = tspg;
+  return true;
+}
+
+template <int XDT, int S, int SPG>
+static void launch_gv_s(const W4Args& a, const GvPlan& p, int layout, hipStream_t st) {
+  if (layout == kLayoutTiles)
+    hipLaunchKernelGGL((w4a16_gemv_kernel<XDT, S, SPG, kLayoutTiles>), dim3(p.wgs), dim3(64 * kGvWaves), 0, st, a, p);
+  else
+    hipLaunchKernelGGL((w4a16_gemv_kernel<XDT, S, SPG, kLayoutRows>), dim3(p.wgs), dim3(64 * kGvWaves), 0, st, a, p);
+}
+
+template <int XDT, int S>
+static void launch_gv_spg(const W4Args& a, const GvPlan& p, int spg, int layout, hipStream_t st) {
+  switch (spg) {
+    case 1: launch_gv_s<XDT, S, 1>(a, p, layout, st); break;
+    case 2: launch_gv_s<XDT, S, 2>(a, p, layout, st); break;
+    case 4: launch_gv_s<XDT, S, 4>(a, p, layout, st); break;
+    default: launch_gv_s<XDT, S, 8>(a, p, layout, st); break;
+  }
+}
+
+template <int XDT>
+static void launch_gv_x(const W4Args& a, const GvPlan& p, int S, int spg, int layout, hipStream_t st) {
+  if (S == 2) launch_gv_spg<XDT, 2>(a, p, spg, layout, st);
+  else if (S == 4) launch_gv_spg<XDT, 4>(a, p, spg, layout, st);
+  else launch_gv_spg<XDT, 8>(a, p, spg, layout, st);
+}
+
+static void launch_gv(const W4Args& a, const GvPlan& p, int xdt, int S, int spg, int layout,
+                      hipStream_t st) {
+  if (xdt == kXF16) launch_gv_x<kXF16>(a, p, S, spg, layout, st);
+  else launch_gv_x<kXBF16>(a, p, S, spg, layout, st);
 }
 
 static int run_w4(const char* what, int fmt, W4Args a, int gmode, void* workspace,
@@ -546,6 +867,29 @@ static int run_w4(const char* what, int fmt, W4Args a, int gmode, void* workspac
   // floor(k / G) = (k * ceil(2^40 / G)) >> 40, exact for k < 2^24, G < 2^16
   a.gmagic = (((uint64_t)1 << 40) + (uint64_t)a.G - 1) / (uint64_t)a.G;
   const bool needs_x16 = gmode == kGroupsPermuted;
+  GvPlan gp{};
+  int gv_s = 0, gv_spg = 0;
+  if (gv_plan(a, fmt, gmode, &gp, &gv_s, &gv_spg)) {
+    int xdt = a.x_dtype == KQ_DTYPE_F16 ? kXF16 : kXBF16;
+    if (needs_x16) {
+      // act-order: gather x through the permutation once per call
+      const size_t x16_bytes = (size_t)a.M * a.K * 2;
+      if (workspace == nullptr || ws_bytes < x16_bytes) {
+        set_error("%s: workspace of %zu bytes is smaller than the %zu bytes this call needs", what,
+                  workspace ? ws_bytes : (size_t)0, x16_bytes);
+        return KQ_EWORKSPACE;
+      }
+      uint16_t* x16 = (uint16_t*)workspace;
+      const int64_t threads = ((int64_t)a.M * a.K + 7) / 8;
+      hipLaunchKernelGGL(w4a16_prep_x_kernel, dim3((unsigned)((threads + 63) / 64)), dim3(64), 0,
+                         stream, a.x, a.x_dtype, a.ldx, a.perm, a.M, a.K, x16);
+      a.x = x16;
+      a.ldx = a.K;
+      xdt = kXF16;
+    }
+    launch_gv(a, gp, xdt, gv_s, gv_spg, a.layout, stream);
+    return check_launch(what);
+  }
   W4Plan p = plan_w4(a.M, a.N, a.K, needs_x16, ws_bytes, workspace != nullptr);
   if (p.x16_bytes + p.partial_bytes > (workspace ? ws_bytes : 0)) {
     set_error("%s: workspace of %zu bytes is smaller than the %zu bytes this call needs", what,
@@ -611,7 +955,7 @@ extern "C" int kq_w4a16_awq_gemm(const void* x, int x_dtype, const int32_t* qwei
   a.x = (const uint16_t*)x; a.x_dtype = x_dtype; a.ldx = (int)k;
   a.qw = (const uint32_t*)qweight; a.qz = (const uint32_t*)qzeros; a.sc = (const uint16_t*)scales;
   a.bias = bias; a.bias_dtype = bias_dtype; a.out = (uint16_t*)out; a.out_dtype = x_dtype;
-  a.M = (int)m; a.N = (int)n; a.K = (int)k; a.G = group_size;
+  a.M = (int)m; a.N = (int)n; a.K = (int)k; a.G = group_size; a.zoff = 0u;
   // the fast path needs every aligned 8-row chunk inside one group
   const int gmode = (group_size % 8 == 0) ? kGroupsUniform : kGroupsPerK;
   return run_w4("kq_w4a16_awq_gemm", kAwq, a, gmode, workspace, workspace_bytes,
@@ -642,9 +986,64 @@ extern "C" int kq_w4a16_gptq_gemm(const void* x, int x_dtype, const int32_t* qwe
   a.qw = (const uint32_t*)qweight; a.qz = (const uint32_t*)qzeros; a.sc = (const uint16_t*)scales;
   a.gidx = g_idx; a.perm = perm;
   a.bias = bias; a.bias_dtype = bias_dtype; a.out = (uint16_t*)out; a.out_dtype = x_dtype;
-  a.M = (int)m; a.N = (int)n; a.K = (int)k; a.G = group_size;
+  a.M = (int)m; a.N = (int)n; a.K = (int)k; a.G = group_size; a.zoff = 1u;
   return run_w4("kq_w4a16_gptq_gemm", kGptq, a, gidx_mode, workspace, workspace_bytes,
                 (hipStream_t)stream);
+}
+
+extern "C" int kq_w4a16_tiled_gemm(const void* x, int x_dtype, const int32_t* tiles,
+                                   const int32_t* qzeros, int zero_offset, const void* scales,
+                                   const int32_t* perm, const void* bias, int bias_dtype, void* out,
+                                   int64_t m, int64_t n, int64_t k, int group_size, void* workspace,
+                                   size_t workspace_bytes, void* stream) {
+  if (m > 0x7fffffff || n > 0x7fffffff || k > 0x7fffffff) {
+    set_error("kq_w4a16_tiled_gemm: dimensions exceed int32");
+    return KQ_EINVAL;
+  }
+  if (k % 8 != 0 || group_size % 8 != 0 || (zero_offset != 0 && zero_offset != 1)) {
+    set_error("kq_w4a16_tiled_gemm: needs k %% 8 == 0, group_size %% 8 == 0, zero_offset 0 or 1");
+    return KQ_EINVAL;
+  }
+  if ((uint64_t)(k / 8) * (uint64_t)((n + 15) / 16 * 16) * 4u >= ((uint64_t)1 << 32)) {
+    set_error("kq_w4a16_tiled_gemm: tiled weight exceeds 4 GiB");
+    return KQ_EINVAL;
+  }
+  W4Args a{};
+  a.x = (const uint16_t*)x; a.x_dtype = x_dtype; a.ldx = (int)k;
+  a.qw = (const uint32_t*)tiles; a.qz = (const uint32_t*)qzeros; a.sc = (const uint16_t*)scales;
+  a.perm = perm;
+  a.bias = bias; a.bias_dtype = bias_dtype; a.out = (uint16_t*)out; a.out_dtype = x_dtype;
+  a.M = (int)m; a.N = (int)n; a.K = (int)k; a.G = group_size; a.zoff = (uint32_t)zero_offset;
+  a.layout = kLayoutTiles;
+  return run_w4("kq_w4a16_tiled_gemm", kGptq, a, perm ? kGroupsPermuted : kGroupsUniform,
+                workspace, workspace_bytes, (hipStream_t)stream);
+}
+
+extern "C" int kq_w4a16_tile_weights(const int32_t* qweight, int src_format, const int32_t* perm,
+                                     int32_t* tiles, int64_t n, int64_t k, void* stream) {
+  if (n < 8 || k < 8 || (n % 8) != 0 || (k % 8) != 0 || n > 0x7fffffff || k > 0x7fffffff ||
+      (src_format != 0 && src_format != 1)) {
+    set_error("kq_w4a16_tile_weights: bad arguments n=%lld k=%lld format=%d", (long long)n,
+              (long long)k, src_format);
+    return KQ_EINVAL;
+  }
+  const int64_t words = (n + 15) / 16 * 16 * (k / 8);
+  hipLaunchKernelGGL(w4_tile_kernel, dim3((unsigned)((words + 255) / 256)), dim3(256), 0,
+                     (hipStream_t)stream, (const uint32_t*)qweight, src_format == 0 ? 1 : 0, perm,
+                     (uint32_t*)tiles, (int)n, (int)k);
+  return check_launch("kq_w4a16_tile_weights");
+}
+
+extern "C" int kq_awq_natural_zeros(const int32_t* qzeros, int32_t* qzeros_n, int64_t n,
+                                    int64_t groups, void* stream) {
+  if (n < 8 || (n % 8) != 0 || groups < 1) {
+    set_error("kq_awq_natural_zeros: bad shape n=%lld groups=%lld", (long long)n, (long long)groups);
+    return KQ_EINVAL;
+  }
+  const int64_t words = groups * (n / 8);
+  hipLaunchKernelGGL(awq_natural_zeros_kernel, dim3((unsigned)((words + 255) / 256)), dim3(256), 0,
+                     (hipStream_t)stream, (const uint32_t*)qzeros, (uint32_t*)qzeros_n, words);
+  return check_launch("kq_awq_natural_zeros");
 }
 
 extern "C" int kq_gptq_permute_qweight(const int32_t* qweight, const int32_t* perm, int32_t* out,

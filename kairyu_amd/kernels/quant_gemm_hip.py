@@ -254,30 +254,82 @@ GIDX_PERMUTED = 1
 GIDX_PER_K = 2
 
 
+def _tile(qweight: torch.Tensor, src_format: int, perm: torch.Tensor | None, n: int, k: int,
+          device: torch.device) -> torch.Tensor:
+    tiles = torch.empty(((n + 15) // 16, k // 8, 16), dtype=torch.int32, device=device)
+    _native.call(
+        "kq_w4a16_tile_weights", qweight.data_ptr(), src_format, _native.ptr(perm),
+        tiles.data_ptr(), n, k, _native.stream_handle(device),
+    )
+    return tiles
+
+
+def _awq_operands(module, device: torch.device):
+    """(tiles, natural-order qzeros) of an AWQ module, or None.
+
+    The W4A16 kernels stream 16-column tiles of K-packed words
+    (``kq_w4a16_tile_weights``); shapes with ``k % 8 == 0`` and
+    ``group_size % 8 == 0`` get that derived, non-persistent copy (plus the
+    zeros in natural nibble order), rebuilt when a source tensor's version
+    changes.  Checkpoint buffers stay untouched, as for the reference's derived
+    operands (quant_gemm_gpu.py:802-850).  Other shapes run on the checkpoint
+    layout.
+    """
+
+    qweight, qzeros = module.qweight, module.qzeros
+    k, n, group = module.in_features, module.out_features, module.group_size
+    if k % 8 != 0 or group % 8 != 0:
+        return None
+    key = (id(qweight), qweight._version, id(qzeros), qzeros._version, str(device))
+    cached = module.__dict__.get("_kq_awq_operands")
+    if cached is not None and cached[0] == key:
+        return cached[1]
+    tiles = _tile(qweight, 0, None, n, k, device)
+    qzeros_n = torch.empty_like(qzeros)
+    _native.call(
+        "kq_awq_natural_zeros", qzeros.data_ptr(), qzeros_n.data_ptr(), n, qzeros.shape[0],
+        _native.stream_handle(device),
+    )
+    result = (tiles, qzeros_n)
+    object.__setattr__(module, "_kq_awq_operands", (key, result))
+    return result
+
+
 def awq_linear_forward(x: torch.Tensor, module, *, add_bias: bool = True) -> torch.Tensor:
     flat, out = _prepare(x, module, "awq")
     bias = _bias(module, add_bias)
     m, k = flat.shape
     ws = _w4_workspace(x.device, m, module.out_features, k, GIDX_UNIFORM)
-    _native.call(
-        "kq_w4a16_awq_gemm",
-        flat.data_ptr(), _native.dtype_code(flat.dtype), module.qweight.data_ptr(),
-        module.qzeros.data_ptr(), module.scales.data_ptr(), _native.ptr(bias),
-        _native.dtype_code(None if bias is None else bias.dtype), out.data_ptr(), m,
-        module.out_features, k, module.group_size, ws.data_ptr(), ws.numel(),
+    tiled = _awq_operands(module, x.device)
+    common = (
+        _native.ptr(bias), _native.dtype_code(None if bias is None else bias.dtype),
+        out.data_ptr(), m, module.out_features, k, module.group_size, ws.data_ptr(), ws.numel(),
         _native.stream_handle(x.device),
     )
+    if tiled is not None:
+        _native.call(
+            "kq_w4a16_tiled_gemm",
+            flat.data_ptr(), _native.dtype_code(flat.dtype), tiled[0].data_ptr(),
+            tiled[1].data_ptr(), 0, module.scales.data_ptr(), None, *common,
+        )
+    else:
+        _native.call(
+            "kq_w4a16_awq_gemm",
+            flat.data_ptr(), _native.dtype_code(flat.dtype), module.qweight.data_ptr(),
+            module.qzeros.data_ptr(), module.scales.data_ptr(), *common,
+        )
     return out.reshape(*x.shape[:-1], module.out_features)
 
 
 def _gptq_operands(module, device: torch.device):
-    """(gidx_mode, qweight operand, perm or None) for a GPTQ module.
+    """(gidx_mode, weight operand, perm or None) for a GPTQ module.
 
-    ``g_idx == k // group_size`` runs on the checkpoint buffers directly.  An
-    act-order ``g_idx`` whose stable sort groups every ``group_size`` rows
-    together gets a K-permuted copy of ``qweight`` (derived, non-persistent,
-    rebuilt when a source tensor's version changes) and gathers ``x`` through
-    the permutation; any other ``g_idx`` uses the per-element group path.
+    ``g_idx == k // group_size`` and an act-order ``g_idx`` whose stable sort
+    groups every ``group_size`` rows together run on a derived, non-persistent
+    tiled copy of ``qweight`` (``kq_w4a16_tile_weights``; for act-order the
+    rows are K-permuted by that sort and ``x`` is gathered through it), rebuilt
+    when a source tensor's version changes.  Any other ``g_idx`` uses the
+    per-element group path on the checkpoint buffers.
     """
 
     g_idx, qweight = module.g_idx, module.qweight
@@ -285,44 +337,47 @@ def _gptq_operands(module, device: torch.device):
     cached = module.__dict__.get("_kq_gptq_operands")
     if cached is not None and cached[0] == key:
         return cached[1]
-    k, group = module.in_features, module.group_size
+    k, n, group = module.in_features, module.out_features, module.group_size
     natural = torch.arange(k, device=device, dtype=torch.int64) // group
     gi = g_idx.to(torch.int64)
-    if torch.equal(gi, natural):
-        result = (GIDX_UNIFORM, qweight, None)
-    else:
-        perm = torch.argsort(gi, stable=True)
-        if group % 8 == 0 and torch.equal(gi[perm], natural):
-            perm32 = perm.to(torch.int32).contiguous()
-            permuted = torch.empty_like(qweight)
-            _native.call(
-                "kq_gptq_permute_qweight",
-                qweight.data_ptr(), perm32.data_ptr(), permuted.data_ptr(),
-                module.out_features, k, _native.stream_handle(device),
-            )
-            result = (GIDX_PERMUTED, permuted, perm32)
+    result = (GIDX_PER_K, qweight, None)
+    if group % 8 == 0:
+        if torch.equal(gi, natural):
+            result = (GIDX_UNIFORM, _tile(qweight, 1, None, n, k, device), None)
         else:
-            result = (GIDX_PER_K, qweight, None)
+            perm = torch.argsort(gi, stable=True)
+            if torch.equal(gi[perm], natural):
+                perm32 = perm.to(torch.int32).contiguous()
+                result = (GIDX_PERMUTED, _tile(qweight, 1, perm32, n, k, device), perm32)
     object.__setattr__(module, "_kq_gptq_operands", (key, result))
     return result
 
 
 def gptq_linear_forward(x: torch.Tensor, module, *, add_bias: bool = True) -> torch.Tensor:
     flat, out = _prepare(x, module, "gptq")
-    mode, qweight, perm = _gptq_operands(module, x.device)
-    g_idx = module.g_idx if module.g_idx.dtype == torch.int32 else module.g_idx.to(torch.int32)
+    mode, weight, perm = _gptq_operands(module, x.device)
     bias = _bias(module, add_bias)
     m, k = flat.shape
     ws = _w4_workspace(x.device, m, module.out_features, k, mode)
-    _native.call(
-        "kq_w4a16_gptq_gemm",
-        flat.data_ptr(), _native.dtype_code(flat.dtype), qweight.data_ptr(),
-        module.qzeros.data_ptr(), module.scales.data_ptr(), g_idx.data_ptr(),
-        _native.ptr(perm), mode, _native.ptr(bias),
-        _native.dtype_code(None if bias is None else bias.dtype), out.data_ptr(), m,
-        module.out_features, k, module.group_size, ws.data_ptr(), ws.numel(),
+    common = (
+        _native.ptr(bias), _native.dtype_code(None if bias is None else bias.dtype),
+        out.data_ptr(), m, module.out_features, k, module.group_size, ws.data_ptr(), ws.numel(),
         _native.stream_handle(x.device),
     )
+    if mode in (GIDX_UNIFORM, GIDX_PERMUTED):
+        _native.call(
+            "kq_w4a16_tiled_gemm",
+            flat.data_ptr(), _native.dtype_code(flat.dtype), weight.data_ptr(),
+            module.qzeros.data_ptr(), 1, module.scales.data_ptr(), _native.ptr(perm), *common,
+        )
+    else:
+        g_idx = module.g_idx if module.g_idx.dtype == torch.int32 else module.g_idx.to(torch.int32)
+        _native.call(
+            "kq_w4a16_gptq_gemm",
+            flat.data_ptr(), _native.dtype_code(flat.dtype), weight.data_ptr(),
+            module.qzeros.data_ptr(), module.scales.data_ptr(), g_idx.data_ptr(), None, mode,
+            *common,
+        )
     return out.reshape(*x.shape[:-1], module.out_features)
 
 

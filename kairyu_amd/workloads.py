@@ -136,5 +136,6 @@ def replicas(workload: Workload, copies: int) -> list[torch.nn.Module]:
         clone._parameters = dict(workload.module._parameters)
         clone._modules = dict(workload.module._modules)
         clone.__dict__.pop("_kq_gptq_operands", None)
+        clone.__dict__.pop("_kq_awq_operands", None)
         mods.append(clone)
     return mods

@@ -225,3 +225,110 @@ def test_graph_replays_match_eager(cuda):
         assert torch.equal(og, eager[1]), step
         gptq(x * 2)
         torch.cuda.synchronize()
+
+
+# Decode GEMV (M <= 16, >= 128 column blocks of 16, group_size % 32 == 0):
+# K tails, per-step / per-window groups, partial last column block, several
+# K chunks per wave, several column blocks per workgroup, act-order gather.
+_GEMV_CASES = [
+    # (fmt, m, k, n, group, dtype, act_order, bias)
+    ("gptq", 1, 4096, 2048, 128, torch.float16, False, True),
+    ("gptq", 16, 4096, 2048, 128, torch.bfloat16, False, False),
+    ("gptq", 7, 4128, 2056, 128, torch.float16, False, True),     # K % 128 != 0, N % 16 == 8
+    ("gptq", 5, 2056, 2048, 32, torch.float16, False, True),      # K % 32 == 8 (tail step)
+    ("gptq", 16, 2048, 2064, 64, torch.bfloat16, False, True),    # two steps per group
+    ("gptq", 3, 1024, 2048, 1024, torch.float16, False, False),   # one group (per channel)
+    ("gptq", 16, 16384, 2048, 128, torch.float16, False, True),   # several K chunks
+    ("gptq", 16, 512, 28672, 128, torch.float16, True, True),     # 7 blocks per CU, act-order
+    ("gptq", 4, 4096, 4096, 128, torch.bfloat16, True, False),    # act-order, bf16
+    ("awq", 1, 4096, 4096, 128, torch.float16, False, True),
+    ("awq", 16, 4096, 2048, 64, torch.bfloat16, False, True),
+    ("awq", 9, 2080, 2056, 32, torch.float16, False, False),
+]
+
+
+@pytest.mark.parametrize("case", _GEMV_CASES, ids=lambda c: "-".join(map(str, c[:5])) + ("-ao" if c[6] else ""))
+def test_decode_gemv_matches_oracle(cuda, case):
+    fmt, m, k, n, group, dtype, act_order, bias = case
+    banner(f"gemv {case}")
+    seed = m * 131 + k + n
+    if fmt == "awq":
+        module = _awq_module(k, n, group=group, seed=seed, bias=bias, random_packed=True)
+    else:
+        g_idx = None
+        if act_order:
+            g_idx = (torch.randperm(k, generator=torch.Generator().manual_seed(seed)) // group).to(torch.int32)
+        module = _gptq_module(k, n, group=group, seed=seed, bias=bias, g_idx=g_idx, random_packed=True)
+        if g_idx is not None:
+            module.g_idx.copy_(g_idx)
+    module = module.to(cuda)
+    x = torch.randn(m, k, generator=torch.Generator().manual_seed(seed + 1)).to(dtype)
+    out = module(x.to(cuda))
+    if fmt == "gptq":
+        assert module._kq_gptq_operands[1][0] == (hip.GIDX_PERMUTED if act_order else hip.GIDX_UNIFORM)
+    else:
+        assert module._kq_awq_operands is not None
+    assert_close_fp(np32(out), _oracle(module, x), label=str(case))
+
+
+def _untile(tiles: torch.Tensor, n: int) -> torch.Tensor:
+    """[U][K/8][16] tiles -> int [K, N] nibbles (test-side inverse of the tiling)."""
+    units, kw8, _ = tiles.shape
+    q = gptq_format.unpack_gptq_rows(tiles.cpu().permute(1, 0, 2).reshape(kw8, units * 16))
+    return q[:, :n]
+
+
+def test_tiled_operands_are_exact_and_follow_updates(cuda):
+    module = _awq_module(256, 72, group=32, seed=11, random_packed=True).to(cuda)
+    tiles, qz = hip._awq_operands(module, torch.device(cuda))
+    assert tiles.shape == (5, 32, 16)
+    assert torch.equal(_untile(tiles, 72), awq_format.unpack_awq(module.qweight.cpu()))
+    assert torch.equal(gptq_format.unpack_gptq_cols(qz.cpu()), awq_format.unpack_awq(module.qzeros.cpu()))
+    assert int(tiles[4, :, 8:].abs().sum()) == 0  # columns past N
+    module.qweight.copy_(awq_format.pack_awq(torch.randint(0, 16, (256, 72))).to(cuda))
+    tiles2, _ = hip._awq_operands(module, torch.device(cuda))
+    assert torch.equal(_untile(tiles2, 72), awq_format.unpack_awq(module.qweight.cpu()))
+    # GPTQ act-order: tile rows follow the stable sort of g_idx
+    g_idx = (torch.randperm(256, generator=torch.Generator().manual_seed(3)) // 32).to(torch.int32)
+    gmod = _gptq_module(256, 64, group=32, seed=12, g_idx=g_idx, random_packed=True)
+    gmod.g_idx.copy_(g_idx)
+    gmod = gmod.to(cuda)
+    mode, tiles, perm = hip._gptq_operands(gmod, torch.device(cuda))
+    assert mode == hip.GIDX_PERMUTED
+    q = gptq_format.unpack_gptq_rows(gmod.qweight.cpu())
+    assert torch.equal(_untile(tiles, 64), q[perm.cpu().long()])
+
+
+def test_checkpoint_layout_entry_points(cuda):
+    """The C ABI's checkpoint-layout GEMMs (no derived operands) stay exact."""
+    from kairyu_amd import _native
+
+    m, k, n, group = 5, 512, 2048, 64
+    awq = _awq_module(k, n, group=group, seed=21, random_packed=True).to(cuda)
+    g_idx = (torch.randperm(k, generator=torch.Generator().manual_seed(22)) // group).to(torch.int32)
+    gptq = _gptq_module(k, n, group=group, seed=23, g_idx=g_idx, random_packed=True)
+    gptq.g_idx.copy_(g_idx)
+    gptq = gptq.to(cuda)
+    x = torch.randn(m, k, generator=torch.Generator().manual_seed(24)).to(torch.float16)
+    xd = x.to(cuda)
+    ws = torch.empty(1 << 24, dtype=torch.uint8, device=cuda)
+    stream = torch.cuda.current_stream().cuda_stream
+    out = torch.empty(m, n, dtype=torch.float16, device=cuda)
+    _native.call("kq_w4a16_awq_gemm", xd.data_ptr(), 0, awq.qweight.data_ptr(), awq.qzeros.data_ptr(),
+                 awq.scales.data_ptr(), awq.bias.data_ptr(), 2, out.data_ptr(), m, n, k, group,
+                 ws.data_ptr(), ws.numel(), stream)
+    assert_close_fp(np32(out), _oracle(awq, x), label="awq checkpoint")
+    perm = torch.argsort(g_idx.long(), stable=True).to(torch.int32).to(cuda)
+    permuted = torch.empty_like(gptq.qweight)
+    _native.call("kq_gptq_permute_qweight", gptq.qweight.data_ptr(), perm.data_ptr(),
+                 permuted.data_ptr(), n, k, stream)
+    _native.call("kq_w4a16_gptq_gemm", xd.data_ptr(), 0, permuted.data_ptr(), gptq.qzeros.data_ptr(),
+                 gptq.scales.data_ptr(), gptq.g_idx.data_ptr(), perm.data_ptr(), 1,
+                 gptq.bias.data_ptr(), 2, out.data_ptr(), m, n, k, group, ws.data_ptr(), ws.numel(),
+                 stream)
+    assert_close_fp(np32(out), _oracle(gptq, x), label="gptq permuted checkpoint")
+    _native.call("kq_w4a16_gptq_gemm", xd.data_ptr(), 0, gptq.qweight.data_ptr(), gptq.qzeros.data_ptr(),
+                 gptq.scales.data_ptr(), gptq.g_idx.data_ptr(), None, 2,
+                 gptq.bias.data_ptr(), 2, out.data_ptr(), m, n, k, group, ws.data_ptr(), ws.numel(),
+                 stream)
+    assert_close_fp(np32(out), _oracle(gptq, x), label="gptq per-k checkpoint")
