@@ -7,6 +7,10 @@ batch; weights rotate over enough distinct HBM copies (> 256 MB MALL) that no
 step is served from the Infinity Cache.  Steps are captured in a HIP graph and
 timed with HIP events on the stream they run on.
 
+``roofline`` describes the dominant kernel alone: the decode GEMV's
+algorithmic bytes per launch over its per-launch time, timed live with HIP
+events on its own captured launches (x gathered once up front).
+
 ``sweep`` reports every BASELINE configuration (C1-C4 over their M values, C5
 when built) with GB/s or TFLOPS and roofline fractions.  ``cpu_baseline``
 times the repo's CPU oracle (a numpy port of the reference's dequantize-then-
@@ -37,6 +41,97 @@ def _weight_bytes(module) -> int:
     return sum(t.numel() * t.element_size() for t in module.buffers(recurse=False))
 
 
+def clock_warmup(seconds: float = 1.0) -> None:
+    """Run dense GEMMs for about `seconds` so clocks and power state settle
+    before the first timed region."""
+
+    import torch
+
+    a = torch.randn(8192, 8192, device="cuda", dtype=torch.float16)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        for _ in range(8):
+            a = (a @ a).clamp_(-1.0, 1.0)
+        torch.cuda.synchronize()
+    del a
+
+
+def _timed_replays(graph, steps: int, repeats: int = 3) -> float:
+    """Median over `repeats` timed replays of ms per captured step (HIP events
+    on the replaying stream; one untimed replay first)."""
+
+    import torch
+
+    graph.replay()
+    torch.cuda.synchronize()
+    times = []
+    for _ in range(repeats):
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        graph.replay()
+        end.record()
+        torch.cuda.synchronize()
+        times.append(start.elapsed_time(end) / steps)
+    return sorted(times)[len(times) // 2]
+
+
+def measure_headline_kernel(workload, steps: int) -> dict:
+    """Live per-launch time of the headline's dominant kernel (the W4A16
+    decode GEMV) alone: the act-order gather is done once up front and each
+    captured step is one kq_w4a16_tiled_gemm launch on the gathered fp16 x,
+    rotating over the same weight copies as the whole-op measurement."""
+
+    import torch
+
+    from kairyu_amd import _native, workloads
+    from kairyu_amd.kernels import quant_gemm_hip as hip
+
+    module = workload.module
+    copies = max(1, math.ceil(1.25 * MALL_BYTES / max(1, _weight_bytes(module))))
+    copies = min(copies, 64)
+    mods = workloads.replicas(workload, copies)
+    device = workload.x.device
+    m, k = workload.x.shape
+    n, group = module.out_features, module.group_size
+    operands = [hip._gptq_operands(mod, device) for mod in mods]
+    mode, _, perm = operands[0]
+    x16 = workload.x[:, perm.long()].contiguous() if mode == hip.GIDX_PERMUTED else workload.x
+    out = torch.empty((m, n), device=device, dtype=torch.float16)
+    ws = _native.workspace(device)
+
+    def launch(i):
+        _, tiles, _ = operands[i % copies]
+        mod = mods[i % copies]
+        _native.call(
+            "kq_w4a16_tiled_gemm", x16.data_ptr(), _native.DTYPE_F16, tiles.data_ptr(),
+            mod.qzeros.data_ptr(), 1, mod.scales.data_ptr(), None, None, _native.DTYPE_NONE,
+            out.data_ptr(), m, n, k, group, ws.data_ptr(), ws.numel(),
+            _native.stream_handle(device),
+        )
+
+    for i in range(copies):
+        launch(i)
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for i in range(copies):
+            launch(i)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for i in range(steps):
+            launch(i)
+    ms = _timed_replays(graph, steps)
+    del graph
+    # bytes one launch reads and writes: packed weights, zeros, scales, x16, out
+    groups = -(-k // group)
+    nbytes = k * n // 2 + groups * (n // 8) * 4 + groups * n * 2 + m * k * 2 + m * n * 2
+    return {"ms": ms, "bytes": nbytes, "gbps": nbytes / (ms * 1e-3) / 1e9}
+
+
 def measure(workload, steps: int, warmup: int) -> dict:
     import torch
 
@@ -60,15 +155,7 @@ def measure(workload, steps: int, warmup: int) -> dict:
     with torch.cuda.graph(graph):
         for i in range(steps):
             mods[i % copies](x)
-    graph.replay()  # untimed replay: first-touch of graph resources
-    torch.cuda.synchronize()
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    start.record()
-    graph.replay()
-    end.record()
-    torch.cuda.synchronize()
-    ms = start.elapsed_time(end) / steps
+    ms = _timed_replays(graph, steps)
     del graph
     gbps = workload.bytes / (ms * 1e-3) / 1e9
     tflops = workload.flops / (ms * 1e-3) / 1e12
@@ -166,6 +253,8 @@ def main() -> int:
     parser.add_argument("--no-sweep", action="store_true")
     parser.add_argument("--no-cpu", action="store_true")
     parser.add_argument("--only", default=None, help="substring filter for sweep entries")
+    parser.add_argument("--copy-calibration", action="store_true",
+                        help="only run 256 MiB device-to-device copies (HBM counter calibration)")
     args = parser.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one MI355X; --gpus {args.gpus} is not supported "
@@ -178,12 +267,26 @@ def main() -> int:
 
     baseline = json.loads((ROOT / "BASELINE.json").read_text())
     torch.cuda.set_device(0)
+    if args.copy_calibration:
+        # a plain copy of known size: FETCH_SIZE / WRITE_SIZE per dispatch of
+        # this kernel calibrate the counters against 268435456 bytes each way
+        src = torch.ones(256 << 20, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes": src.numel(), "copies": 5}), flush=True)
+        return 0
 
+    clock_warmup()
     headline_wl = W.gptq_layer(m=16)
     print(f"[bench] headline {headline_wl.name}", file=sys.stderr, flush=True)
     head = measure(headline_wl, args.steps, args.warmup)
     head_summary = summarize("C2 GPTQ act-order W4A16 N=28672 K=4096 g128 M=16", "fp16",
                              headline_wl, head)
+    kernel = measure_headline_kernel(headline_wl, args.steps)
+    print(f"[bench] headline {head['ms'] * 1e3:.2f} us per op, decode GEMV "
+          f"{kernel['ms'] * 1e3:.2f} us per launch", file=sys.stderr, flush=True)
     del headline_wl
     torch.cuda.empty_cache()
 
@@ -207,10 +310,9 @@ def main() -> int:
         traffic = json.loads(traffic_file.read_text()).get(head_summary["workload"])
 
     cpu = None if args.no_cpu else cpu_baseline()
-    achieved = head["gbps"]
     line = {
         "metric": baseline["metric"],
-        "value": round(achieved, 1),
+        "value": round(head["gbps"], 1),
         "unit": "GB/s",
         "n_gpus": 1,
         "steps": args.steps,
@@ -228,11 +330,14 @@ def main() -> int:
         },
         "roofline": {
             "bound": "hbm",
-            "achieved": round(achieved, 1),
+            "kernel": "w4a16_gemv_kernel (kq_w4a16_tiled_gemm, M=16 decode GEMV)",
+            "achieved": round(kernel["gbps"], 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "frac": round(kernel["gbps"] / HBM_PEAK_GBS, 4),
             "traffic": traffic,
+            "bytes_per_launch": kernel["bytes"],
+            "us_per_launch": round(kernel["ms"] * 1e3, 3),
         },
         "cpu_baseline": cpu,
         "sweep": sweep,
