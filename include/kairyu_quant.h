@@ -167,6 +167,56 @@ size_t kq_w4a16_workspace_size(int64_t m, int64_t n, int64_t k, int gidx_mode);
 int kq_gptq_permute_qweight(const int32_t* qweight, const int32_t* perm, int32_t* out,
                             int64_t n, int64_t k, void* stream);
 
+/* ------------------------------------------------ block-FP8 and MoE experts
+ * Block FP8: weight e4m3 [n, k] with fp32 weight_scale_inv [ceil(n/128),
+ * ceil(k/128)], W = q * S[n/128][k/128]; activations quantized per token per
+ * 128-wide K block, s = max(amax, 1e-12) / 448, q = e4m3(clamp(x / s, +-448))
+ * (the finegrained_fp8_linear(..., block_size=[128, 128]) convention the
+ * reference calls at kairyu/kernels/deepseek_v4_moe_gpu.py:60-74). */
+
+/* Per token, per 128-wide block quantization of x [rows, k] (fp16/bf16):
+ * xq e4m3 [rows, k], xs fp32 [rows, ceil(k/128)].  Replaces the activation
+ * side of finegrained_fp8_linear (deepseek_v4_moe_gpu.py:60-74). */
+int kq_act_quant_fp8_blocks(const void* x, int x_dtype, int64_t rows, int64_t k, int64_t ldx,
+                            uint8_t* xq, float* xs, void* stream);
+
+/* Dense block-FP8 linear: out[m, n] = sum over 128-wide K blocks b of
+ * (xq . w) * xs[m][b] * ws[n/128][b] (fp32) + bias, cast to out_dtype;
+ * k % 128 == 0.  Replaces finegrained_fp8_linear (deepseek_v4_moe_gpu.py:60-74)
+ * for BlockFp8Linear. */
+int kq_block_fp8_gemm(const uint8_t* xq, const float* xs, const uint8_t* w, const float* ws,
+                      const void* bias, int bias_dtype, void* out, int out_dtype, int64_t m,
+                      int64_t n, int64_t k, void* stream);
+
+/* Qwen3 routing of logits [tokens, experts] (fp16/bf16/fp32; experts <= 512,
+ * top_k <= 32): stable descending top-k (ties -> smaller expert id) into
+ * topk_idx int32 [tokens, top_k]; topk_w fp32 = softmax of the selected
+ * logits (norm_topk_prob != 0) or the full softmax gathered at the
+ * selection.  Replaces route_experts' Qwen3 branch (kairyu/models/moe.py:255-273). */
+int kq_moe_route_topk(const void* logits, int dtype, int64_t tokens, int64_t experts, int top_k,
+                      int norm_topk_prob, int32_t* topk_idx, float* topk_w, void* stream);
+
+/* Bytes of workspace kq_moe_block_fp8_experts needs for this shape. */
+size_t kq_moe_workspace_size(int64_t tokens, int64_t hidden, int64_t inter, int64_t experts,
+                             int top_k);
+
+/* Routed block-FP8 SwiGLU experts + combine: for token t and slot s with
+ * expert e = topk_idx[t, s], y = down_e(bf16(silu(gate_e(x_t))) * up_e(x_t))
+ * (each projection a block-FP8 linear rounded to the hidden dtype); out[t] =
+ * sum over s in slot order of fp32(y) * topk_w[t, s], one final cast.
+ * w13 e4m3 [experts, 2*inter, hidden] (gate rows then up rows), s13 fp32
+ * [experts, 2*inter/128, hidden/128]; w2 e4m3 [experts, hidden, inter], s2
+ * fp32 [experts, hidden/128, inter/128]; hidden, inter multiples of 128.
+ * Device-side stable sort by expert, grouped GEMMs, no host synchronization.
+ * Replaces _mix_experts / GroupedExpertPack.forward / the EP slot-order
+ * combine (kairyu/models/moe.py:86-119, grouped_moe.py:239-330,
+ * moe_parallel.py:255-283) for block-FP8 experts. */
+int kq_moe_block_fp8_experts(const void* hidden, int dtype, int64_t tokens, int64_t hidden_size,
+                             int64_t inter, int64_t experts, int top_k, const int32_t* topk_idx,
+                             const float* topk_w, const uint8_t* w13, const float* s13,
+                             const uint8_t* w2, const float* s2, void* out, void* workspace,
+                             size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

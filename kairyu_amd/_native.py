@@ -58,6 +58,13 @@ _SIGNATURES: dict[str, list] = {
         _P, _I, _P, _P, _I, _P, _P, _P, _I, _P, _I64, _I64, _I64, _I, _P, _SZ, _P,
     ],
     "kq_w4a16_workspace_size": [_I64, _I64, _I64, _I],
+    "kq_moe_route_topk": [_P, _I, _I64, _I64, _I, _I, _P, _P, _P],
+    "kq_act_quant_fp8_blocks": [_P, _I, _I64, _I64, _I64, _P, _P, _P],
+    "kq_block_fp8_gemm": [_P, _P, _P, _P, _P, _I, _P, _I, _I64, _I64, _I64, _P],
+    "kq_moe_workspace_size": [_I64, _I64, _I64, _I64, _I],
+    "kq_moe_block_fp8_experts": [
+        _P, _I, _I64, _I64, _I64, _I64, _I, _P, _P, _P, _P, _P, _P, _P, _P, _SZ, _P,
+    ],
 }
 
 _lock = threading.Lock()
@@ -83,7 +90,8 @@ def _load() -> ctypes.CDLL:
             fn = getattr(lib, name)
             fn.argtypes = argtypes
             fn.restype = {"kq_last_error": ctypes.c_char_p,
-                          "kq_w4a16_workspace_size": ctypes.c_size_t}.get(name, ctypes.c_int)
+                          "kq_w4a16_workspace_size": ctypes.c_size_t,
+                          "kq_moe_workspace_size": ctypes.c_size_t}.get(name, ctypes.c_int)
         _lib = lib
         return lib
 

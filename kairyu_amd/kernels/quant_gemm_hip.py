@@ -381,12 +381,38 @@ def gptq_linear_forward(x: torch.Tensor, module, *, add_bias: bool = True) -> to
     return out.reshape(*x.shape[:-1], module.out_features)
 
 
-def block_fp8_linear_forward(x: torch.Tensor, module, *, add_bias: bool = True) -> torch.Tensor:
-    flat, out = _prepare(x, module, "fp8_block")
-    from kairyu_amd import moe
+def quantize_activation_blocks(flat: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """Per token per 128-wide K block e4m3 quantization of ``flat [M, K]``:
+    (e4m3 ``[M, K]``, fp32 ``[M, ceil(K/128)]``), ``s = max(amax, 1e-12)/448``."""
 
-    result = moe.block_fp8_dense_forward(flat, module, add_bias=add_bias, out=out)
-    return result.reshape(*x.shape[:-1], module.out_features)
+    rows, k = flat.shape
+    quantized = torch.empty((rows, k), device=flat.device, dtype=torch.float8_e4m3fn)
+    scales = torch.empty((rows, -(-k // 128)), device=flat.device, dtype=torch.float32)
+    _native.call(
+        "kq_act_quant_fp8_blocks", flat.data_ptr(), _native.dtype_code(flat.dtype), rows, k,
+        flat.stride(0), quantized.data_ptr(), scales.data_ptr(), _native.stream_handle(flat.device),
+    )
+    return quantized, scales
+
+
+def block_fp8_linear_forward(x: torch.Tensor, module, *, add_bias: bool = True) -> torch.Tensor:
+    """128x128 block-scaled FP8 linear: dynamic 1x128 activation blocks, e4m3
+    MFMA per block scaled by ``s_x * s_w`` in fp32, output in ``x.dtype``."""
+
+    flat, out = _prepare(x, module, "fp8_block")
+    m, k = flat.shape
+    if k % 128 != 0:
+        raise ValueError(f"block FP8 kernel needs in_features % 128 == 0, got {k}")
+    bias = _bias(module, add_bias)
+    x_q, x_scale = quantize_activation_blocks(flat)
+    scale_inv = _f32(module.weight_scale_inv)
+    _native.call(
+        "kq_block_fp8_gemm", x_q.data_ptr(), x_scale.data_ptr(), module.weight.data_ptr(),
+        scale_inv.data_ptr(), _native.ptr(bias),
+        _native.dtype_code(None if bias is None else bias.dtype), out.data_ptr(),
+        _native.dtype_code(out.dtype), m, module.out_features, k, _native.stream_handle(x.device),
+    )
+    return out.reshape(*x.shape[:-1], module.out_features)
 
 
 _DISPATCH = {

@@ -34,7 +34,7 @@ def quantize_block_fp8(weight: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor
     *lead, out_features, in_features = weight.shape
     ob, ib = _blocks(out_features), _blocks(in_features)
     w = weight.to(torch.float32)
-    padded = torch.zeros(*lead, ob * BLOCK, ib * BLOCK, dtype=torch.float32)
+    padded = torch.zeros(*lead, ob * BLOCK, ib * BLOCK, dtype=torch.float32, device=weight.device)
     padded[..., :out_features, :in_features] = w
     tiles = padded.reshape(*lead, ob, BLOCK, ib, BLOCK)
     amax = tiles.abs().amax(dim=(-3, -1))  # [..., ob, ib]

@@ -139,3 +139,56 @@ def replicas(workload: Workload, copies: int) -> list[torch.nn.Module]:
         clone.__dict__.pop("_kq_awq_operands", None)
         mods.append(clone)
     return mods
+
+
+class MoeFromLogits(torch.nn.Module):
+    """C5 step on given router logits (the router GEMM is excluded): Qwen3
+    top-k routing, then the block-FP8 experts with the fp32 slot-order
+    combine."""
+
+    def __init__(self, w13, s13, w2, s2, logits, top_k: int, norm_topk_prob: bool = True):
+        super().__init__()
+        self.top_k = top_k
+        self.norm_topk_prob = norm_topk_prob
+        for name, t in (("w13", w13), ("s13", s13), ("w2", w2), ("s2", s2), ("logits", logits)):
+            self.register_buffer(name, t)
+
+    def forward(self, hidden: torch.Tensor) -> torch.Tensor:
+        from kairyu_amd import moe
+
+        indices, weights = moe._route(self.logits, self.top_k, self.norm_topk_prob)
+        pack = moe.GroupedBlockFp8Experts.from_tensors(self.w13, self.s13, self.w2, self.s2)
+        return pack.forward(hidden, indices, weights)
+
+
+def moe_layer(tokens: int = 4096, hidden: int = 2048, inter: int = 768, experts: int = 128,
+              top_k: int = 8, seed: int = 0, device="cuda", norm_topk_prob: bool = True,
+              x_dtype=torch.bfloat16) -> Workload:
+    """C5: Qwen3-MoE-like block-FP8 experts, E=128, H=2048, I=768; gate_up
+    [E, 1536, 2048] (gate rows first) and down [E, 2048, 768] ~ N(0, 0.02)
+    quantized per 128x128 block; hidden bf16 ~ N(0,1) [4096, 2048]; router
+    logits ~ N(0,1) [4096, 128], top-8."""
+
+    from kairyu_amd.quant.block_fp8 import quantize_block_fp8
+
+    g = _gen(device, seed)
+    w13 = torch.empty((experts, 2 * inter, hidden), dtype=torch.float8_e4m3fn, device=device)
+    s13 = torch.empty((experts, 2 * inter // 128, hidden // 128), dtype=torch.float32, device=device)
+    w2 = torch.empty((experts, hidden, inter), dtype=torch.float8_e4m3fn, device=device)
+    s2 = torch.empty((experts, hidden // 128, inter // 128), dtype=torch.float32, device=device)
+    for e in range(0, experts, 16):
+        sl = slice(e, min(experts, e + 16))
+        count = sl.stop - sl.start
+        q, s = quantize_block_fp8(torch.randn((count, 2 * inter, hidden), generator=g, device=device) * 0.02)
+        w13[sl], s13[sl] = q, s
+        q, s = quantize_block_fp8(torch.randn((count, hidden, inter), generator=g, device=device) * 0.02)
+        w2[sl], s2[sl] = q, s
+    x = torch.randn((tokens, hidden), generator=g, device=device).to(x_dtype)
+    logits = torch.randn((tokens, experts), generator=g, device=device)
+    module = MoeFromLogits(w13, s13, w2, s2, logits, top_k, norm_topk_prob)
+    weight_bytes = experts * (2 * inter * hidden + hidden * inter)
+    scale_bytes = experts * ((2 * inter // 128) * (hidden // 128) + (hidden // 128) * (inter // 128)) * 4
+    nbytes = weight_bytes + scale_bytes + 2 * tokens * hidden * 2
+    flops = 2 * tokens * top_k * (2 * inter * hidden + hidden * inter)
+    return Workload(f"moe_block_fp8_t{tokens}_h{hidden}_i{inter}_e{experts}_k{top_k}", module, x,
+                    nbytes, flops, "hbm")
