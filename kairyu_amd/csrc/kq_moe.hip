@@ -124,99 +124,118 @@ moe_route_kernel(const void* __restrict__ logits, int dtype, int T, int E, int k
 }
 
 // -------------------------------------------------------------- stable sort
-constexpr int kSortChunk = 1024;
+constexpr int kSortChunk = 256;   // rows per chunk = threads per sort workgroup
 
 // Per-chunk expert histogram: counts[c][e].
-__global__ void __launch_bounds__(256)
+__global__ void __launch_bounds__(kSortChunk)
 moe_count_kernel(const int32_t* __restrict__ idx, int R, int E, int32_t* __restrict__ counts) {
   extern __shared__ int hist[];
-  for (int i = threadIdx.x; i < E; i += 256) hist[i] = 0;
+  for (int i = threadIdx.x; i < E; i += kSortChunk) hist[i] = 0;
   __syncthreads();
-  const int c = blockIdx.x;
-  for (int j = threadIdx.x; j < kSortChunk; j += 256) {
-    const int r = c * kSortChunk + j;
-    if (r < R) {
-      const int e = idx[r];
-      if (e >= 0 && e < E) atomicAdd(&hist[e], 1);
-    }
+  const int r = blockIdx.x * kSortChunk + threadIdx.x;
+  if (r < R) {
+    const int e = idx[r];
+    if (e >= 0 && e < E) atomicAdd(&hist[e], 1);
   }
   __syncthreads();
-  for (int i = threadIdx.x; i < E; i += 256) counts[(int64_t)c * E + i] = hist[i];
+  for (int i = threadIdx.x; i < E; i += kSortChunk) counts[(int64_t)blockIdx.x * E + i] = hist[i];
 }
 
-// One workgroup: expert offsets, per-chunk output bases and the M-tile table
-// (tile i -> (expert, first row)); unused table entries get expert -1.
+// Exclusive prefix sum of v[0..n) in LDS (n <= 1024, 1024 threads); returns the total.
+KQ_DEV int block_exclusive_scan(int* v, int* tmp, int n) {
+  const int t = threadIdx.x;
+  int x = t < n ? v[t] : 0;
+  tmp[t] = x;
+  __syncthreads();
+  for (int off = 1; off < 1024; off <<= 1) {
+    const int y = t >= off ? tmp[t - off] : 0;
+    __syncthreads();
+    tmp[t] += y;
+    __syncthreads();
+  }
+  const int total = tmp[1023];
+  if (t < n) v[t] = tmp[t] - x;
+  __syncthreads();
+  return total;
+}
+
+// One 1024-thread workgroup: column-wise exclusive scan of counts[C][E] into
+// base[c][e] (sorted position of chunk c's first row of expert e), expert
+// offsets, and the M-tile table (tile i -> (expert, first row); unused
+// entries get expert -1).  Thread (slice, e) scans a contiguous run of chunks.
 __global__ void __launch_bounds__(1024)
 moe_scan_kernel(const int32_t* __restrict__ counts, int C, int E, int BM, int max_tiles,
                 int32_t* __restrict__ offsets, int32_t* __restrict__ base, int32_t* __restrict__ tiles) {
-  __shared__ int tot[1024], ntile[1024], off[1024], tstart[1024];
-  __shared__ int total_tiles;
-  for (int e = threadIdx.x; e < E; e += 1024) {
-    int s = 0;
-    for (int c = 0; c < C; ++c) {
-      base[(int64_t)c * E + e] = s;
-      s += counts[(int64_t)c * E + e];
+  __shared__ int part[1024], tot[1024], ntile[1024], tmp[1024];
+  const int t = threadIdx.x;
+  int slices = 1;
+  while (slices * 2 * E <= 1024) slices *= 2;
+  const int per = (C + slices - 1) / slices;
+  const int e = t % E, sl = t / E;
+  const bool active = sl < slices;
+  const int c0 = active ? sl * per : 0, c1 = active ? min(C, c0 + per) : 0;
+  int sum = 0;
+  for (int c = c0; c < c1; ++c) sum += counts[(int64_t)c * E + e];
+  part[t] = sum;
+  __syncthreads();
+  if (t < E) {
+    int run = 0;
+    for (int q = 0; q < slices; ++q) {
+      const int v = part[q * E + t];
+      part[q * E + t] = run;   // slice start within the expert
+      run += v;
     }
-    tot[e] = s;
-    ntile[e] = (s + BM - 1) / BM;
+    tot[t] = run;
+    ntile[t] = (run + BM - 1) / BM;
   }
   __syncthreads();
-  if (threadIdx.x == 0) {
-    int run = 0, trun = 0;
-    for (int e = 0; e < E; ++e) {
-      off[e] = run;
-      offsets[e] = run;
-      run += tot[e];
-      tstart[e] = trun;
-      trun += ntile[e];
-    }
-    offsets[E] = run;
-    total_tiles = trun;
-  }
-  __syncthreads();
-  for (int e = threadIdx.x; e < E; e += 1024) {
-    for (int c = 0; c < C; ++c) base[(int64_t)c * E + e] += off[e];
-    for (int i = 0; i < ntile[e] && tstart[e] + i < max_tiles; ++i) {
-      tiles[2 * (tstart[e] + i)] = e;
-      tiles[2 * (tstart[e] + i) + 1] = off[e] + i * BM;
+  const int total_rows = block_exclusive_scan(tot, tmp, E);     // tot -> expert offsets
+  const int total_tiles = block_exclusive_scan(ntile, tmp, E);  // ntile -> first tile
+  (void)total_rows;
+  if (active) {
+    int run = tot[e] + part[t];
+    for (int c = c0; c < c1; ++c) {
+      base[(int64_t)c * E + e] = run;
+      run += counts[(int64_t)c * E + e];
     }
   }
-  for (int i = total_tiles + threadIdx.x; i < max_tiles; i += 1024) {
+  if (t < E) {
+    offsets[t] = tot[t];
+    if (t == E - 1) offsets[E] = total_rows;
+    const int rows = (t == E - 1 ? total_rows : tot[t + 1]) - tot[t];
+    const int nt = (rows + BM - 1) / BM;
+    for (int i = 0; i < nt && ntile[t] + i < max_tiles; ++i) {
+      tiles[2 * (ntile[t] + i)] = t;
+      tiles[2 * (ntile[t] + i) + 1] = tot[t] + i * BM;
+    }
+  }
+  for (int i = total_tiles + t; i < max_tiles; i += 1024) {
     tiles[2 * i] = -1;
     tiles[2 * i + 1] = 0;
   }
 }
 
-// One wave per chunk: sorted position of flat row r = base[c][e] + its rank
-// among the chunk's earlier rows routed to the same expert.
-__global__ void __launch_bounds__(64)
+// Sorted position of row r = base[chunk][e] + its rank among the chunk's
+// earlier rows routed to the same expert (stable).
+__global__ void __launch_bounds__(kSortChunk)
 moe_scatter_kernel(const int32_t* __restrict__ idx, int R, int E, const int32_t* __restrict__ base,
                    int32_t* __restrict__ sorted_rows, int32_t* __restrict__ inv) {
-  extern __shared__ int running[];
-  for (int i = threadIdx.x; i < E; i += 64) running[i] = 0;
+  __shared__ int ids[kSortChunk];
+  const int c = blockIdx.x, t = threadIdx.x;
+  const int r = c * kSortChunk + t;
+  const int e = r < R ? idx[r] : -1;
+  ids[t] = e;
   __syncthreads();
-  const int c = blockIdx.x, lane = threadIdx.x;
-  for (int g = 0; g < kSortChunk / 64; ++g) {
-    const int r = c * kSortChunk + g * 64 + lane;
-    const int e = r < R ? idx[r] : -1;
-    const bool ok = e >= 0 && e < E;
-    int rank = 0;
-    for (int d = 1; d < 64; ++d) {
-      const int o = __shfl(e, (lane - d) & 63, 64);
-      rank += (d <= lane && o == e) ? 1 : 0;
-    }
-    const int before = ok ? running[e] : 0;
-    __syncthreads();
-    if (ok) {
-      const int pos = base[(int64_t)c * E + e] + before + rank;
-      sorted_rows[pos] = r;
-      inv[r] = pos;
-      atomicAdd(&running[e], 1);
-    } else if (r < R) {
-      inv[r] = -1;
-    }
-    __syncthreads();
+  if (r >= R) return;
+  if (e < 0 || e >= E) {
+    inv[r] = -1;
+    return;
   }
+  int rank = 0;
+  for (int j = 0; j < t; ++j) rank += ids[j] == e ? 1 : 0;
+  const int pos = base[(int64_t)c * E + e] + rank;
+  sorted_rows[pos] = r;
+  inv[r] = pos;
 }
 
 // --------------------------------------------------- 1x128 activation quant
@@ -266,14 +285,27 @@ act_quant_fp8_blocks_kernel(const uint16_t* __restrict__ x, int dtype, int K, in
 }
 
 // ------------------------------------------------------------ grouped GEMM
-constexpr int kBM = 64;     // rows per tile
+// A tile is up to 256 rows of one expert x 256 weight rows; eight waves in a
+// 2 (row halves of 128) x 4 (column quarters of 64) grid.  Each wave keeps its
+// four B operands of a K block in registers while its eight 16-row A blocks
+// stream from LDS (~24 KB of LDS reads per wave per K block).  A, B and the
+// activation scales move global -> LDS with buffer_load ... lds (no register
+// staging), double-buffered: K block kb+1 is in flight while kb is
+// multiplied.  The loop is unrolled by two so the two LDS stages are distinct
+// arrays and reads of one stage never wait for the other stage's loads.
+// Tiles of one expert and column range are adjacent and land on one XCD, so
+// a second row chunk of an expert finds the weights in that XCD's L2.
+constexpr int kBM = 256;    // rows per tile
 constexpr int kBN = 256;    // weight rows per tile
 constexpr int kBK = 128;    // one scale block of K per step
+constexpr int kGemmThreads = 512;
+constexpr int32_t kOob = (int32_t)0x80000000u;  // buffer offset past every resource: reads 0
 enum { kModeGateUp = 0, kModeDown = 1 };
 
 struct MoeGemmArgs {
   const uint8_t* a;        // e4m3 activation rows of length K
   const float* as;         // activation block scales [rows][K/128]
+  int a_rows;              // rows of a / as (resource bounds)
   const int32_t* rows;     // sorted row -> flat routed row (token = flat / topk); null: identity
   int topk;
   const uint8_t* w;        // [E][N][K] e4m3
@@ -298,18 +330,33 @@ KQ_DEV float round_act(float v, int dtype) {
   return dtype == KQ_DTYPE_BF16 ? bf16_to_f32(f32_to_bf16(v)) : f16_to_f32(f32_to_f16(v));
 }
 
+// Global -> LDS copy of 16 (or 4) bytes per lane with buffer_load ... lds:
+// lane i writes at LDS byte lds + i * size.  Written as inline asm so the
+// compiler does not make every later LDS read wait for it (it cannot tell the
+// two stages apart); the kernel waits with s_waitcnt + s_barrier before it
+// reads a stage.  M0 carries the wave-uniform LDS address.
+KQ_DEV void dma_lds16(i32x4 rsrc, uint32_t lds, int32_t voff, int32_t soff) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+               ::"s"(lds), "v"(voff), "s"(rsrc), "s"(soff) : "memory", "m0");
+}
+KQ_DEV void dma_lds4(i32x4 rsrc, uint32_t lds, int32_t voff, int32_t soff) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, %3 offen lds"
+               ::"s"(lds), "v"(voff), "s"(rsrc), "s"(soff) : "memory", "m0");
+}
+
+// LDS map: two A stages, two B stages, two scale stages.
+constexpr int kMaxKB = 128;   // K <= 16384
+constexpr int kLdsA = 0, kLdsB = 2 * kBM * kBK, kLdsS = kLdsB + 2 * kBN * kBK;
+constexpr int kLdsW = kLdsS + 2 * kBM * 4;            // the tile's two weight-scale rows
+constexpr int kLdsBytes = kLdsW + 2 * kMaxKB * 4;
+
 template <int MODE>
-__global__ void __launch_bounds__(256)
+__global__ void __launch_bounds__(kGemmThreads)
 moe_gemm_kernel(MoeGemmArgs a) {
-  // one LDS stage (40 KB: up to three workgroups per CU); the next K block
-  // is fetched into registers while this one is multiplied
-  __shared__ __attribute__((aligned(16))) uint8_t sA[kBM * kBK];
-  __shared__ __attribute__((aligned(16))) uint8_t sB[kBN * kBK];
-  __shared__ float sS[kBM];
-  __shared__ float sRed[4][kBM];
-  const int tid = threadIdx.x, lane = lane_id();
+  __shared__ __attribute__((aligned(16))) uint8_t smem[kLdsBytes];
+  const int lane = lane_id();
   const int wave = __builtin_amdgcn_readfirstlane(wave_id());
-  // tiles sharing an n-tile and an expert are adjacent and land on one XCD
+  const int wr = wave >> 2, wc = wave & 3;
   const int nblk = a.mtiles * a.ntiles;
   const int L = xcd_swizzle(blockIdx.x, nblk);
   const int ntile = L / a.mtiles, mtile = L % a.mtiles;
@@ -318,111 +365,110 @@ moe_gemm_kernel(MoeGemmArgs a) {
     e = a.tiles[2 * mtile];
     if (e < 0) return;
     row0 = a.tiles[2 * mtile + 1];
-    row_end = a.offsets[e + 1];
+    row_end = min(a.offsets[e + 1], row0 + kBM);
   } else {
     e = 0;
     row0 = mtile * kBM;
-    row_end = a.M;
+    row_end = min(a.M, row0 + kBM);
   }
   const int KB = a.K / kBK;
   const int NB = (a.N + 127) / 128;
   const int n0 = MODE == kModeGateUp ? ntile * 128 : ntile * kBN;
-  const uint8_t* wexp = a.w + (int64_t)e * a.N * a.K;
+  const i32x4 ra = make_rsrc(a.a, (uint32_t)((uint64_t)a.a_rows * a.K));
+  const i32x4 rsc = make_rsrc(a.as, (uint32_t)((uint64_t)a.a_rows * KB * 4));
+  const i32x4 rw = make_rsrc(a.w + (int64_t)e * a.N * a.K, (uint32_t)((uint64_t)a.N * a.K));
   const float* wsexp = a.ws + (int64_t)e * NB * KB;
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)smem;
 
-  // global -> register staging of one K block: 2 A chunks, 8 B chunks, 1 scale
-  int64_t a_src[2];
-  bool a_ok[2];
+  // lane offsets of this wave's four 1 KB DMA blocks of the A and B stages:
+  // LDS slot p = block*64 + lane holds chunk c = (p & 7) ^ (row & 7) of row p / 8
+  int32_t a_off[4], b_off[4];
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int q = tid + 256 * i, r = row0 + (q >> 3);
-    a_ok[i] = r < row_end;
-    int64_t src = 0;
-    if (a_ok[i]) src = a.rows ? (int64_t)(a.rows[r] / a.topk) : (int64_t)r;
-    a_src[i] = src * a.K + (q & 7) * 16;
-  }
-  int64_t s_src = -1;
-  if (tid < kBM && row0 + tid < row_end)
-    s_src = (a.rows ? (int64_t)(a.rows[row0 + tid] / a.topk) : (int64_t)(row0 + tid)) * KB;
-  int64_t b_src[8];
-  bool b_ok[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int q = tid + 256 * i, j = q >> 3;
-    const int wrow = MODE == kModeGateUp ? (j < 128 ? n0 + j : a.I + n0 + (j - 128)) : n0 + j;
-    b_ok[i] = wrow < a.N;
-    b_src[i] = (int64_t)(b_ok[i] ? wrow : 0) * a.K + (q & 7) * 16;
-  }
-  i32x4 ra[2], rb[8];
-  float rs = 0.0f;
-  auto gload = [&](int kb) {
-    const int64_t ko = (int64_t)kb * kBK;
-#pragma unroll
-    for (int i = 0; i < 2; ++i) ra[i] = a_ok[i] ? *(const i32x4*)(a.a + a_src[i] + ko) : i32x4{0, 0, 0, 0};
-#pragma unroll
-    for (int i = 0; i < 8; ++i) rb[i] = b_ok[i] ? *(const i32x4*)(wexp + b_src[i] + ko) : i32x4{0, 0, 0, 0};
-    rs = s_src >= 0 ? a.as[s_src + kb] : 0.0f;
-  };
-  auto sstore = [&]() {
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int q = tid + 256 * i;
-      *(i32x4*)(&sA[tswz(q >> 3, q & 7)]) = ra[i];
+  for (int i = 0; i < 4; ++i) {
+    const int p = (wave * 4 + i) * 64 + lane, row = p >> 3, c = (p & 7) ^ (row & 7);
+    const int r = row0 + row;
+    a_off[i] = kOob;
+    if (r < row_end) {
+      const int src = a.rows ? a.rows[r] / a.topk : r;
+      a_off[i] = src * a.K + c * 16;
     }
+    const int wrow = MODE == kModeGateUp ? (row < 128 ? n0 + row : a.I + n0 + (row - 128)) : n0 + row;
+    b_off[i] = wrow < a.N ? wrow * a.K + c * 16 : kOob;
+  }
+  int32_t s_off = kOob;  // waves 0-3 fetch the 256 activation scales
+  if (wave < 4) {
+    const int r = row0 + wave * 64 + lane;
+    if (r < row_end) s_off = (a.rows ? a.rows[r] / a.topk : r) * KB * 4;
+  }
+  auto issue = [&](int kb, int st) {
+    const uint32_t la = lds0 + kLdsA + st * (kBM * kBK) + wave * 4096;
+    const uint32_t lb = lds0 + kLdsB + st * (kBN * kBK) + wave * 4096;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int q = tid + 256 * i;
-      *(i32x4*)(&sB[tswz(q >> 3, q & 7)]) = rb[i];
+    for (int i = 0; i < 4; ++i) {
+      dma_lds16(ra, la + i * 1024, a_off[i], kb * kBK);
+      dma_lds16(rw, lb + i * 1024, b_off[i], kb * kBK);
     }
-    if (tid < kBM) sS[tid] = rs;
+    if (wave < 4) dma_lds4(rsc, lds0 + kLdsS + st * (kBM * 4) + wave * 256, s_off, kb * 4);
   };
 
   // this wave's four 16-column blocks of the tile's 256 weight rows
   int cbr[4];
 #pragma unroll
   for (int c = 0; c < 4; ++c)
-    cbr[c] = MODE == kModeGateUp ? (c < 2 ? 32 * wave + 16 * c : 128 + 32 * wave + 16 * (c - 2))
-                                 : 64 * wave + 16 * c;
-  // their weight scale blocks (row block of weight row n0 + cbr[c])
-  int cnb[4];
-#pragma unroll
-  for (int c = 0; c < 4; ++c) {
-    const int j = cbr[c];
-    const int wrow = MODE == kModeGateUp ? (j < 128 ? n0 + j : a.I + n0 + (j - 128)) : n0 + j;
-    cnb[c] = min(wrow, a.N - 1) / 128;
+    cbr[c] = MODE == kModeGateUp ? (c < 2 ? 32 * wc + 16 * c : 128 + 32 * wc + 16 * (c - 2))
+                                 : 64 * wc + 16 * c;
+  // the tile's weight rows span two 128-row scale blocks (gate_up: the gate
+  // block and the up block; down: n0/128 and the next); stage both scale rows
+  // for every K block in LDS before the loop
+  float* sWs = (float*)(smem + kLdsW);
+  {
+    const int nb0 = (MODE == kModeGateUp ? n0 : n0) / 128;
+    const int nb1 = MODE == kModeGateUp ? (a.I + n0) / 128 : min(n0 / 128 + 1, NB - 1);
+    for (int t = threadIdx.x; t < 2 * KB; t += kGemmThreads)
+      sWs[t] = wsexp[(t < KB ? nb0 : nb1) * KB + (t % KB)];
   }
-
-  f32x4 acc[4][4];
+  int cslot[4];  // which staged scale row each of the wave's column blocks uses
 #pragma unroll
-  for (int r = 0; r < 4; ++r)
+  for (int c = 0; c < 4; ++c) cslot[c] = MODE == kModeGateUp ? (c < 2 ? 0 : 1) : (wc >> 1);
+
+  f32x4 acc[8][4];
+#pragma unroll
+  for (int r = 0; r < 8; ++r)
 #pragma unroll
     for (int c = 0; c < 4; ++c) acc[r][c] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   const int lr = lane & 15, kc = (lane >> 4) * 2;  // operand row and 16-byte chunk pair
-  gload(0);
-  sstore();
+  const int rbase = 128 * wr;
+  // rows 16*r + lr share (row & 7), so one swizzled offset serves all blocks
+  const int a_lo = tswz(rbase + lr, kc), a_hi = tswz(rbase + lr, kc + 1);
+  const int b_lo = tswz(lr, kc), b_hi = tswz(lr, kc + 1);
+
+  issue(0, 0);
+  __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   for (int kb = 0; kb < KB; ++kb) {
-    if (kb + 1 < KB) gload(kb + 1);
+    const int st = kb & 1;
+    if (kb + 1 < KB) issue(kb + 1, st ^ 1);
+    const uint8_t* sA = smem + kLdsA + st * (kBM * kBK);
+    const uint8_t* sB = smem + kLdsB + st * (kBN * kBK);
+    const float* sS = (const float*)(smem + kLdsS + st * (kBM * 4));
     float sw[4];
 #pragma unroll
-    for (int c = 0; c < 4; ++c) sw[c] = wsexp[cnb[c] * KB + kb];
+    for (int c = 0; c < 4; ++c) sw[c] = sWs[cslot[c] * KB + kb];
     i32x8 B[4];
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
-      const int row = cbr[c] + lr;
-      const i32x4 lo = *(const i32x4*)(&sB[tswz(row, kc)]);
-      const i32x4 hi = *(const i32x4*)(&sB[tswz(row, kc + 1)]);
+      const i32x4 lo = *(const i32x4*)(sB + cbr[c] * 128 + b_lo);
+      const i32x4 hi = *(const i32x4*)(sB + cbr[c] * 128 + b_hi);
       B[c] = i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
     }
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int row = 16 * r + lr;
-      const i32x4 lo = *(const i32x4*)(&sA[tswz(row, kc)]);
-      const i32x4 hi = *(const i32x4*)(&sA[tswz(row, kc + 1)]);
+    for (int r = 0; r < 8; ++r) {
+      const i32x4 lo = *(const i32x4*)(sA + r * 2048 + a_lo);
+      const i32x4 hi = *(const i32x4*)(sA + r * 2048 + a_hi);
       const i32x8 A = i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
       // activation scales of the four output rows this lane holds
-      const f32x4 sx = *(const f32x4*)(&sS[16 * r + 4 * (lane >> 4)]);
+      const f32x4 sx = *(const f32x4*)(&sS[rbase + 16 * r + 4 * (lane >> 4)]);
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
         const f32x4 blk = mfma_fp8(A, B[c], f32x4{0.f, 0.f, 0.f, 0.f});
@@ -430,22 +476,17 @@ moe_gemm_kernel(MoeGemmArgs a) {
         for (int q = 0; q < 4; ++q) acc[r][c][q] = fmaf(blk[q], sx[q] * sw[c], acc[r][c][q]);
       }
     }
-    if (kb + 1 < KB) {
-      __syncthreads();  // every wave is done reading this stage
-      sstore();
-    }
-    __syncthreads();
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's copies of stage kb+1 have landed
+    __syncthreads();                 // ... and everyone's; stage kb is free again
   }
 
   if constexpr (MODE == kModeGateUp) {
-    // SwiGLU in the activation dtype (out_dtype), then 1x128 e4m3 quantization of
-    // the tile's finished 128 activation columns
-    float act[4][2][4];
-    float rmax[4][4];
+    // SwiGLU in the activation dtype (out_dtype), then 1x128 e4m3 quantization
+    // of the tile's finished 128 activation columns; act overwrites acc[r][0..1]
+    float (*sRed)[kBM] = (float (*)[kBM])smem;  // stages are free after the loop
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-#pragma unroll
-      for (int q = 0; q < 4; ++q) rmax[r][q] = 0.0f;
+    for (int r = 0; r < 8; ++r) {
+      float rmax[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int g = 0; g < 2; ++g)
 #pragma unroll
@@ -454,53 +495,53 @@ moe_gemm_kernel(MoeGemmArgs a) {
           const float ub = round_act(acc[r][2 + g][q], a.out_dtype);
           const float sl = round_act(gb / (1.0f + expf(-gb)), a.out_dtype);
           const float av = round_act(sl * ub, a.out_dtype);
-          act[r][g][q] = av;
-          rmax[r][q] = fmaxf(rmax[r][q], fabsf(av));
+          acc[r][g][q] = av;
+          rmax[q] = fmaxf(rmax[q], fabsf(av));
         }
 #pragma unroll
       for (int q = 0; q < 4; ++q)
 #pragma unroll
-        for (int off = 8; off > 0; off >>= 1) rmax[r][q] = fmaxf(rmax[r][q], __shfl_xor(rmax[r][q], off, 64));
+        for (int off = 8; off > 0; off >>= 1) rmax[q] = fmaxf(rmax[q], __shfl_xor(rmax[q], off, 64));
       if (lr == 0)
 #pragma unroll
-        for (int q = 0; q < 4; ++q) sRed[wave][16 * r + 4 * (lane >> 4) + q] = rmax[r][q];
+        for (int q = 0; q < 4; ++q) sRed[wc][rbase + 16 * r + 4 * (lane >> 4) + q] = rmax[q];
     }
     __syncthreads();
     const int IB = a.I / 128;
 #pragma unroll
-    for (int r = 0; r < 4; ++r)
+    for (int r = 0; r < 8; ++r)
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const int lrow = 16 * r + 4 * (lane >> 4) + q;
+        const int lrow = rbase + 16 * r + 4 * (lane >> 4) + q;
         const int grow = row0 + lrow;
         if (grow >= row_end) continue;
         const float amax = fmaxf(fmaxf(sRed[0][lrow], sRed[1][lrow]), fmaxf(sRed[2][lrow], sRed[3][lrow]));
         const float s = __fdiv_rn(fmaxf(amax, 1e-12f), 448.0f);
 #pragma unroll
         for (int g = 0; g < 2; ++g) {
-          float v = __fdiv_rn(act[r][g][q], s);
+          float v = __fdiv_rn(acc[r][g][q], s);
           v = v < -448.0f ? -448.0f : (v > 448.0f ? 448.0f : v);
-          a.actq[(int64_t)grow * a.I + n0 + 32 * wave + 16 * g + lr] = (uint8_t)f32_to_e4m3(v);
+          a.actq[(int64_t)grow * a.I + n0 + 32 * wc + 16 * g + lr] = (uint8_t)f32_to_e4m3(v);
         }
-        if (wave == 0 && lr == 0) a.acts[(int64_t)grow * IB + n0 / 128] = s;
+        if (wc == 0 && lr == 0) a.acts[(int64_t)grow * IB + n0 / 128] = s;
       }
   } else {
 #pragma unroll
-    for (int r = 0; r < 4; ++r)
+    for (int c = 0; c < 4; ++c) {
+      const int n = n0 + cbr[c] + lr;
+      if (n >= a.N) continue;
+      const float bv = a.bias_dtype != KQ_DTYPE_NONE ? load_as_f32(a.bias, a.bias_dtype, n) : 0.0f;
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const int n = n0 + cbr[c] + lr;
-        if (n >= a.N) continue;
-        const float bv = a.bias_dtype != KQ_DTYPE_NONE ? load_as_f32(a.bias, a.bias_dtype, n) : 0.0f;
+      for (int r = 0; r < 8; ++r)
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-          const int grow = row0 + 16 * r + 4 * (lane >> 4) + q;
+          const int grow = row0 + rbase + 16 * r + 4 * (lane >> 4) + q;
           if (grow >= row_end) continue;
           float v = acc[r][c][q];
           if (a.bias_dtype != KQ_DTYPE_NONE) v = __fadd_rn(v, bv);
           ((uint16_t*)a.out)[(int64_t)grow * a.N + n] = f32_to_out(v, a.out_dtype);
         }
-      }
+    }
   }
 }
 
@@ -626,21 +667,21 @@ extern "C" int kq_block_fp8_gemm(const uint8_t* xq, const float* xs, const uint8
     set_error("kq_block_fp8_gemm: output dtype must be fp16 or bf16");
     return KQ_EUNSUPPORTED;
   }
-  if (m < 0 || n < 1 || k < kBK || (k % kBK) != 0 || m > 0x7fffffffLL || n > 0x7fffffffLL ||
-      k > 0x7fffffffLL) {
+  if (m < 0 || n < 1 || k < kBK || (k % kBK) != 0 || k > kBK * kMaxKB || m > 0x7fffffffLL ||
+      n > 0x7fffffffLL || n * k > 0x7fffffffLL) {
     set_error("kq_block_fp8_gemm: bad shape m=%lld n=%lld k=%lld (k must be a multiple of 128)",
               (long long)m, (long long)n, (long long)k);
     return KQ_EINVAL;
   }
   if (m == 0) return KQ_OK;
   MoeGemmArgs a{};
-  a.a = xq; a.as = xs; a.rows = nullptr; a.topk = 1;
+  a.a = xq; a.as = xs; a.a_rows = (int)m; a.rows = nullptr; a.topk = 1;
   a.w = w; a.ws = ws; a.tiles = nullptr; a.offsets = nullptr;
   a.M = (int)m; a.N = (int)n; a.K = (int)k; a.I = 0;
   a.mtiles = (int)((m + kBM - 1) / kBM);
   a.ntiles = (int)((n + kBN - 1) / kBN);
   a.out = out; a.out_dtype = out_dtype; a.bias = bias; a.bias_dtype = bias_dtype;
-  hipLaunchKernelGGL(moe_gemm_kernel<kModeDown>, dim3((unsigned)(a.mtiles * a.ntiles)), dim3(256), 0,
+  hipLaunchKernelGGL(moe_gemm_kernel<kModeDown>, dim3((unsigned)(a.mtiles * a.ntiles)), dim3(kGemmThreads), 0,
                      (hipStream_t)stream, a);
   return check_launch("kq_block_fp8_gemm");
 }
@@ -663,7 +704,9 @@ extern "C" int kq_moe_block_fp8_experts(const void* hidden, int dtype, int64_t t
   }
   if (tokens < 0 || hidden_size < kBK || (hidden_size % kBK) != 0 || inter < kBK ||
       (inter % kBK) != 0 || experts < 1 || experts > 1024 || top_k < 1 || top_k > experts ||
-      tokens * top_k > 0x7fffffffLL || hidden_size * 2 * inter > 0x7fffffffLL) {
+      hidden_size > kBK * kMaxKB || inter > kBK * kMaxKB || tokens * top_k > 0x7fffffffLL ||
+      hidden_size * 2 * inter > 0x7fffffffLL || tokens * hidden_size > 0x7fffffffLL ||
+      tokens * top_k * inter > 0x7fffffffLL) {
     set_error("kq_moe_block_fp8_experts: bad shape tokens=%lld hidden=%lld inter=%lld experts=%lld "
               "top_k=%d (hidden and inter must be multiples of 128)",
               (long long)tokens, (long long)hidden_size, (long long)inter, (long long)experts, top_k);
@@ -694,29 +737,30 @@ extern "C" int kq_moe_block_fp8_experts(const void* hidden, int dtype, int64_t t
   const int E = (int)experts;
   const int max_tiles = (R + kBM - 1) / kBM + E;
 
-  hipLaunchKernelGGL(moe_count_kernel, dim3(C), dim3(256), E * sizeof(int), st, topk_idx, R, E, counts);
+  hipLaunchKernelGGL(moe_count_kernel, dim3(C), dim3(kSortChunk), E * sizeof(int), st, topk_idx, R, E,
+                     counts);
   hipLaunchKernelGGL(moe_scan_kernel, dim3(1), dim3(1024), 0, st, counts, C, E, kBM, max_tiles, offsets,
                      base, tiles);
-  hipLaunchKernelGGL(moe_scatter_kernel, dim3(C), dim3(64), E * sizeof(int), st, topk_idx, R, E, base,
-                     sorted, inv);
+  hipLaunchKernelGGL(moe_scatter_kernel, dim3(C), dim3(kSortChunk), 0, st, topk_idx, R, E, base, sorted,
+                     inv);
   launch_act_quant_blocks(hidden, dtype, tokens, hidden_size, hidden_size, xq, xs, st);
 
   MoeGemmArgs g{};
-  g.a = xq; g.as = xs; g.rows = sorted; g.topk = top_k;
+  g.a = xq; g.as = xs; g.a_rows = (int)tokens; g.rows = sorted; g.topk = top_k;
   g.w = w13; g.ws = s13; g.tiles = tiles; g.offsets = offsets;
   g.N = (int)(2 * inter); g.K = (int)hidden_size; g.I = (int)inter;
   g.mtiles = max_tiles; g.ntiles = (int)(inter / 128);
   g.actq = actq; g.acts = acts; g.out_dtype = dtype;
-  hipLaunchKernelGGL(moe_gemm_kernel<kModeGateUp>, dim3((unsigned)(g.mtiles * g.ntiles)), dim3(256), 0,
+  hipLaunchKernelGGL(moe_gemm_kernel<kModeGateUp>, dim3((unsigned)(g.mtiles * g.ntiles)), dim3(kGemmThreads), 0,
                      st, g);
 
   MoeGemmArgs d{};
-  d.a = actq; d.as = acts; d.rows = nullptr; d.topk = 1;
+  d.a = actq; d.as = acts; d.a_rows = R; d.rows = nullptr; d.topk = 1;
   d.w = w2; d.ws = s2; d.tiles = tiles; d.offsets = offsets;
   d.N = (int)hidden_size; d.K = (int)inter; d.I = 0;
   d.mtiles = max_tiles; d.ntiles = (int)((hidden_size + kBN - 1) / kBN);
   d.out = y; d.out_dtype = dtype; d.bias = nullptr; d.bias_dtype = KQ_DTYPE_NONE;
-  hipLaunchKernelGGL(moe_gemm_kernel<kModeDown>, dim3((unsigned)(d.mtiles * d.ntiles)), dim3(256), 0,
+  hipLaunchKernelGGL(moe_gemm_kernel<kModeDown>, dim3((unsigned)(d.mtiles * d.ntiles)), dim3(kGemmThreads), 0,
                      st, d);
 
   hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)tokens), dim3(256), 0, st, y, dtype, inv, topk_w,
