@@ -20,17 +20,19 @@
 //      the grid's M tiles, per-chunk ranks); every output row keeps the
 //      ascending flat order inside its expert segment.
 //   2. act_quant_fp8_blocks: each token quantized once (not once per slot).
-//   3. grouped GEMM 1 (gate_up): A rows gathered through the sorted order,
-//      B = the expert's stacked [gate; up] weight.  A 64 x 256 tile pairs
-//      gate columns [n0, n0+128) with up columns [I+n0, I+n0+128), so the
-//      epilogue forms bf16 SwiGLU and quantizes the finished 128-column
-//      activation block to e4m3 in registers (no bf16 intermediate in HBM).
-//   4. grouped GEMM 2 (down): 64 x 256 tiles -> expert outputs (bf16/fp16).
+//   3. grouped GEMM 1 (gate_up), kq_tile_gemm.h: activation rows gathered
+//      through the sorted order, weights = the expert's stacked [gate; up].
+//      A 256 x 256 tile pairs gate columns [n0, n0+128) with up columns
+//      [I+n0, I+n0+128), so the epilogue forms the SwiGLU in the activation
+//      dtype and quantizes the finished 128-column block to e4m3 in registers
+//      (no bf16 intermediate in HBM).
+//   4. grouped GEMM 2 (down): 256 x 256 tiles -> expert outputs (bf16/fp16).
 //   5. combine: fp32 slot-order weighted sum per token.
 // Both GEMMs use v_mfma_scale_f32_16x16x128_f8f6f4 (unit E8M0 scales): one
 // MFMA spans one 128-wide K block, and its fp32 result is scaled by
 // s_act[row][kb] * s_w[nb][kb] before it is added to the accumulator.
 #include "kq_common.h"
+#include "kq_tile_gemm.h"
 
 #include <algorithm>
 
@@ -125,6 +127,7 @@ moe_route_kernel(const void* __restrict__ logits, int dtype, int T, int E, int k
 
 // -------------------------------------------------------------- stable sort
 constexpr int kSortChunk = 256;   // rows per chunk = threads per sort workgroup
+constexpr int kBM = kTgBM;        // rows per GEMM row tile
 
 // Per-chunk expert histogram: counts[c][e].
 __global__ void __launch_bounds__(kSortChunk)
@@ -161,11 +164,13 @@ KQ_DEV int block_exclusive_scan(int* v, int* tmp, int n) {
 
 // One 1024-thread workgroup: column-wise exclusive scan of counts[C][E] into
 // base[c][e] (sorted position of chunk c's first row of expert e), expert
-// offsets, and the M-tile table (tile i -> (expert, first row); unused
-// entries get expert -1).  Thread (slice, e) scans a contiguous run of chunks.
+// offsets, the row-tile table (tile i -> (expert, first row, end row, 0);
+// unused entries get expert -1) and the count of tiles in use.  Thread
+// (slice, e) scans a contiguous run of chunks.
 __global__ void __launch_bounds__(1024)
 moe_scan_kernel(const int32_t* __restrict__ counts, int C, int E, int BM, int max_tiles,
-                int32_t* __restrict__ offsets, int32_t* __restrict__ base, int32_t* __restrict__ tiles) {
+                int32_t* __restrict__ offsets, int32_t* __restrict__ base, int32_t* __restrict__ tiles,
+                int32_t* __restrict__ tile_count) {
   __shared__ int part[1024], tot[1024], ntile[1024], tmp[1024];
   const int t = threadIdx.x;
   int slices = 1;
@@ -205,13 +210,19 @@ moe_scan_kernel(const int32_t* __restrict__ counts, int C, int E, int BM, int ma
     const int rows = (t == E - 1 ? total_rows : tot[t + 1]) - tot[t];
     const int nt = (rows + BM - 1) / BM;
     for (int i = 0; i < nt && ntile[t] + i < max_tiles; ++i) {
-      tiles[2 * (ntile[t] + i)] = t;
-      tiles[2 * (ntile[t] + i) + 1] = tot[t] + i * BM;
+      int32_t* d = tiles + 4 * (ntile[t] + i);
+      d[0] = t;
+      d[1] = tot[t] + i * BM;
+      d[2] = min(tot[t] + rows, tot[t] + (i + 1) * BM);
+      d[3] = 0;
     }
   }
+  if (t == 0) tile_count[0] = min(total_tiles, max_tiles);
   for (int i = total_tiles + t; i < max_tiles; i += 1024) {
-    tiles[2 * i] = -1;
-    tiles[2 * i + 1] = 0;
+    tiles[4 * i] = -1;
+    tiles[4 * i + 1] = 0;
+    tiles[4 * i + 2] = 0;
+    tiles[4 * i + 3] = 0;
   }
 }
 
@@ -284,267 +295,6 @@ act_quant_fp8_blocks_kernel(const uint16_t* __restrict__ x, int dtype, int K, in
   if ((threadIdx.x & 15) == 0) xs[row * ((K + 127) / 128) + k0 / 128] = s;
 }
 
-// ------------------------------------------------------------ grouped GEMM
-// A tile is up to 256 rows of one expert x 256 weight rows; eight waves in a
-// 2 (row halves of 128) x 4 (column quarters of 64) grid.  Each wave keeps its
-// four B operands of a K block in registers while its eight 16-row A blocks
-// stream from LDS (~24 KB of LDS reads per wave per K block).  A, B and the
-// activation scales move global -> LDS with buffer_load ... lds (no register
-// staging), double-buffered: K block kb+1 is in flight while kb is
-// multiplied.  The loop is unrolled by two so the two LDS stages are distinct
-// arrays and reads of one stage never wait for the other stage's loads.
-// Tiles of one expert and column range are adjacent and land on one XCD, so
-// a second row chunk of an expert finds the weights in that XCD's L2.
-constexpr int kBM = 256;    // rows per tile
-constexpr int kBN = 256;    // weight rows per tile
-constexpr int kBK = 128;    // one scale block of K per step
-constexpr int kGemmThreads = 512;
-constexpr int32_t kOob = (int32_t)0x80000000u;  // buffer offset past every resource: reads 0
-enum { kModeGateUp = 0, kModeDown = 1 };
-
-struct MoeGemmArgs {
-  const uint8_t* a;        // e4m3 activation rows of length K
-  const float* as;         // activation block scales [rows][K/128]
-  int a_rows;              // rows of a / as (resource bounds)
-  const int32_t* rows;     // sorted row -> flat routed row (token = flat / topk); null: identity
-  int topk;
-  const uint8_t* w;        // [E][N][K] e4m3
-  const float* ws;         // [E][N/128][K/128]
-  const int32_t* tiles;    // [max_tiles][2] (expert, first row); null: dense tiles of M rows
-  const int32_t* offsets;  // [E+1] expert row offsets; null: dense
-  int M;                   // dense row count
-  int N, K, I;             // weight rows, K, activation width (gate_up: N = 2I)
-  int mtiles, ntiles;
-  uint8_t* actq;           // gate_up: e4m3 activations [rows][I] (out_dtype: their dtype)
-  float* acts;             // gate_up: their block scales [rows][I/128]
-  void* out;               // down: [rows][N] in out_dtype
-  int out_dtype;
-  const void* bias;        // down (dense linear only)
-  int bias_dtype;
-};
-
-KQ_DEV int tswz(int r, int c) { return r * 128 + ((c ^ (r & 7)) << 4); }
-
-// Round to the activation dtype (bf16 or fp16) and back.
-KQ_DEV float round_act(float v, int dtype) {
-  return dtype == KQ_DTYPE_BF16 ? bf16_to_f32(f32_to_bf16(v)) : f16_to_f32(f32_to_f16(v));
-}
-
-// Global -> LDS copy of 16 (or 4) bytes per lane with buffer_load ... lds:
-// lane i writes at LDS byte lds + i * size.  Written as inline asm so the
-// compiler does not make every later LDS read wait for it (it cannot tell the
-// two stages apart); the kernel waits with s_waitcnt + s_barrier before it
-// reads a stage.  M0 carries the wave-uniform LDS address.
-KQ_DEV void dma_lds16(i32x4 rsrc, uint32_t lds, int32_t voff, int32_t soff) {
-  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
-               ::"s"(lds), "v"(voff), "s"(rsrc), "s"(soff) : "memory", "m0");
-}
-KQ_DEV void dma_lds4(i32x4 rsrc, uint32_t lds, int32_t voff, int32_t soff) {
-  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, %3 offen lds"
-               ::"s"(lds), "v"(voff), "s"(rsrc), "s"(soff) : "memory", "m0");
-}
-
-// LDS map: two A stages, two B stages, two scale stages.
-constexpr int kMaxKB = 128;   // K <= 16384
-constexpr int kLdsA = 0, kLdsB = 2 * kBM * kBK, kLdsS = kLdsB + 2 * kBN * kBK;
-constexpr int kLdsW = kLdsS + 2 * kBM * 4;            // the tile's two weight-scale rows
-constexpr int kLdsBytes = kLdsW + 2 * kMaxKB * 4;
-
-template <int MODE>
-__global__ void __launch_bounds__(kGemmThreads)
-moe_gemm_kernel(MoeGemmArgs a) {
-  __shared__ __attribute__((aligned(16))) uint8_t smem[kLdsBytes];
-  const int lane = lane_id();
-  const int wave = __builtin_amdgcn_readfirstlane(wave_id());
-  const int wr = wave >> 2, wc = wave & 3;
-  const int nblk = a.mtiles * a.ntiles;
-  const int L = xcd_swizzle(blockIdx.x, nblk);
-  const int ntile = L / a.mtiles, mtile = L % a.mtiles;
-  int e, row0, row_end;
-  if (a.tiles) {
-    e = a.tiles[2 * mtile];
-    if (e < 0) return;
-    row0 = a.tiles[2 * mtile + 1];
-    row_end = min(a.offsets[e + 1], row0 + kBM);
-  } else {
-    e = 0;
-    row0 = mtile * kBM;
-    row_end = min(a.M, row0 + kBM);
-  }
-  const int KB = a.K / kBK;
-  const int NB = (a.N + 127) / 128;
-  const int n0 = MODE == kModeGateUp ? ntile * 128 : ntile * kBN;
-  const i32x4 ra = make_rsrc(a.a, (uint32_t)((uint64_t)a.a_rows * a.K));
-  const i32x4 rsc = make_rsrc(a.as, (uint32_t)((uint64_t)a.a_rows * KB * 4));
-  const i32x4 rw = make_rsrc(a.w + (int64_t)e * a.N * a.K, (uint32_t)((uint64_t)a.N * a.K));
-  const float* wsexp = a.ws + (int64_t)e * NB * KB;
-  const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)smem;
-
-  // lane offsets of this wave's four 1 KB DMA blocks of the A and B stages:
-  // LDS slot p = block*64 + lane holds chunk c = (p & 7) ^ (row & 7) of row p / 8
-  int32_t a_off[4], b_off[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int p = (wave * 4 + i) * 64 + lane, row = p >> 3, c = (p & 7) ^ (row & 7);
-    const int r = row0 + row;
-    a_off[i] = kOob;
-    if (r < row_end) {
-      const int src = a.rows ? a.rows[r] / a.topk : r;
-      a_off[i] = src * a.K + c * 16;
-    }
-    const int wrow = MODE == kModeGateUp ? (row < 128 ? n0 + row : a.I + n0 + (row - 128)) : n0 + row;
-    b_off[i] = wrow < a.N ? wrow * a.K + c * 16 : kOob;
-  }
-  int32_t s_off = kOob;  // waves 0-3 fetch the 256 activation scales
-  if (wave < 4) {
-    const int r = row0 + wave * 64 + lane;
-    if (r < row_end) s_off = (a.rows ? a.rows[r] / a.topk : r) * KB * 4;
-  }
-  auto issue = [&](int kb, int st) {
-    const uint32_t la = lds0 + kLdsA + st * (kBM * kBK) + wave * 4096;
-    const uint32_t lb = lds0 + kLdsB + st * (kBN * kBK) + wave * 4096;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      dma_lds16(ra, la + i * 1024, a_off[i], kb * kBK);
-      dma_lds16(rw, lb + i * 1024, b_off[i], kb * kBK);
-    }
-    if (wave < 4) dma_lds4(rsc, lds0 + kLdsS + st * (kBM * 4) + wave * 256, s_off, kb * 4);
-  };
-
-  // this wave's four 16-column blocks of the tile's 256 weight rows
-  int cbr[4];
-#pragma unroll
-  for (int c = 0; c < 4; ++c)
-    cbr[c] = MODE == kModeGateUp ? (c < 2 ? 32 * wc + 16 * c : 128 + 32 * wc + 16 * (c - 2))
-                                 : 64 * wc + 16 * c;
-  // the tile's weight rows span two 128-row scale blocks (gate_up: the gate
-  // block and the up block; down: n0/128 and the next); stage both scale rows
-  // for every K block in LDS before the loop
-  float* sWs = (float*)(smem + kLdsW);
-  {
-    const int nb0 = (MODE == kModeGateUp ? n0 : n0) / 128;
-    const int nb1 = MODE == kModeGateUp ? (a.I + n0) / 128 : min(n0 / 128 + 1, NB - 1);
-    for (int t = threadIdx.x; t < 2 * KB; t += kGemmThreads)
-      sWs[t] = wsexp[(t < KB ? nb0 : nb1) * KB + (t % KB)];
-  }
-  int cslot[4];  // which staged scale row each of the wave's column blocks uses
-#pragma unroll
-  for (int c = 0; c < 4; ++c) cslot[c] = MODE == kModeGateUp ? (c < 2 ? 0 : 1) : (wc >> 1);
-
-  f32x4 acc[8][4];
-#pragma unroll
-  for (int r = 0; r < 8; ++r)
-#pragma unroll
-    for (int c = 0; c < 4; ++c) acc[r][c] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-  const int lr = lane & 15, kc = (lane >> 4) * 2;  // operand row and 16-byte chunk pair
-  const int rbase = 128 * wr;
-  // rows 16*r + lr share (row & 7), so one swizzled offset serves all blocks
-  const int a_lo = tswz(rbase + lr, kc), a_hi = tswz(rbase + lr, kc + 1);
-  const int b_lo = tswz(lr, kc), b_hi = tswz(lr, kc + 1);
-
-  issue(0, 0);
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  for (int kb = 0; kb < KB; ++kb) {
-    const int st = kb & 1;
-    if (kb + 1 < KB) issue(kb + 1, st ^ 1);
-    const uint8_t* sA = smem + kLdsA + st * (kBM * kBK);
-    const uint8_t* sB = smem + kLdsB + st * (kBN * kBK);
-    const float* sS = (const float*)(smem + kLdsS + st * (kBM * 4));
-    float sw[4];
-#pragma unroll
-    for (int c = 0; c < 4; ++c) sw[c] = sWs[cslot[c] * KB + kb];
-    i32x8 B[4];
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const i32x4 lo = *(const i32x4*)(sB + cbr[c] * 128 + b_lo);
-      const i32x4 hi = *(const i32x4*)(sB + cbr[c] * 128 + b_hi);
-      B[c] = i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-    }
-#pragma unroll
-    for (int r = 0; r < 8; ++r) {
-      const i32x4 lo = *(const i32x4*)(sA + r * 2048 + a_lo);
-      const i32x4 hi = *(const i32x4*)(sA + r * 2048 + a_hi);
-      const i32x8 A = i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-      // activation scales of the four output rows this lane holds
-      const f32x4 sx = *(const f32x4*)(&sS[rbase + 16 * r + 4 * (lane >> 4)]);
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const f32x4 blk = mfma_fp8(A, B[c], f32x4{0.f, 0.f, 0.f, 0.f});
-#pragma unroll
-        for (int q = 0; q < 4; ++q) acc[r][c][q] = fmaf(blk[q], sx[q] * sw[c], acc[r][c][q]);
-      }
-    }
-    __builtin_amdgcn_s_waitcnt(0);  // this wave's copies of stage kb+1 have landed
-    __syncthreads();                 // ... and everyone's; stage kb is free again
-  }
-
-  if constexpr (MODE == kModeGateUp) {
-    // SwiGLU in the activation dtype (out_dtype), then 1x128 e4m3 quantization
-    // of the tile's finished 128 activation columns; act overwrites acc[r][0..1]
-    float (*sRed)[kBM] = (float (*)[kBM])smem;  // stages are free after the loop
-#pragma unroll
-    for (int r = 0; r < 8; ++r) {
-      float rmax[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int g = 0; g < 2; ++g)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const float gb = round_act(acc[r][g][q], a.out_dtype);
-          const float ub = round_act(acc[r][2 + g][q], a.out_dtype);
-          const float sl = round_act(gb / (1.0f + expf(-gb)), a.out_dtype);
-          const float av = round_act(sl * ub, a.out_dtype);
-          acc[r][g][q] = av;
-          rmax[q] = fmaxf(rmax[q], fabsf(av));
-        }
-#pragma unroll
-      for (int q = 0; q < 4; ++q)
-#pragma unroll
-        for (int off = 8; off > 0; off >>= 1) rmax[q] = fmaxf(rmax[q], __shfl_xor(rmax[q], off, 64));
-      if (lr == 0)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) sRed[wc][rbase + 16 * r + 4 * (lane >> 4) + q] = rmax[q];
-    }
-    __syncthreads();
-    const int IB = a.I / 128;
-#pragma unroll
-    for (int r = 0; r < 8; ++r)
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int lrow = rbase + 16 * r + 4 * (lane >> 4) + q;
-        const int grow = row0 + lrow;
-        if (grow >= row_end) continue;
-        const float amax = fmaxf(fmaxf(sRed[0][lrow], sRed[1][lrow]), fmaxf(sRed[2][lrow], sRed[3][lrow]));
-        const float s = __fdiv_rn(fmaxf(amax, 1e-12f), 448.0f);
-#pragma unroll
-        for (int g = 0; g < 2; ++g) {
-          float v = __fdiv_rn(acc[r][g][q], s);
-          v = v < -448.0f ? -448.0f : (v > 448.0f ? 448.0f : v);
-          a.actq[(int64_t)grow * a.I + n0 + 32 * wc + 16 * g + lr] = (uint8_t)f32_to_e4m3(v);
-        }
-        if (wc == 0 && lr == 0) a.acts[(int64_t)grow * IB + n0 / 128] = s;
-      }
-  } else {
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const int n = n0 + cbr[c] + lr;
-      if (n >= a.N) continue;
-      const float bv = a.bias_dtype != KQ_DTYPE_NONE ? load_as_f32(a.bias, a.bias_dtype, n) : 0.0f;
-#pragma unroll
-      for (int r = 0; r < 8; ++r)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int grow = row0 + rbase + 16 * r + 4 * (lane >> 4) + q;
-          if (grow >= row_end) continue;
-          float v = acc[r][c][q];
-          if (a.bias_dtype != KQ_DTYPE_NONE) v = __fadd_rn(v, bv);
-          ((uint16_t*)a.out)[(int64_t)grow * a.N + n] = f32_to_out(v, a.out_dtype);
-        }
-    }
-  }
-}
-
 // ------------------------------------------------------------------ combine
 // out[t] = sum over slots s (in order) of fp32(y[inv[t*k+s]]) * w[t*k+s].
 __global__ void __launch_bounds__(256)
@@ -584,7 +334,7 @@ moe_combine_kernel(const uint16_t* __restrict__ y, int y_dtype, const int32_t* _
 
 // ------------------------------------------------------------------- host
 struct MoeWorkspace {
-  size_t counts, base, offsets, tiles, sorted, inv, xq, xs, actq, acts, y, total;
+  size_t counts, base, offsets, tiles, tile_count, sorted, inv, xq, xs, actq, acts, y, total;
 };
 
 static size_t align256(size_t v) { return (v + 255) / 256 * 256; }
@@ -599,7 +349,8 @@ static MoeWorkspace moe_layout(int64_t T, int64_t H, int64_t I, int64_t E, int64
   w.counts = take((size_t)C * E * 4);
   w.base = take((size_t)C * E * 4);
   w.offsets = take((size_t)(E + 1) * 4);
-  w.tiles = take((size_t)max_tiles * 8);
+  w.tiles = take((size_t)max_tiles * 16);
+  w.tile_count = take(4);
   w.sorted = take((size_t)R * 4);
   w.inv = take((size_t)R * 4);
   w.xq = take((size_t)T * H);
@@ -667,22 +418,21 @@ extern "C" int kq_block_fp8_gemm(const uint8_t* xq, const float* xs, const uint8
     set_error("kq_block_fp8_gemm: output dtype must be fp16 or bf16");
     return KQ_EUNSUPPORTED;
   }
-  if (m < 0 || n < 1 || k < kBK || (k % kBK) != 0 || k > kBK * kMaxKB || m > 0x7fffffffLL ||
-      n > 0x7fffffffLL || n * k > 0x7fffffffLL) {
+  if (m < 0 || n < 1 || k < kTgBK || (k % kTgBK) != 0 || k > kTgBK * kTgMaxKB || m > 0x7fffffffLL ||
+      n > 0x7fffffffLL || n * k > 0x7fffffffLL || m * k > 0x7fffffffLL) {
     set_error("kq_block_fp8_gemm: bad shape m=%lld n=%lld k=%lld (k must be a multiple of 128)",
               (long long)m, (long long)n, (long long)k);
     return KQ_EINVAL;
   }
   if (m == 0) return KQ_OK;
-  MoeGemmArgs a{};
-  a.a = xq; a.as = xs; a.a_rows = (int)m; a.rows = nullptr; a.topk = 1;
-  a.w = w; a.ws = ws; a.tiles = nullptr; a.offsets = nullptr;
+  TileGemmArgs a{};
+  a.x = xq; a.xs = xs; a.x_rows = (int)m; a.gather = nullptr; a.topk = 1;
+  a.w = w; a.ws = ws; a.mtile_table = nullptr; a.mtile_count = nullptr;
   a.M = (int)m; a.N = (int)n; a.K = (int)k; a.I = 0;
-  a.mtiles = (int)((m + kBM - 1) / kBM);
-  a.ntiles = (int)((n + kBN - 1) / kBN);
+  a.mtiles = (int)((m + kTgBM - 1) / kTgBM);
+  a.ntiles = (int)((n + kTgBN - 1) / kTgBN);
   a.out = out; a.out_dtype = out_dtype; a.bias = bias; a.bias_dtype = bias_dtype;
-  hipLaunchKernelGGL(moe_gemm_kernel<kModeDown>, dim3((unsigned)(a.mtiles * a.ntiles)), dim3(kGemmThreads), 0,
-                     (hipStream_t)stream, a);
+  tg_launch<kTgFp8, true, kTgEpiStore>(a, (hipStream_t)stream);
   return check_launch("kq_block_fp8_gemm");
 }
 
@@ -702,9 +452,9 @@ extern "C" int kq_moe_block_fp8_experts(const void* hidden, int dtype, int64_t t
     set_error("kq_moe_block_fp8_experts: hidden dtype must be fp16 or bf16");
     return KQ_EUNSUPPORTED;
   }
-  if (tokens < 0 || hidden_size < kBK || (hidden_size % kBK) != 0 || inter < kBK ||
-      (inter % kBK) != 0 || experts < 1 || experts > 1024 || top_k < 1 || top_k > experts ||
-      hidden_size > kBK * kMaxKB || inter > kBK * kMaxKB || tokens * top_k > 0x7fffffffLL ||
+  if (tokens < 0 || hidden_size < kTgBK || (hidden_size % kTgBK) != 0 || inter < kTgBK ||
+      (inter % kTgBK) != 0 || experts < 1 || experts > 1024 || top_k < 1 || top_k > experts ||
+      hidden_size > kTgBK * kTgMaxKB || inter > kTgBK * kTgMaxKB || tokens * top_k > 0x7fffffffLL ||
       hidden_size * 2 * inter > 0x7fffffffLL || tokens * hidden_size > 0x7fffffffLL ||
       tokens * top_k * inter > 0x7fffffffLL) {
     set_error("kq_moe_block_fp8_experts: bad shape tokens=%lld hidden=%lld inter=%lld experts=%lld "
@@ -725,6 +475,7 @@ extern "C" int kq_moe_block_fp8_experts(const void* hidden, int dtype, int64_t t
   int32_t* base = (int32_t*)(ws + L.base);
   int32_t* offsets = (int32_t*)(ws + L.offsets);
   int32_t* tiles = (int32_t*)(ws + L.tiles);
+  int32_t* tile_count = (int32_t*)(ws + L.tile_count);
   int32_t* sorted = (int32_t*)(ws + L.sorted);
   int32_t* inv = (int32_t*)(ws + L.inv);
   uint8_t* xq = ws + L.xq;
@@ -740,28 +491,26 @@ extern "C" int kq_moe_block_fp8_experts(const void* hidden, int dtype, int64_t t
   hipLaunchKernelGGL(moe_count_kernel, dim3(C), dim3(kSortChunk), E * sizeof(int), st, topk_idx, R, E,
                      counts);
   hipLaunchKernelGGL(moe_scan_kernel, dim3(1), dim3(1024), 0, st, counts, C, E, kBM, max_tiles, offsets,
-                     base, tiles);
+                     base, tiles, tile_count);
   hipLaunchKernelGGL(moe_scatter_kernel, dim3(C), dim3(kSortChunk), 0, st, topk_idx, R, E, base, sorted,
                      inv);
   launch_act_quant_blocks(hidden, dtype, tokens, hidden_size, hidden_size, xq, xs, st);
 
-  MoeGemmArgs g{};
-  g.a = xq; g.as = xs; g.a_rows = (int)tokens; g.rows = sorted; g.topk = top_k;
-  g.w = w13; g.ws = s13; g.tiles = tiles; g.offsets = offsets;
+  TileGemmArgs g{};
+  g.x = xq; g.xs = xs; g.x_rows = (int)tokens; g.gather = sorted; g.topk = top_k;
+  g.w = w13; g.ws = s13; g.mtile_table = tiles; g.mtile_count = tile_count;
   g.N = (int)(2 * inter); g.K = (int)hidden_size; g.I = (int)inter;
   g.mtiles = max_tiles; g.ntiles = (int)(inter / 128);
-  g.actq = actq; g.acts = acts; g.out_dtype = dtype;
-  hipLaunchKernelGGL(moe_gemm_kernel<kModeGateUp>, dim3((unsigned)(g.mtiles * g.ntiles)), dim3(kGemmThreads), 0,
-                     st, g);
+  g.actq = actq; g.acts = acts; g.out_dtype = dtype; g.bias_dtype = KQ_DTYPE_NONE;
+  tg_launch<kTgFp8, true, kTgEpiSwiGluQuant>(g, st);
 
-  MoeGemmArgs d{};
-  d.a = actq; d.as = acts; d.a_rows = R; d.rows = nullptr; d.topk = 1;
-  d.w = w2; d.ws = s2; d.tiles = tiles; d.offsets = offsets;
+  TileGemmArgs d{};
+  d.x = actq; d.xs = acts; d.x_rows = R; d.gather = nullptr; d.topk = 1;
+  d.w = w2; d.ws = s2; d.mtile_table = tiles; d.mtile_count = tile_count;
   d.N = (int)hidden_size; d.K = (int)inter; d.I = 0;
-  d.mtiles = max_tiles; d.ntiles = (int)((hidden_size + kBN - 1) / kBN);
+  d.mtiles = max_tiles; d.ntiles = (int)((hidden_size + kTgBN - 1) / kTgBN);
   d.out = y; d.out_dtype = dtype; d.bias = nullptr; d.bias_dtype = KQ_DTYPE_NONE;
-  hipLaunchKernelGGL(moe_gemm_kernel<kModeDown>, dim3((unsigned)(d.mtiles * d.ntiles)), dim3(kGemmThreads), 0,
-                     st, d);
+  tg_launch<kTgFp8, true, kTgEpiStore>(d, st);
 
   hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)tokens), dim3(256), 0, st, y, dtype, inv, topk_w,
                      top_k, (int)hidden_size, (uint16_t*)out);

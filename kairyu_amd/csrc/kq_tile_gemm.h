@@ -1,0 +1,528 @@
+// Persistent 256x256 fp8 / int8 MFMA tile engine for gfx950.
+//
+//   D[m, n] = sum_k X[m, k] * W[n, k]        (X: activation rows, W: weight rows,
+//                                            both K-contiguous bytes)
+//
+// Used by the grouped block-FP8 MoE expert GEMMs, the dense block-FP8 linear
+// and the W8A8 (FP8 / INT8) prefill GEMMs.
+//
+// Work decomposition
+//   * Tiles of 256 activation rows x 256 weight rows.  The grid is persistent
+//     (one 512-thread workgroup per CU).  Workgroup b runs on XCD b % 8; XCD x
+//     owns the contiguous slice [x*T/8, (x+1)*T/8) of the T tiles, walked by
+//     its workgroups in order, so the 32 tiles an XCD has in flight are
+//     neighbours: the column tiles of one row tile (shared activation rows)
+//     and the row tiles of one expert / column range (shared weight rows) meet
+//     in that XCD's L2.  T may come from device memory (MoE: the number of
+//     row tiles the routing produced), so the host launches no empty tiles.
+//   * Eight waves: wn = wave / 4 owns 128 weight rows (8 blocks of 16),
+//     wm = wave % 4 owns 64 activation rows (4 blocks of 16).  Weights are the
+//     MFMA A operand and activations the B operand, so a lane's four results
+//     are four consecutive output columns of one row: one activation scale and
+//     one weight scale cover all four (one multiply per 16x16 block and K
+//     block for block scaling), and stores are 8 bytes wide.
+//
+// Memory pipeline
+//   K advances in 128-byte blocks.  W and X blocks (32 KB each) move global ->
+//   LDS with buffer_load ... lds (no registers), double-buffered: block kb+1
+//   is in flight while kb is multiplied.  Rows are 128 bytes in LDS, their
+//   16-byte chunks permuted by an XOR of row bits chosen per operand pattern
+//   (measured with ds_read_b128 on gfx950: FP8 lanes read chunk pairs
+//   (2g, 2g+1) of 16 rows -> c ^ (r & 7) ^ ((r >> 3) & 1); INT8 lanes read
+//   chunks g and 4+g -> c ^ ((r >> 1) & 7); both run at the conflict-free
+//   rate, where c ^ (r & 7) alone costs 1.7x).  A DMA lane writes LDS slot
+//   M0 + 16 * lane, so each lane fetches the global chunk that belongs in its
+//   slot.
+//
+// Numerics
+//   FP8, block scales : per K block t = mfma(Wq, Xq) (exact e4m3 products, fp32
+//                       sums), acc = fma(t, xs[m, kb] * ws[n/128, kb], acc).
+//   FP8, plain        : acc accumulates in the MFMA; the epilogue applies
+//                       ((acc * xs[m]) * ws[n]) (+ bias) with separate roundings.
+//   INT8              : int32 accumulation, exact; same epilogue on fp32(acc).
+#pragma once
+
+#include "kq_common.h"
+
+namespace kq {
+
+constexpr int kTgBM = 256;        // activation rows per tile
+constexpr int kTgBN = 256;        // weight rows per tile
+constexpr int kTgBK = 128;        // K bytes per pipeline stage (one block-scale block)
+constexpr int kTgThreads = 512;
+constexpr int kTgMaxKB = 128;     // K <= 16384 for block scaling (weight scale rows in LDS)
+constexpr int32_t kTgOob = (int32_t)0x80000000u;  // buffer offset past every resource: reads 0
+
+enum { kTgFp8 = 0, kTgI8 = 1 };
+enum { kTgEpiStore = 0, kTgEpiSwiGluQuant = 1 };
+
+// LDS map (bytes)
+constexpr int kTgLdsW = 0;                                // 2 stages x 256 weight rows x 128
+constexpr int kTgLdsX = kTgLdsW + 2 * kTgBN * kTgBK;      // 2 stages x 256 activation rows x 128
+constexpr int kTgLdsXs = kTgLdsX + 2 * kTgBM * kTgBK;     // 2 stages x 256 activation block scales
+constexpr int kTgLdsWs = kTgLdsXs + 2 * kTgBM * 4;        // 2 tiles x 2 weight-scale rows x kTgMaxKB
+constexpr int kTgLdsRed = kTgLdsWs + 4 * kTgMaxKB * 4;    // 2 x 256 row maxima (SwiGLU quant)
+constexpr int kTgLdsEpi = kTgLdsRed + 2 * kTgBM * 4;      // 2 tiles x {row scale, column scale, bias} x 256
+constexpr int kTgLdsBytes = kTgLdsEpi + 2 * 3 * 256 * 4;
+
+struct TileGemmArgs {
+  // activations (MFMA B operand)
+  const uint8_t* x;          // [x_rows][K]
+  int x_rows;                // rows addressable through x (buffer bound)
+  const float* xs;           // block scaling: [x_rows][ceil(K/128)]; otherwise per-row scale [M]
+  const int32_t* gather;     // tile row -> flat routed row (source row = flat / topk); null: identity
+  int topk;
+  // weights (MFMA A operand)
+  const uint8_t* w;          // [E][N][K]
+  const float* ws;           // block scaling: [E][ceil(N/128)][K/128]; otherwise [N] or [1]
+  int ws_per_channel;
+  // tiles: row tile i covers rows [row0, row_end) of expert e
+  const int32_t* mtile_table;   // [mtiles][4] (expert, first row, end row, 0); null: dense rows 256*i
+  const int32_t* mtile_count;   // device count of row tiles in use; null: mtiles
+  int mtiles, ntiles;
+  int M;                     // dense row count (mtile_table == null)
+  int N, K, I;               // weight rows, K bytes, activation width I (SwiGLU: N = 2I)
+  // epilogue
+  void* out;                 // [rows][N] in out_dtype
+  int out_dtype;
+  const void* bias;          // [N] or null
+  int bias_dtype;
+  int32_t* acc_out;          // INT8: raw int32 accumulators [M][N] or null
+  uint8_t* actq;             // SwiGLU: e4m3 activations [rows][I]
+  float* acts;               // SwiGLU: their 1x128 block scales [rows][I/128]
+};
+
+// physical 16-byte chunk of logical chunk c in LDS row r (an involution)
+template <int FMT>
+KQ_DEV int tg_chunk(int r, int c) {
+  if constexpr (FMT == kTgFp8) return c ^ (r & 7) ^ ((r >> 3) & 1);
+  else return c ^ ((r >> 1) & 7);
+}
+
+KQ_DEV void tg_dma16(i32x4 rsrc, uint32_t lds, int32_t voff, int32_t soff) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+               ::"s"(lds), "v"(voff), "s"(rsrc), "s"(soff) : "memory", "m0");
+}
+KQ_DEV void tg_dma4(i32x4 rsrc, uint32_t lds, int32_t voff, int32_t soff) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, %3 offen lds"
+               ::"s"(lds), "v"(voff), "s"(rsrc), "s"(soff) : "memory", "m0");
+}
+
+KQ_DEV float tg_round_act(float v, int dtype) {
+  if (dtype == KQ_DTYPE_BF16) return (float)(__bf16)v;
+  return (float)(_Float16)v;
+}
+
+KQ_DEV uint16_t tg_to_out(float v, int dtype) {
+  if (dtype == KQ_DTYPE_BF16) return __builtin_bit_cast(uint16_t, (__bf16)v);
+  return __builtin_bit_cast(uint16_t, (_Float16)v);
+}
+
+// Correctly rounded v / s from r = RN(1 / s): q0 = RN(v r) is within one ulp
+// of v / s, and one fma-computed remainder step rounds it correctly
+// (Markstein's theorem; finite, non-underflowing quotients).
+KQ_DEV float tg_div(float v, float s, float r) {
+  const float q0 = v * r;
+  const float e = fmaf(-q0, s, v);
+  return fmaf(e, r, q0);
+}
+
+// Four e4m3 bytes of v[0..3] (|v| <= 448), little-endian in one word.
+KQ_DEV uint32_t tg_pack_e4m3(float v0, float v1, float v2, float v3) {
+  int w = __builtin_amdgcn_cvt_pk_fp8_f32(v0, v1, 0, false);
+  w = __builtin_amdgcn_cvt_pk_fp8_f32(v2, v3, w, true);
+  return (uint32_t)w;
+}
+
+template <int FMT> struct TgTraits;
+template <> struct TgTraits<kTgFp8> { using Acc = f32x4; };
+template <> struct TgTraits<kTgI8> { using Acc = i32x4; };
+
+// Operand fragment of one 16-row block: FP8 uses chunks 2g, 2g+1 (32 bytes of
+// K 32g..32g+31 for the 16x16x128 MFMA); INT8 uses chunk g (K 16g..) for the
+// first 16x16x64 MFMA and chunk 4+g for the second.
+struct TgFrag {
+  i32x4 lo, hi;
+};
+
+KQ_DEV TgFrag tg_load(const uint8_t* blk, int off_lo, int off_hi) {
+  TgFrag f;
+  f.lo = *(const i32x4*)(blk + off_lo);
+  f.hi = *(const i32x4*)(blk + off_hi);
+  return f;
+}
+
+// Wave-uniform description of one tile.
+struct TgTile {
+  int e, row0, row_end, ntile;
+};
+
+template <int FMT, bool BLOCK, int EPI>
+__global__ void __launch_bounds__(kTgThreads)
+tile_gemm_kernel(TileGemmArgs a) {
+  using Acc = typename TgTraits<FMT>::Acc;
+  __shared__ __attribute__((aligned(16))) uint8_t smem[kTgLdsBytes];
+  const int lane = lane_id();
+  const int wave = __builtin_amdgcn_readfirstlane(wave_id());
+  const int wn = wave >> 2, wm = wave & 3;
+  const int lr = lane & 15, lg = lane >> 4;
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)smem;
+  const int K = a.K;
+  const int KB = (K + kTgBK - 1) / kTgBK;
+  const int ktail = K - (KB - 1) * kTgBK;  // bytes of K in the last block (16..128)
+  const int NB = (a.N + 127) / 128;
+
+  const int mt_used = a.mtile_count ? __builtin_amdgcn_readfirstlane(*a.mtile_count) : a.mtiles;
+  const int total = min(mt_used, a.mtiles) * a.ntiles;
+  const int xcd = blockIdx.x & 7, per = gridDim.x >> 3, slot = blockIdx.x >> 3;
+  const int t_lo = (int)((int64_t)total * xcd / 8), t_hi = (int)((int64_t)total * (xcd + 1) / 8);
+  int t = t_lo + slot;
+  if (t >= t_hi) return;
+
+  const i32x4 rx = make_rsrc(a.x, (uint32_t)((uint64_t)a.x_rows * K));
+  const i32x4 rxs = make_rsrc(a.xs, BLOCK ? (uint32_t)((uint64_t)a.x_rows * KB * 4) : 0u);
+  const i32x4 rtab = make_rsrc(a.mtile_table, a.mtile_table ? (uint32_t)a.mtiles * 16u : 0u);
+
+  // lane-constant parts of the operand reads: row lr of a 16-row block
+  const int o_lo = lr * kTgBK + (tg_chunk<FMT>(lr, FMT == kTgFp8 ? 2 * lg : lg) << 4);
+  const int o_hi = lr * kTgBK + (tg_chunk<FMT>(lr, FMT == kTgFp8 ? 2 * lg + 1 : 4 + lg) << 4);
+
+  float* sRed = (float*)(smem + kTgLdsRed);
+
+  // ---- tile metadata.  A row tile's table entry is (expert, first row, end
+  // row, 0); lane l < 3 of a table word holds entry word l.
+  auto load_tab = [&](int tt) -> int {
+    if (!a.mtile_table) return 0;
+    return kq_rbl_i32(rtab, (4 * (tt / a.ntiles) + (lane & 3)) * 4, 0, 0);
+  };
+  auto tile_of = [&](int tt, int tab) -> TgTile {
+    TgTile r;
+    r.ntile = tt % a.ntiles;
+    if (a.mtile_table) {
+      r.e = __builtin_amdgcn_readlane(tab, 0);
+      r.row0 = __builtin_amdgcn_readlane(tab, 1);
+      r.row_end = __builtin_amdgcn_readlane(tab, 2);
+    } else {
+      r.e = 0;
+      r.row0 = (tt / a.ntiles) * kTgBM;
+      r.row_end = min(a.M, r.row0 + kTgBM);
+    }
+    return r;
+  };
+  // the two 128-row weight-scale blocks a tile spans: SwiGLU the gate and the
+  // up block of activation columns ntile*128; otherwise n0/128 and the next
+  auto scale_block = [&](const TgTile& tl, int half) -> int {
+    if constexpr (EPI == kTgEpiSwiGluQuant) return half ? (a.I + tl.ntile * 128) / 128 : tl.ntile;
+    else return min(tl.ntile * 2 + half, NB - 1);
+  };
+
+  // ---- per-tile loads (row sources, weight scales), issued one tile ahead
+  int pf_src[4], pf_xsrc = -1;
+  float pf_ws = 0.0f, pf_exs = 1.0f, pf_ews = 1.0f, pf_eb = 0.0f;
+  auto prefetch = [&](const TgTile& tl) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = tl.row0 + (((wave * 4 + i) * 64 + lane) >> 3);
+      pf_src[i] = r < tl.row_end ? (a.gather ? a.gather[r] : r) : -1;
+    }
+    if (BLOCK && wave < 4) {  // LDS scale float p holds tile row (p % 16) * 16 + p / 16
+      const int p = wave * 64 + lane;
+      const int r = tl.row0 + (p & 15) * 16 + (p >> 4);
+      pf_xsrc = r < tl.row_end ? (a.gather ? a.gather[r] : r) : -1;
+    }
+    if (BLOCK && (int)threadIdx.x < 2 * KB) {
+      const int half = (int)threadIdx.x >= KB;
+      const int kb = (int)threadIdx.x - half * KB;
+      pf_ws = a.ws[((int64_t)tl.e * NB + scale_block(tl, half)) * KB + kb];
+    }
+    if (EPI == kTgEpiStore && threadIdx.x < 256) {
+      // epilogue constants of tile row / column t: loaded here, one tile
+      // ahead, so the epilogue issues no global loads between its stores
+      // (loads and stores share vmcnt: a load would wait for every store)
+      const int t = (int)threadIdx.x, r = tl.row0 + t, n = min(tl.ntile * kTgBN + t, a.N - 1);
+      if (!BLOCK) {
+        pf_exs = r < tl.row_end ? a.xs[r] : 0.0f;
+        pf_ews = a.ws_per_channel ? a.ws[n] : a.ws[0];
+      }
+      if (a.bias_dtype != KQ_DTYPE_NONE) pf_eb = load_as_f32(a.bias, a.bias_dtype, n);
+    }
+  };
+
+  // ---- DMA state of the tile being loaded
+  i32x4 rw;
+  int32_t w_off[4], x_off[4], xs_off = kTgOob;
+  auto set_offsets = [&](const TgTile& tl) {
+    rw = make_rsrc(a.w + (int64_t)tl.e * a.N * K, (uint32_t)((uint64_t)a.N * K));
+    // this wave fills 1 KB blocks 4*wave+i of each 32 KB stage; slot
+    // p = block*64 + lane is row p/8, physical chunk p%8
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int p = (wave * 4 + i) * 64 + lane, row = p >> 3;
+      const int c = tg_chunk<FMT>(row, p & 7);
+      int n;
+      if constexpr (EPI == kTgEpiSwiGluQuant) {
+        // wave half wn: blocks j < 4 gate rows, j >= 4 up rows of activation
+        // columns ntile*128 + 64*wn + 16*(j&3) + (row&15)
+        const int j = (row >> 4) & 7;
+        const int col = tl.ntile * 128 + 64 * (row >> 7) + 16 * (j & 3) + (row & 15);
+        n = j < 4 ? col : a.I + col;
+      } else {
+        n = tl.ntile * kTgBN + row;
+      }
+      w_off[i] = n < a.N ? n * K + c * 16 : kTgOob;
+      x_off[i] = pf_src[i] >= 0 ? (pf_src[i] / a.topk) * K + c * 16 : kTgOob;
+    }
+    if (BLOCK && wave < 4) xs_off = pf_xsrc >= 0 ? (pf_xsrc / a.topk) * KB * 4 : kTgOob;
+  };
+  auto stage_ws = [&](int buf) {
+    if (BLOCK && (int)threadIdx.x < 2 * KB)
+      ((float*)(smem + kTgLdsWs))[buf * 2 * kTgMaxKB + (int)threadIdx.x] = pf_ws;
+    if (EPI == kTgEpiStore && threadIdx.x < 256) {
+      float* e = (float*)(smem + kTgLdsEpi) + buf * 3 * 256 + (int)threadIdx.x;
+      e[0] = pf_exs;
+      e[256] = pf_ews;
+      e[512] = pf_eb;
+    }
+  };
+  auto issue = [&](int kb, int st) {
+    const uint32_t lw = lds0 + kTgLdsW + st * (kTgBN * kTgBK) + wave * 4096;
+    const uint32_t lx = lds0 + kTgLdsX + st * (kTgBM * kTgBK) + wave * 4096;
+    const int soff = kb * kTgBK;
+    if (kb == KB - 1 && ktail < kTgBK) {
+      // ragged last block: chunks past K read zeros (K % 16 == 0)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int row = (wave * 4 + i) * 8 + (lane >> 3);
+        const bool ok = tg_chunk<FMT>(row, lane & 7) * 16 < ktail;
+        tg_dma16(rw, lw + i * 1024, ok ? w_off[i] : kTgOob, soff);
+        tg_dma16(rx, lx + i * 1024, ok ? x_off[i] : kTgOob, soff);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        tg_dma16(rw, lw + i * 1024, w_off[i], soff);
+        tg_dma16(rx, lx + i * 1024, x_off[i], soff);
+      }
+    }
+    if (BLOCK && wave < 4) tg_dma4(rxs, lds0 + kTgLdsXs + st * (kTgBM * 4) + wave * 256, xs_off, kb * 4);
+  };
+
+  // ---- first tile: synchronous set-up
+  TgTile cur = tile_of(t, load_tab(t));
+  prefetch(cur);
+  set_offsets(cur);
+  int buf = 0, st = 0;
+  stage_ws(buf);
+  issue(0, st);
+  int tn = t + per;
+  int pf_tab = tn < t_hi ? load_tab(tn) : 0;
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+
+  while (true) {
+    const bool has_next = tn < t_hi;
+    TgTile nxt = cur;
+    if (has_next) {
+      // the next tile's row sources and weight scales load under this tile's
+      // K loop; the table word of the tile after it as well
+      nxt = tile_of(tn, pf_tab);
+      prefetch(nxt);
+      if (tn + per < t_hi) pf_tab = load_tab(tn + per);
+    }
+    int wslot = 0;  // block scaling: staged weight-scale row of this wave's blocks j < 4
+    if (BLOCK && EPI != kTgEpiSwiGluQuant) wslot = wn;
+    const float* sWs = (const float*)(smem + kTgLdsWs) + buf * 2 * kTgMaxKB;
+
+    Acc acc[8][4];
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+#pragma unroll
+      for (int mb = 0; mb < 4; ++mb) acc[j][mb] = Acc{0, 0, 0, 0};
+
+    for (int kb = 0; kb < KB; ++kb) {
+      if (kb + 1 < KB) issue(kb + 1, st ^ 1);
+      const uint8_t* sW = smem + kTgLdsW + st * (kTgBN * kTgBK) + (128 * wn) * kTgBK;
+      const uint8_t* sX = smem + kTgLdsX + st * (kTgBM * kTgBK) + (64 * wm) * kTgBK;
+      float prod[2][4];
+      if constexpr (BLOCK) {
+        const f32x4 sx = *(const f32x4*)(smem + kTgLdsXs + st * (kTgBM * 4) + (lr * 16 + 4 * wm) * 4);
+        if constexpr (EPI == kTgEpiSwiGluQuant) {
+          const float s0 = sWs[kb], s1 = sWs[KB + kb];
+#pragma unroll
+          for (int mb = 0; mb < 4; ++mb) {
+            prod[0][mb] = sx[mb] * s0;
+            prod[1][mb] = sx[mb] * s1;
+          }
+        } else {
+          const float s0 = sWs[wslot * KB + kb];
+#pragma unroll
+          for (int mb = 0; mb < 4; ++mb) prod[0][mb] = prod[1][mb] = sx[mb] * s0;
+        }
+      }
+      TgFrag xf[4];
+#pragma unroll
+      for (int mb = 0; mb < 4; ++mb) xf[mb] = tg_load(sX + mb * 16 * kTgBK, o_lo, o_hi);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const TgFrag wf = tg_load(sW + j * 16 * kTgBK, o_lo, o_hi);
+#pragma unroll
+        for (int mb = 0; mb < 4; ++mb) {
+          if constexpr (FMT == kTgI8) {
+            acc[j][mb] = mfma_i8(wf.lo, xf[mb].lo, acc[j][mb]);
+            acc[j][mb] = mfma_i8(wf.hi, xf[mb].hi, acc[j][mb]);
+          } else {
+            const i32x8 A = i32x8{wf.lo[0], wf.lo[1], wf.lo[2], wf.lo[3], wf.hi[0], wf.hi[1], wf.hi[2], wf.hi[3]};
+            const i32x8 B = i32x8{xf[mb].lo[0], xf[mb].lo[1], xf[mb].lo[2], xf[mb].lo[3],
+                                  xf[mb].hi[0], xf[mb].hi[1], xf[mb].hi[2], xf[mb].hi[3]};
+            if constexpr (BLOCK) {
+              const f32x4 blk = mfma_fp8(A, B, f32x4{0.f, 0.f, 0.f, 0.f});
+              const float sc = prod[j >> 2][mb];
+#pragma unroll
+              for (int q = 0; q < 4; ++q) acc[j][mb][q] = fmaf(blk[q], sc, acc[j][mb][q]);
+            } else {
+              acc[j][mb] = mfma_fp8(A, B, acc[j][mb]);
+            }
+          }
+        }
+      }
+      __builtin_amdgcn_s_waitcnt(0);  // this wave's copies of the next block have landed
+      __syncthreads();                 // ... and everyone's; stage st is free again
+      st ^= 1;
+    }
+
+    if (has_next) {
+      // the next tile's first K block loads while this tile's epilogue runs
+      set_offsets(nxt);
+      stage_ws(buf ^ 1);
+      issue(0, st);
+    }
+
+    // ------------------------------------------------------------ epilogue
+    // lane holds rows m = 64*wm + 16*mb + lr, columns 128*wn + 16*j + 4*lg + q
+    const int row0 = cur.row0, row_end = cur.row_end, ntile = cur.ntile;
+    if constexpr (EPI == kTgEpiSwiGluQuant) {
+      // SwiGLU rounded to the activation dtype at each step (as torch does for
+      // bf16 / fp16 tensors), then 1x128 e4m3 quantization of the tile's 128
+      // activation columns: s = max(amax, 1e-12) / 448, q = e4m3(clamp(v / s)).
+      float amax[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const float g = tg_round_act(acc[j][mb][q], a.out_dtype);
+            const float u = tg_round_act(acc[j + 4][mb][q], a.out_dtype);
+            const float sl = tg_round_act(g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)), a.out_dtype);
+            const float v = tg_round_act(sl * u, a.out_dtype);
+            acc[j][mb][q] = v;
+            amax[mb] = fmaxf(amax[mb], fabsf(v));
+          }
+#pragma unroll
+      for (int mb = 0; mb < 4; ++mb) {
+        amax[mb] = fmaxf(amax[mb], __shfl_xor(amax[mb], 16, 64));
+        amax[mb] = fmaxf(amax[mb], __shfl_xor(amax[mb], 32, 64));
+        if (lg == 0) sRed[wn * kTgBM + 64 * wm + 16 * mb + lr] = amax[mb];
+      }
+      __syncthreads();
+      const int IB = a.I / 128;
+#pragma unroll
+      for (int mb = 0; mb < 4; ++mb) {
+        const int lrow = 64 * wm + 16 * mb + lr;
+        const int grow = row0 + lrow;
+        if (grow >= row_end) continue;
+        const float am = fmaxf(sRed[lrow], sRed[kTgBM + lrow]);
+        const float s = __fdiv_rn(fmaxf(am, 1e-12f), 448.0f);
+        const float rs = __fdiv_rn(1.0f, s);
+        uint8_t* dst = a.actq + (int64_t)grow * a.I + ntile * 128 + 64 * wn + 4 * lg;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          float v[4];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) v[q] = fminf(fmaxf(tg_div(acc[j][mb][q], s, rs), -448.0f), 448.0f);
+          *(uint32_t*)(dst + 16 * j) = tg_pack_e4m3(v[0], v[1], v[2], v[3]);
+        }
+        if (wn == 0 && lg == 0) a.acts[(int64_t)grow * IB + ntile] = s;
+      }
+    } else {
+      const bool vec_ok = (a.N & 3) == 0;
+      const float* eX = (const float*)(smem + kTgLdsEpi) + buf * 3 * 256;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int nl = 128 * wn + 16 * j + 4 * lg;  // tile column of q = 0
+        const int n = ntile * kTgBN + nl;
+        if (n >= a.N) continue;
+        const f32x4 wsc = *(const f32x4*)(eX + 256 + nl);
+        const f32x4 bv = *(const f32x4*)(eX + 512 + nl);
+#pragma unroll
+        for (int mb = 0; mb < 4; ++mb) {
+          const int grow = row0 + 64 * wm + 16 * mb + lr;
+          if (grow >= row_end) continue;
+          const float xsc = eX[64 * wm + 16 * mb + lr];
+          uint16_t o[4];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            float v = (float)acc[j][mb][q];
+            if (!BLOCK) v = __fmul_rn(__fmul_rn(v, xsc), wsc[q]);
+            if (a.bias_dtype != KQ_DTYPE_NONE) v = __fadd_rn(v, bv[q]);
+            o[q] = tg_to_out(v, a.out_dtype);
+          }
+          uint16_t* dst = (uint16_t*)a.out + (int64_t)grow * a.N + n;
+          if (vec_ok) {
+            *(u32x2*)dst = u32x2{(uint32_t)o[0] | ((uint32_t)o[1] << 16), (uint32_t)o[2] | ((uint32_t)o[3] << 16)};
+          } else {
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+              if (n + q < a.N) dst[q] = o[q];
+          }
+          if constexpr (FMT == kTgI8) {
+            if (a.acc_out) {
+              int32_t* ad = a.acc_out + (int64_t)grow * a.N + n;
+              if (vec_ok) {
+                *(i32x4*)ad = acc[j][mb];
+              } else {
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                  if (n + q < a.N) ad[q] = acc[j][mb][q];
+              }
+            }
+          }
+        }
+      }
+    }
+    if (!has_next) break;
+    __builtin_amdgcn_s_waitcnt(0);  // the next tile's first block has landed
+    __syncthreads();
+    cur = nxt;
+    buf ^= 1;
+    tn += per;
+  }
+}
+
+// ------------------------------------------------------------------ host
+static inline int tg_device_cus() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) dev = 0;
+  const int slot = dev & 63;
+  if (cached[slot] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      n = 256;
+    cached[slot] = n;
+  }
+  return cached[slot];
+}
+
+// Persistent launch: one workgroup per CU (never more than the tiles), a
+// multiple of 8 so every XCD gets the same number of workgroups.
+template <int FMT, bool BLOCK, int EPI>
+static void tg_launch(const TileGemmArgs& a, hipStream_t stream) {
+  const int64_t max_total = (int64_t)a.mtiles * a.ntiles;
+  int64_t grid = max_total < tg_device_cus() ? max_total : tg_device_cus();
+  grid = (grid + 7) / 8 * 8;
+  hipLaunchKernelGGL((tile_gemm_kernel<FMT, BLOCK, EPI>), dim3((unsigned)grid), dim3(kTgThreads), 0,
+                     stream, a);
+}
+
+}  // namespace kq

@@ -8,15 +8,19 @@
 //   FP8 : acc (fp32) * xscale[m] * wscale[n or 0] (+ bias[n])
 //         (kairyu/quant/fp8.py:48-56, linear.py:463-469).
 //
-// Two kernels:
+// Kernels:
 //   * skinny (M <= 64): a workgroup owns 16 output columns; its 8 waves split
 //     K, stream weight rows straight into MFMA B-operand registers and reduce
 //     through LDS.  Small-N shapes also split K across workgroups, finished
 //     by a separate reduce kernel (no inter-workgroup sync).  HBM-bound.
-//   * tiled (M > 64): 128x128x128 workgroup tiles, 4 waves of 64x64, LDS
-//     double buffer with an XOR chunk swizzle.  MFMA-bound.
+//   * M > 64 with at least one 256x256 tile per CU: the persistent tile
+//     engine of kq_tile_gemm.h (LDS DMA double buffering, XCD-grouped tiles).
+//   * other M > 64: 128x128x128 workgroup tiles, 4 waves of 64x64, LDS
+//     double buffer with an XOR chunk swizzle (twice the workgroups of the
+//     256x256 engine for shapes that would leave CUs idle).
 #include "kq_common.h"
 #include "kq_splitk.h"
+#include "kq_tile_gemm.h"
 
 namespace kq {
 
@@ -406,7 +410,21 @@ static int run_w8a8(const char* what, const uint8_t* xq, const uint8_t* w, int64
   if (m <= 16) launch_skinny<FMT, 1>(xq, w, K, ep, workspace, ws_bytes, stream);
   else if (m <= 32) launch_skinny<FMT, 2>(xq, w, K, ep, workspace, ws_bytes, stream);
   else if (m <= 64) launch_skinny<FMT, 4>(xq, w, K, ep, workspace, ws_bytes, stream);
-  else {
+  else if (m * k < ((int64_t)1 << 31) && n * k < ((int64_t)1 << 31) &&
+           ((m + kTgBM - 1) / kTgBM) * ((n + kTgBN - 1) / kTgBN) >= tg_device_cus()) {
+    // persistent 256x256 MFMA tiles (kq_tile_gemm.h), scales in the epilogue;
+    // shapes with fewer 256x256 tiles than CUs keep the 128x128 kernel below
+    TileGemmArgs a{};
+    a.x = xq; a.x_rows = (int)m; a.xs = ep.xscale; a.gather = nullptr; a.topk = 1;
+    a.w = w; a.ws = ep.wscale; a.ws_per_channel = ep.ws_per_channel;
+    a.mtile_table = nullptr; a.mtile_count = nullptr;
+    a.M = (int)m; a.N = (int)n; a.K = K; a.I = 0;
+    a.mtiles = (int)((m + kTgBM - 1) / kTgBM);
+    a.ntiles = (int)((n + kTgBN - 1) / kTgBN);
+    a.out = ep.out; a.out_dtype = ep.out_dtype; a.bias = ep.bias; a.bias_dtype = ep.bias_dtype;
+    a.acc_out = ep.acc_out;
+    tg_launch<FMT == kFmtI8 ? kTgI8 : kTgFp8, false, kTgEpiStore>(a, stream);
+  } else {
     const int tiles_m = (int)((m + kTile - 1) / kTile);
     const int tiles_n = (int)((n + kTile - 1) / kTile);
     hipLaunchKernelGGL(w8a8_tile_kernel<FMT>, dim3(tiles_m * tiles_n), dim3(256), 0, stream, xq,
