@@ -6,6 +6,15 @@
 // the reference's CPU oracle exactly (kairyu/quant/int8.py:25-30,
 // kairyu/quant/fp8.py:33-45): fp32 amax, IEEE division for the scale and for
 // x/scale, round-half-even for INT8, RNE e4m3 after a +-448 clamp for FP8.
+//
+// Rows of finite values divide by one correctly rounded reciprocal per row
+// plus an fma remainder step (div_by_recip: the IEEE quotient for every
+// element that does not quantize to zero) and convert with v_cvt_pk_fp8_f32;
+// rows holding inf / NaN, or static scales below 2^-60, take the
+// per-element IEEE path.  The row amax is an integer max of |bits|: it
+// orders inf and NaN above every finite magnitude, so it is the float amax of
+// a finite row, inf for a row with inf, and NaN for a row with NaN (torch's
+// amax and clamp propagate NaN into the scale).
 #include "kq_common.h"
 
 #include <algorithm>
@@ -32,6 +41,28 @@ KQ_DEV void load8_f32(const uint16_t* row, int64_t i, int64_t k, int dtype, bool
       v[j] = c < k ? (dtype == KQ_DTYPE_BF16 ? bf16_to_f32(row[c]) : f16_to_f32(row[c])) : 0.0f;
     }
   }
+}
+
+KQ_DEV uint32_t block_max_u32(uint32_t v, uint32_t* red) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v = max(v, (uint32_t)__shfl_xor((int)v, off, 64));
+  if (lane_id() == 0) red[wave_id()] = v;
+  __syncthreads();
+  uint32_t r = red[0];
+  for (int w = 1; w < (int)(blockDim.x >> 6); ++w) r = max(r, red[w]);
+  __syncthreads();
+  return r;
+}
+
+// max |bits| over the row held in registers (finite rows: the bits of the amax)
+template <int NCH>
+KQ_DEV uint32_t row_abs_bits(float v[NCH][8]) {
+  uint32_t m = 0;
+#pragma unroll
+  for (int c = 0; c < NCH; ++c)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) m = max(m, __float_as_uint(v[c][e]) & 0x7fffffffu);
+  return m;
 }
 
 KQ_DEV float block_max(float v, float* red) {
@@ -94,8 +125,11 @@ act_quant_i8_kernel(const uint16_t* __restrict__ x, int dtype, int64_t k, int64_
   __shared__ float red[16];
   const int64_t r = blockIdx.x;
   float v[NCH][8];
-  float amax = block_max(load_row_regs<NCH>(x + r * ldx, k, dtype, vec_ok, v), red);
-  const float s = __fdiv_rn(fmaxf(amax, 1e-12f), 127.0f);
+  load_row_regs<NCH>(x + r * ldx, k, dtype, vec_ok, v);
+  const uint32_t abits = block_max_u32(row_abs_bits<NCH>(v), (uint32_t*)red);
+  const bool fast = abits < 0x7f800000u;
+  const float s = __fdiv_rn(max_keep_nan(__uint_as_float(abits), 1e-12f), 127.0f);
+  const float rs = __fdiv_rn(1.0f, s);
 #pragma unroll
   for (int c = 0; c < NCH; ++c) {
     const int64_t i = ((int64_t)threadIdx.x + (int64_t)blockDim.x * c) * 8;
@@ -103,7 +137,8 @@ act_quant_i8_kernel(const uint16_t* __restrict__ x, int dtype, int64_t k, int64_
     uint32_t packed[2] = {0u, 0u};
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      const float q = __builtin_rintf(clamp_keep_nan(__fdiv_rn(v[c][e], s), 127.0f));
+      const float q = fast ? __builtin_rintf(fminf(fmaxf(div_by_recip(v[c][e], s, rs), -127.0f), 127.0f))
+                           : __builtin_rintf(clamp_keep_nan(__fdiv_rn(v[c][e], s), 127.0f));
       packed[e >> 2] |= ((uint32_t)(int32_t)q & 0xffu) << (8 * (e & 3));
     }
     store8((uint8_t*)xq + r * k, i, k, packed[0], packed[1]);
@@ -119,19 +154,35 @@ act_quant_fp8_kernel(const uint16_t* __restrict__ x, int dtype, int64_t k, int64
   __shared__ float red[16];
   const int64_t r = blockIdx.x;
   float v[NCH][8];
-  const float amax = load_row_regs<NCH>(x + r * ldx, k, dtype, vec_ok, v);
+  load_row_regs<NCH>(x + r * ldx, k, dtype, vec_ok, v);
+  const uint32_t abits = block_max_u32(row_abs_bits<NCH>(v), (uint32_t*)red);
+  bool fast = abits < 0x7f800000u;
   float s;
-  if (scale_mode == 0) s = __fdiv_rn(fmaxf(block_max(amax, red), 1e-12f), 448.0f);
-  else if (scale_mode == 1) s = scale_in[0];
-  else s = scale_in[r];
+  if (scale_mode == 0) {
+    s = __fdiv_rn(max_keep_nan(__uint_as_float(abits), 1e-12f), 448.0f);
+  } else {
+    s = scale_mode == 1 ? scale_in[0] : scale_in[r];
+    fast = fast && s >= 0x1p-60f && s <= 3.4028235e38f;
+  }
+  const float rs = __fdiv_rn(1.0f, s);
 #pragma unroll
   for (int c = 0; c < NCH; ++c) {
     const int64_t i = ((int64_t)threadIdx.x + (int64_t)blockDim.x * c) * 8;
     if (i >= k) break;
     uint32_t packed[2] = {0u, 0u};
+    if (fast) {
 #pragma unroll
-    for (int e = 0; e < 8; ++e)
-      packed[e >> 2] |= f32_to_e4m3(clamp_keep_nan(__fdiv_rn(v[c][e], s), 448.0f)) << (8 * (e & 3));
+      for (int h = 0; h < 2; ++h) {
+        float q[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) q[e] = fminf(fmaxf(div_by_recip(v[c][4 * h + e], s, rs), -448.0f), 448.0f);
+        packed[h] = pack4_e4m3(q[0], q[1], q[2], q[3]);
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        packed[e >> 2] |= f32_to_e4m3(clamp_keep_nan(__fdiv_rn(v[c][e], s), 448.0f)) << (8 * (e & 3));
+    }
     store8(xq + r * k, i, k, packed[0], packed[1]);
   }
   if (threadIdx.x == 0) xscale[r] = s;

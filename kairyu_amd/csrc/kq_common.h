@@ -91,6 +91,32 @@ KQ_DEV uint32_t f32_to_e4m3(float v) {
   return sign | (e << 3) | m;
 }
 
+// Four e4m3 bytes of v0..v3 (little-endian) with the hardware converter
+// (v_cvt_pk_fp8_f32: round to nearest even, OCP e4m3fn).  Bit-identical to
+// f32_to_e4m3 for every |v| <= 448 (checked on gfx950 over all such fp32
+// values); callers clamp to +-448 and keep NaN away from it.
+KQ_DEV uint32_t pack4_e4m3(float v0, float v1, float v2, float v3) {
+  int w = __builtin_amdgcn_cvt_pk_fp8_f32(v0, v1, 0, false);
+  w = __builtin_amdgcn_cvt_pk_fp8_f32(v2, v3, w, true);
+  return (uint32_t)w;
+}
+
+// v / s, rounded like IEEE division, from r = RN(1 / s): q0 = RN(v r) is within
+// one ulp of v / s, and one fma remainder step rounds it correctly (Markstein's
+// theorem) whenever the remainder v - q0 s is a normal float.  With
+// s >= 2^-60 that holds for every quotient of magnitude >= 2^-10, i.e. for
+// every quotient that does not quantize to zero in e4m3 or int8; copysign
+// keeps the sign of a zero dividend (-0 / s = -0).  Checked against IEEE
+// division on 2^32 random pairs on gfx950.
+KQ_DEV float div_by_recip(float v, float s, float r) {
+  const float q0 = v * r;
+  const float e = fmaf(-q0, s, v);
+  return __builtin_copysignf(fmaf(e, r, q0), v);
+}
+
+// max(amax, floor) that keeps a NaN amax (torch.clamp / numpy.maximum)
+KQ_DEV float max_keep_nan(float a, float floor) { return a != a ? a : fmaxf(a, floor); }
+
 KQ_DEV float e4m3_to_f32(uint32_t b) {
   uint32_t s = b & 0x80u, e = (b >> 3) & 0xfu, m = b & 7u;
   float v;

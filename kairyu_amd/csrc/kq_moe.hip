@@ -270,21 +270,35 @@ act_quant_fp8_blocks_kernel(const uint16_t* __restrict__ x, int dtype, int K, in
     for (int e = 0; e < 8; ++e)
       v[e] = k0 + e < K ? (dtype == KQ_DTYPE_BF16 ? bf16_to_f32(xr[k0 + e]) : f16_to_f32(xr[k0 + e])) : 0.0f;
   }
-  float amax = 0.0f;
+  // block amax as an integer max of |bits|: inf and NaN order above every
+  // finite magnitude, so a NaN in the block makes the scale NaN (torch's amax
+  // and clamp propagate it) and a non-finite block takes the IEEE path below
+  uint32_t abits = 0;
 #pragma unroll
-  for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(v[e]));
+  for (int e = 0; e < 8; ++e) abits = max(abits, __float_as_uint(v[e]) & 0x7fffffffu);
 #pragma unroll
-  for (int off = 8; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
+  for (int off = 8; off > 0; off >>= 1) abits = max(abits, (uint32_t)__shfl_xor((int)abits, off, 64));
   if (k0 >= K) return;
-  const float s = __fdiv_rn(fmaxf(amax, 1e-12f), 448.0f);
+  const float s = __fdiv_rn(max_keep_nan(__uint_as_float(abits), 1e-12f), 448.0f);
   uint32_t lo = 0, hi = 0;
+  if (abits < 0x7f800000u) {
+    // finite block: reciprocal + fma remainder (IEEE quotient wherever it
+    // matters) and the hardware e4m3 converter
+    const float rs = __fdiv_rn(1.0f, s);
+    float q[8];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    float q = __fdiv_rn(v[e], s);
-    q = q < -448.0f ? -448.0f : (q > 448.0f ? 448.0f : q);
-    const uint32_t b = f32_to_e4m3(q);
-    if (e < 4) lo |= b << (8 * e);
-    else hi |= b << (8 * (e - 4));
+    for (int e = 0; e < 8; ++e) q[e] = fminf(fmaxf(div_by_recip(v[e], s, rs), -448.0f), 448.0f);
+    lo = pack4_e4m3(q[0], q[1], q[2], q[3]);
+    hi = pack4_e4m3(q[4], q[5], q[6], q[7]);
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float q = __fdiv_rn(v[e], s);
+      q = q < -448.0f ? -448.0f : (q > 448.0f ? 448.0f : q);
+      const uint32_t b = f32_to_e4m3(q);
+      if (e < 4) lo |= b << (8 * e);
+      else hi |= b << (8 * (e - 4));
+    }
   }
   uint8_t* qr = xq + row * (int64_t)K;
   if (k0 + 8 <= K && (K % 8) == 0) {

@@ -118,21 +118,6 @@ KQ_DEV uint16_t tg_to_out(float v, int dtype) {
   return __builtin_bit_cast(uint16_t, (_Float16)v);
 }
 
-// Correctly rounded v / s from r = RN(1 / s): q0 = RN(v r) is within one ulp
-// of v / s, and one fma-computed remainder step rounds it correctly
-// (Markstein's theorem; finite, non-underflowing quotients).
-KQ_DEV float tg_div(float v, float s, float r) {
-  const float q0 = v * r;
-  const float e = fmaf(-q0, s, v);
-  return fmaf(e, r, q0);
-}
-
-// Four e4m3 bytes of v[0..3] (|v| <= 448), little-endian in one word.
-KQ_DEV uint32_t tg_pack_e4m3(float v0, float v1, float v2, float v3) {
-  int w = __builtin_amdgcn_cvt_pk_fp8_f32(v0, v1, 0, false);
-  w = __builtin_amdgcn_cvt_pk_fp8_f32(v2, v3, w, true);
-  return (uint32_t)w;
-}
 
 template <int FMT> struct TgTraits;
 template <> struct TgTraits<kTgFp8> { using Acc = f32x4; };
@@ -439,8 +424,8 @@ tile_gemm_kernel(TileGemmArgs a) {
         for (int j = 0; j < 4; ++j) {
           float v[4];
 #pragma unroll
-          for (int q = 0; q < 4; ++q) v[q] = fminf(fmaxf(tg_div(acc[j][mb][q], s, rs), -448.0f), 448.0f);
-          *(uint32_t*)(dst + 16 * j) = tg_pack_e4m3(v[0], v[1], v[2], v[3]);
+          for (int q = 0; q < 4; ++q) v[q] = fminf(fmaxf(div_by_recip(acc[j][mb][q], s, rs), -448.0f), 448.0f);
+          *(uint32_t*)(dst + 16 * j) = pack4_e4m3(v[0], v[1], v[2], v[3]);
         }
         if (wn == 0 && lg == 0) a.acts[(int64_t)grow * IB + ntile] = s;
       }

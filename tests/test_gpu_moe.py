@@ -59,6 +59,26 @@ def test_block_activation_quant_is_bit_exact(cuda, shape, dtype):
     assert np.array_equal(s.cpu().numpy().view(np.uint32), os_.view(np.uint32))
 
 
+def test_block_activation_quant_edge_values_bit_exact(cuda):
+    g = torch.Generator().manual_seed(9)
+    x = torch.randn(4, 1024, generator=g) * 5
+    x[0, :128:3] = -0.0                                  # signed zeros
+    x[0, 128:256] = torch.randn(128, generator=g) * 1e-30
+    x[0, 200] = 2.0                                      # the rest quantizes to +-0
+    x[1, :128] = torch.tensor([1.0625, -1.1875, 0.017578125, 240.0]).repeat(32)
+    x[1, 127] = 448.0                                    # s = 1: exact e4m3 ties
+    x[2, 300] = float("inf")                             # block 2 of row 2: IEEE path
+    x[3, 700] = float("nan")                             # block 5 of row 3: NaN scale
+    x[3, 900:1024] = torch.randn(124, generator=g) * 1e37
+    x = x.to(torch.bfloat16)
+    q, s = hip.quantize_activation_blocks(x.to(cuda))
+    with np.errstate(invalid="ignore", divide="ignore"):
+        oq, os_ = formats.block_fp8_quantize_rows(x.float().numpy())
+    assert np.array_equal(_bits(q), oq)
+    # scales: bit-exact where finite; any NaN where the block holds a NaN
+    np.testing.assert_array_equal(s.cpu().numpy(), os_)
+
+
 @pytest.mark.parametrize("m", [1, 17, 130])
 @pytest.mark.parametrize("n", [384, 200])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])

@@ -103,6 +103,52 @@ def test_int8_generic_k_path(cuda):
     assert np.array_equal(np32(out), expected)
 
 
+def _edge_rows(k: int, nonfinite: bool) -> torch.Tensor:
+    """Rows aimed at the quantizers' corner cases: signed zeros, values far
+    below the row amax, exact rounding ties of e4m3 (amax 448 -> s = 1) and of
+    int8 (amax 127 -> s = 1), near-max bf16 magnitudes, and (optionally) rows
+    holding +inf or NaN, which take the per-element IEEE path."""
+    g = torch.Generator().manual_seed(k)
+    x = torch.randn(8, k, generator=g)
+    x[0, ::3] = -0.0
+    x[1] = torch.randn(k, generator=g) * 1e-30
+    x[1, 0] = 1.0                      # most elements quantize to (signed) zero
+    ties8 = torch.tensor([1.0625, -1.1875, 0.017578125, -0.009765625, 240.0, 3.25, -6.5, 13.0])
+    x[2] = ties8.repeat(k // 8 + 1)[:k]
+    x[2, -1] = 448.0
+    ties_i8 = torch.tensor([2.5, -3.5, 0.5, -0.5, 126.5, -1.5, 64.5, 7.0])
+    x[3] = ties_i8.repeat(k // 8 + 1)[:k]
+    x[3, -1] = 127.0
+    x[4] = torch.randn(k, generator=g) * 1e37
+    x[5, ::7] = -0.0
+    if nonfinite:
+        x[6, k // 2] = float("inf")
+        x[7, k // 3] = float("nan")
+    return x.to(torch.bfloat16)
+
+
+@pytest.mark.parametrize("k", [1536, 14336])
+def test_fp8_activation_quantization_edge_values_bit_exact(cuda, k):
+    banner(f"fp8 act quant edge values k={k}")
+    x = _edge_rows(k, nonfinite=True)
+    q, s = hip._quantize_activation(x.to(cuda), torch.float8_e4m3fn, 448.0)
+    with np.errstate(invalid="ignore", divide="ignore"):
+        eq, es = formats.fp8_quantize_rows(np32(x))
+    assert np.array_equal(bits(q), eq)
+    # scales: bit-exact where finite; any NaN where the row holds a NaN
+    np.testing.assert_array_equal(np32(s), es)
+
+
+@pytest.mark.parametrize("k", [1536, 3584])
+def test_int8_activation_quantization_edge_values_bit_exact(cuda, k):
+    banner(f"int8 act quant edge values k={k}")
+    x = _edge_rows(k, nonfinite=False)
+    q, s = hip._quantize_activation(x.to(cuda), torch.int8, 127.0)
+    eq, es = formats.int8_quantize_rows(np32(x))
+    assert np.array_equal(bits(q), eq)
+    assert np.array_equal(np32(s), es)
+
+
 # ----------------------------------------------------------------- FP8
 @pytest.mark.parametrize("mode", ["dynamic", "static", "row"])
 def test_fp8_activation_quantization_bit_exact(cuda, mode):
