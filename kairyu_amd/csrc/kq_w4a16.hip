@@ -473,7 +473,9 @@ w4a16_skinny_kernel(W4Args a) {
 // dequantizes the packed word of column block*16 + j, packed row step*4 + kb:
 // the B operand of one v_mfma_f32_16x16x32_f16 (k order [0,4,1,5,2,6,3,7],
 // matched in A).  The 16 waves' partial sums meet in LDS and are added in
-// wave order, so results do not depend on timing.  Weights, scales and zeros
+// wave order, so results do not depend on timing; they meet once per round of
+// 2*D blocks (one round covers a workgroup's share for typical N), so the
+// waves stream without barriers in between.  Weights, scales and zeros
 // are read through buffer resources: every address is a scalar base and
 // offset plus one fixed 32-bit lane offset; reads past a buffer return 0 and
 // columns past N are computed but never stored.
@@ -489,7 +491,9 @@ struct GvPlan {
 template <int S, int SPG>
 struct GvShape {
   static constexpr int kGroups = SPG >= S ? 1 : S / SPG;        // group slots per window
-  static constexpr int kDepth = (S + 2 * kGroups) > 16 ? 2 : 3;  // blocks in flight
+  static constexpr int kDepth = (S + 2 * kGroups) > 16 ? 2 : ((S + 2 * kGroups) > 12 ? 3 : 4);  // blocks in flight
+  static constexpr int kRound = kDepth;  // blocks per reduction round (several rounds)
+  static constexpr int kOneRound = 2 * kDepth;  // a workgroup's whole share in one round
 };
 
 template <int S, int SPG>
@@ -548,11 +552,14 @@ KQ_DEV f32x4 gv_compute(const W4Args& a, const NibbleConsts& nc, uint32_t zsh,
   return acc;
 }
 
-template <int XDT, int S, int SPG, int LAYOUT>
+// ONE: the launch guarantees ncb <= 2*D blocks per workgroup, so one round
+// with the accumulators of all of them in registers (no outer loop).
+template <int XDT, int S, int SPG, int LAYOUT, bool ONE>
 __global__ void __launch_bounds__(64 * kGvWaves)
 w4a16_gemv_kernel(W4Args a, GvPlan p) {
   constexpr int D = GvShape<S, SPG>::kDepth;
-  __shared__ float red[kGvWaves][D * 4][64];
+  constexpr int U = ONE ? GvShape<S, SPG>::kOneRound : GvShape<S, SPG>::kRound;
+  __shared__ float red[kGvWaves][U * 4][64];
   const int lane = lane_id();
   const int wave = __builtin_amdgcn_readfirstlane(wave_id());
   const int j = lane & 15, kb = lane >> 4;
@@ -581,6 +588,12 @@ w4a16_gemv_kernel(W4Args a, GvPlan p) {
   c.g0 = __builtin_amdgcn_readfirstlane(group_of(a, c.st0 * 32));
   const uint32_t zsh = 4u * (uint32_t)(j & 7);
 
+  // rolling window: block q's weights were requested D blocks earlier
+  GvBlock<S, SPG> buf[D];
+#pragma unroll
+  for (int d = 0; d < D; ++d)
+    if (d < ncb) gv_load<S, SPG, LAYOUT>(a, c, u0 + d, buf[d]);
+
   // x chunks of this wave's steps, loaded once and kept for every block
   u32x4 A[S];
   {
@@ -589,41 +602,35 @@ w4a16_gemv_kernel(W4Args a, GvPlan p) {
     for (int s = 0; s < S; ++s) A[s] = gptq_order(x_to_f16<XDT>(*(const u32x4*)(xr + s * 32)));
   }
 
-  // rolling window: block q's weights were requested D blocks earlier
-  GvBlock<S, SPG> buf[D];
+  for (int q0 = 0; q0 < (ONE ? 1 : ncb); q0 += U) {
+    // U blocks per round (U a multiple of D, so block q0+q sits in buf[q % D])
+    f32x4 acc[U];
 #pragma unroll
-  for (int d = 0; d < D; ++d)
-    if (d < ncb) gv_load<S, SPG, LAYOUT>(a, c, u0 + d, buf[d]);
-
-  for (int q0 = 0; q0 < ncb; q0 += D) {
-    f32x4 acc[D];
-#pragma unroll
-    for (int d = 0; d < D; ++d) {
-      acc[d] = f32x4{0.f, 0.f, 0.f, 0.f};
-      if (q0 + d < ncb) {
-        acc[d] = gv_compute<S, SPG>(a, nc, zsh, buf[d], A);
-        if (q0 + d + D < ncb) gv_load<S, SPG, LAYOUT>(a, c, u0 + q0 + d + D, buf[d]);
+    for (int q = 0; q < U; ++q) {
+      acc[q] = f32x4{0.f, 0.f, 0.f, 0.f};
+      if (q0 + q < ncb) {
+        acc[q] = gv_compute<S, SPG>(a, nc, zsh, buf[q % D], A);
+        if (q0 + q + D < ncb) gv_load<S, SPG, LAYOUT>(a, c, u0 + q0 + q + D, buf[q % D]);
       }
     }
-    // fixed-order reduction of the 16 waves' partial sums (the next blocks'
+    // fixed-order reduction of the 16 waves' partial sums (the next round's
     // loads stay in flight across the barriers)
 #pragma unroll
-    for (int d = 0; d < D; ++d)
+    for (int q = 0; q < U; ++q)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) red[wave][d * 4 + r][lane] = acc[d][r];
+      for (int r = 0; r < 4; ++r) red[wave][q * 4 + r][lane] = acc[q][r];
     __syncthreads();
-    if (wave < D * 4) {
-      const int i = wave, d = i >> 2, r = i & 3;   // one output per thread
-      if (q0 + d < ncb) {
-        float v = red[0][i][lane];
+    for (int i = wave; i < U * 4; i += kGvWaves) {   // one output per thread
+      const int q = i >> 2, r = i & 3;
+      if (q0 + q >= ncb) continue;
+      float v = red[0][i][lane];
 #pragma unroll
-        for (int w = 1; w < kGvWaves; ++w) v = __fadd_rn(v, red[w][i][lane]);
-        const int m = 4 * kb + r;
-        const int n = (u0 + q0 + d) * 16 + j;
-        if (m < a.M && n < a.N) {
-          if (a.bias_dtype != KQ_DTYPE_NONE) v = __fadd_rn(v, load_as_f32(a.bias, a.bias_dtype, n));
-          a.out[(int64_t)m * a.N + n] = f32_to_out(v, a.out_dtype);
-        }
+      for (int w = 1; w < kGvWaves; ++w) v = __fadd_rn(v, red[w][i][lane]);
+      const int m = 4 * kb + r;
+      const int n = (u0 + q0 + q) * 16 + j;
+      if (m < a.M && n < a.N) {
+        if (a.bias_dtype != KQ_DTYPE_NONE) v = __fadd_rn(v, load_as_f32(a.bias, a.bias_dtype, n));
+        a.out[(int64_t)m * a.N + n] = f32_to_out(v, a.out_dtype);
       }
     }
     __syncthreads();
@@ -815,10 +822,15 @@ static bool gv_plan(const W4Args& a, int fmt, int gmode, GvPlan* p, int* S, int*
 
 template <int XDT, int S, int SPG>
 static void launch_gv_s(const W4Args& a, const GvPlan& p, int layout, hipStream_t st) {
-  if (layout == kLayoutTiles)
-    hipLaunchKernelGGL((w4a16_gemv_kernel<XDT, S, SPG, kLayoutTiles>), dim3(p.wgs), dim3(64 * kGvWaves), 0, st, a, p);
-  else
-    hipLaunchKernelGGL((w4a16_gemv_kernel<XDT, S, SPG, kLayoutRows>), dim3(p.wgs), dim3(64 * kGvWaves), 0, st, a, p);
+  const bool one = (p.units + p.wgs - 1) / p.wgs <= GvShape<S, SPG>::kOneRound;
+  const dim3 g(p.wgs), b(64 * kGvWaves);
+  if (layout == kLayoutTiles) {
+    if (one) hipLaunchKernelGGL((w4a16_gemv_kernel<XDT, S, SPG, kLayoutTiles, true>), g, b, 0, st, a, p);
+    else hipLaunchKernelGGL((w4a16_gemv_kernel<XDT, S, SPG, kLayoutTiles, false>), g, b, 0, st, a, p);
+  } else {
+    if (one) hipLaunchKernelGGL((w4a16_gemv_kernel<XDT, S, SPG, kLayoutRows, true>), g, b, 0, st, a, p);
+    else hipLaunchKernelGGL((w4a16_gemv_kernel<XDT, S, SPG, kLayoutRows, false>), g, b, 0, st, a, p);
+  }
 }
 
 template <int XDT, int S>
