@@ -57,14 +57,20 @@ def clock_warmup(seconds: float = 1.0) -> None:
     del a
 
 
-def _timed_replays(graph, steps: int, repeats: int = 3) -> float:
+def _timed_replays(graph, steps: int, repeats: int = 3, settle_s: float = 0.3) -> float:
     """Median over `repeats` timed replays of ms per captured step (HIP events
-    on the replaying stream; one untimed replay first)."""
+    on the replaying stream).  Untimed replays first, for at least `settle_s`
+    seconds: the GPU idles while the host builds a workload and its graph, and
+    its clocks need that long under load to return to their steady state."""
 
     import torch
 
+    t0 = time.perf_counter()
     graph.replay()
     torch.cuda.synchronize()
+    while time.perf_counter() - t0 < settle_s:
+        graph.replay()
+        torch.cuda.synchronize()
     times = []
     for _ in range(repeats):
         start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)

@@ -193,10 +193,12 @@ struct RowPlan {
   int threads, nch;
 };
 
+// About 256 threads per row: a row's load -> amax -> quantize -> store chain is
+// latency-bound, so several rows per CU must be in flight at once.
 static RowPlan plan_rows(int64_t k) {
   const int64_t chunks = (k + 7) / 8;
   RowPlan p{};
-  p.nch = chunks <= 1024 ? 1 : (chunks <= 2048 ? 2 : (chunks <= 4096 ? 4 : 8));
+  p.nch = chunks <= 256 ? 1 : (chunks <= 512 ? 2 : (chunks <= 1024 ? 4 : 8));
   const int64_t per = (chunks + p.nch - 1) / p.nch;
   p.threads = (int)std::min<int64_t>(1024, std::max<int64_t>(64, (per + 63) / 64 * 64));
   return p;

@@ -345,6 +345,7 @@ tile_gemm_kernel(TileGemmArgs a) {
         }
       }
       TgFrag xf[4];
+      f32x4 blk[2];
 #pragma unroll
       for (int mb = 0; mb < 4; ++mb) xf[mb] = tg_load(sX + mb * 16 * kTgBK, o_lo, o_hi);
 #pragma unroll
@@ -360,10 +361,21 @@ tile_gemm_kernel(TileGemmArgs a) {
             const i32x8 B = i32x8{xf[mb].lo[0], xf[mb].lo[1], xf[mb].lo[2], xf[mb].lo[3],
                                   xf[mb].hi[0], xf[mb].hi[1], xf[mb].hi[2], xf[mb].hi[3]};
             if constexpr (BLOCK) {
-              const f32x4 blk = mfma_fp8(A, B, f32x4{0.f, 0.f, 0.f, 0.f});
-              const float sc = prod[j >> 2][mb];
+              // scale-accumulate one MFMA behind, from alternating temporaries,
+              // so no MFMA waits on its own result before the next is issued
+              const int idx = j * 4 + mb;
+              blk[idx & 1] = mfma_fp8(A, B, f32x4{0.f, 0.f, 0.f, 0.f});
+              if (idx > 0) {
+                const int pj = (idx - 1) >> 2, pm = (idx - 1) & 3;
+                const float sc = prod[pj >> 2][pm];
 #pragma unroll
-              for (int q = 0; q < 4; ++q) acc[j][mb][q] = fmaf(blk[q], sc, acc[j][mb][q]);
+                for (int q = 0; q < 4; ++q) acc[pj][pm][q] = fmaf(blk[(idx - 1) & 1][q], sc, acc[pj][pm][q]);
+              }
+              if (idx == 31) {
+                const float sc = prod[1][3];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) acc[7][3][q] = fmaf(blk[1][q], sc, acc[7][3][q]);
+              }
             } else {
               acc[j][mb] = mfma_fp8(A, B, acc[j][mb]);
             }
@@ -481,6 +493,190 @@ tile_gemm_kernel(TileGemmArgs a) {
     cur = nxt;
     buf ^= 1;
     tn += per;
+  }
+}
+
+// Four-wave variant for the plain (unscaled K loop) FP8 / INT8 GEMM: each
+// wave owns 128 weight rows x 128 activation rows, so its 256 accumulators can
+// live in AGPRs (the MFMA accumulates there in place) and the CU reads each
+// operand block from LDS twice instead of four / two times (128 KB of
+// ds_read per K block instead of 192 KB).  One wave per SIMD: the 64
+// independent MFMAs of a K block keep the matrix pipe fed.  Same tiles,
+// persistent XCD order, LDS map, DMA pipeline and epilogue as above.
+constexpr int kTg4Threads = 256;
+
+template <int FMT>
+__global__ void __launch_bounds__(kTg4Threads)
+tile_gemm4_kernel(TileGemmArgs a) {
+  using Acc = typename TgTraits<FMT>::Acc;
+  __shared__ __attribute__((aligned(16))) uint8_t smem[kTgLdsBytes];
+  const int lane = lane_id();
+  const int wave = __builtin_amdgcn_readfirstlane(wave_id());
+  const int wn = wave >> 1, wm = wave & 1;
+  const int lr = lane & 15, lg = lane >> 4;
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)smem;
+  const int K = a.K;
+  const int KB = (K + kTgBK - 1) / kTgBK;
+  const int ktail = K - (KB - 1) * kTgBK;
+
+  const int total = a.mtiles * a.ntiles;
+  const int xcd = blockIdx.x & 7, per = gridDim.x >> 3, slot = blockIdx.x >> 3;
+  const int t_lo = (int)((int64_t)total * xcd / 8), t_hi = (int)((int64_t)total * (xcd + 1) / 8);
+  int t = t_lo + slot;
+  if (t >= t_hi) return;
+
+  const i32x4 rx = make_rsrc(a.x, (uint32_t)((uint64_t)a.x_rows * K));
+  const i32x4 rw = make_rsrc(a.w, (uint32_t)((uint64_t)a.N * K));
+  const int o_lo = lr * kTgBK + (tg_chunk<FMT>(lr, FMT == kTgFp8 ? 2 * lg : lg) << 4);
+  const int o_hi = lr * kTgBK + (tg_chunk<FMT>(lr, FMT == kTgFp8 ? 2 * lg + 1 : 4 + lg) << 4);
+
+  // DMA state: this wave fills 1 KB blocks 8*wave+i of each 32 KB stage
+  int32_t w_off[8], x_off[8];
+  float pf_exs = 1.0f, pf_ews = 1.0f, pf_eb = 0.0f;
+  auto set_tile = [&](int tt) {
+    const int mtile = tt / a.ntiles, ntile = tt % a.ntiles;
+    const int row0 = mtile * kTgBM, row_end = min(a.M, row0 + kTgBM);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int p = (wave * 8 + i) * 64 + lane, row = p >> 3;
+      const int c = tg_chunk<FMT>(row, p & 7);
+      const int n = ntile * kTgBN + row, r = row0 + row;
+      w_off[i] = n < a.N ? n * K + c * 16 : kTgOob;
+      x_off[i] = r < row_end ? r * K + c * 16 : kTgOob;
+    }
+    // epilogue constants of tile row / column t (one per thread)
+    const int tr = (int)threadIdx.x, r = row0 + tr, n = min(ntile * kTgBN + tr, a.N - 1);
+    pf_exs = r < row_end ? a.xs[r] : 0.0f;
+    pf_ews = a.ws_per_channel ? a.ws[n] : a.ws[0];
+    pf_eb = a.bias_dtype != KQ_DTYPE_NONE ? load_as_f32(a.bias, a.bias_dtype, n) : 0.0f;
+  };
+  auto stage_consts = [&](int buf) {
+    float* e = (float*)(smem + kTgLdsEpi) + buf * 3 * 256 + (int)threadIdx.x;
+    e[0] = pf_exs;
+    e[256] = pf_ews;
+    e[512] = pf_eb;
+  };
+  auto issue = [&](int kb, int st) {
+    const uint32_t lw = lds0 + kTgLdsW + st * (kTgBN * kTgBK) + wave * 8192;
+    const uint32_t lx = lds0 + kTgLdsX + st * (kTgBM * kTgBK) + wave * 8192;
+    const int soff = kb * kTgBK;
+    if (kb == KB - 1 && ktail < kTgBK) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int row = (wave * 8 + i) * 8 + (lane >> 3);
+        const bool ok = tg_chunk<FMT>(row, lane & 7) * 16 < ktail;
+        tg_dma16(rw, lw + i * 1024, ok ? w_off[i] : kTgOob, soff);
+        tg_dma16(rx, lx + i * 1024, ok ? x_off[i] : kTgOob, soff);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        tg_dma16(rw, lw + i * 1024, w_off[i], soff);
+        tg_dma16(rx, lx + i * 1024, x_off[i], soff);
+      }
+    }
+  };
+
+  set_tile(t);
+  int buf = 0, st = 0;
+  stage_consts(buf);
+  issue(0, st);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+
+  while (true) {
+    const int tn = t + per;
+    const bool has_next = tn < t_hi;
+    Acc acc[8][8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+#pragma unroll
+      for (int mb = 0; mb < 8; ++mb) acc[j][mb] = Acc{0, 0, 0, 0};
+
+    for (int kb = 0; kb < KB; ++kb) {
+      if (kb + 1 < KB) issue(kb + 1, st ^ 1);
+      const uint8_t* sW = smem + kTgLdsW + st * (kTgBN * kTgBK) + (128 * wn) * kTgBK;
+      const uint8_t* sX = smem + kTgLdsX + st * (kTgBM * kTgBK) + (128 * wm) * kTgBK;
+      TgFrag xf[8];
+#pragma unroll
+      for (int mb = 0; mb < 8; ++mb) xf[mb] = tg_load(sX + mb * 16 * kTgBK, o_lo, o_hi);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const TgFrag wf = tg_load(sW + j * 16 * kTgBK, o_lo, o_hi);
+#pragma unroll
+        for (int mb = 0; mb < 8; ++mb) {
+          if constexpr (FMT == kTgI8) {
+            acc[j][mb] = mfma_i8(wf.lo, xf[mb].lo, acc[j][mb]);
+            acc[j][mb] = mfma_i8(wf.hi, xf[mb].hi, acc[j][mb]);
+          } else {
+            const i32x8 A = i32x8{wf.lo[0], wf.lo[1], wf.lo[2], wf.lo[3], wf.hi[0], wf.hi[1], wf.hi[2], wf.hi[3]};
+            const i32x8 B = i32x8{xf[mb].lo[0], xf[mb].lo[1], xf[mb].lo[2], xf[mb].lo[3],
+                                  xf[mb].hi[0], xf[mb].hi[1], xf[mb].hi[2], xf[mb].hi[3]};
+            acc[j][mb] = mfma_fp8(A, B, acc[j][mb]);
+          }
+        }
+      }
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+      st ^= 1;
+    }
+
+    const int ntile = t % a.ntiles;
+    const int row0 = (t / a.ntiles) * kTgBM, row_end = min(a.M, row0 + kTgBM);
+    if (has_next) {
+      set_tile(tn);        // the next tile's first K block loads under this epilogue
+      issue(0, st);
+      stage_consts(buf ^ 1);
+    }
+    const bool vec_ok = (a.N & 3) == 0;
+    const float* eX = (const float*)(smem + kTgLdsEpi) + buf * 3 * 256;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int nl = 128 * wn + 16 * j + 4 * lg;
+      const int n = ntile * kTgBN + nl;
+      if (n >= a.N) continue;
+      const f32x4 wsc = *(const f32x4*)(eX + 256 + nl);
+      const f32x4 bv = *(const f32x4*)(eX + 512 + nl);
+#pragma unroll
+      for (int mb = 0; mb < 8; ++mb) {
+        const int ml = 128 * wm + 16 * mb + lr;
+        const int grow = row0 + ml;
+        if (grow >= row_end) continue;
+        const float xsc = eX[ml];
+        uint16_t o[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          float v = __fmul_rn(__fmul_rn((float)acc[j][mb][q], xsc), wsc[q]);
+          if (a.bias_dtype != KQ_DTYPE_NONE) v = __fadd_rn(v, bv[q]);
+          o[q] = tg_to_out(v, a.out_dtype);
+        }
+        uint16_t* dst = (uint16_t*)a.out + (int64_t)grow * a.N + n;
+        if (vec_ok) {
+          *(u32x2*)dst = u32x2{(uint32_t)o[0] | ((uint32_t)o[1] << 16), (uint32_t)o[2] | ((uint32_t)o[3] << 16)};
+        } else {
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            if (n + q < a.N) dst[q] = o[q];
+        }
+        if constexpr (FMT == kTgI8) {
+          if (a.acc_out) {
+            int32_t* ad = a.acc_out + (int64_t)grow * a.N + n;
+            if (vec_ok) {
+              *(i32x4*)ad = acc[j][mb];
+            } else {
+#pragma unroll
+              for (int q = 0; q < 4; ++q)
+                if (n + q < a.N) ad[q] = acc[j][mb][q];
+            }
+          }
+        }
+      }
+    }
+    if (!has_next) break;
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    t = tn;
+    buf ^= 1;
   }
 }
 
