@@ -423,66 +423,93 @@ tile_gemm_kernel(TileGemmArgs a) {
       }
       __syncthreads();
       const int IB = a.I / 128;
+      // the tile's 256 x 128 e4m3 block goes through the idle pipeline stage
+      // (row r at r*128, 16-byte chunk c at c ^ (r & 7)) so that the global
+      // stores below write whole 128-byte rows
+      uint8_t* stg = smem + kTgLdsX + (st ^ 1) * (kTgBM * kTgBK);
 #pragma unroll
       for (int mb = 0; mb < 4; ++mb) {
         const int lrow = 64 * wm + 16 * mb + lr;
-        const int grow = row0 + lrow;
-        if (grow >= row_end) continue;
         const float am = fmaxf(sRed[lrow], sRed[kTgBM + lrow]);
         const float s = __fdiv_rn(fmaxf(am, 1e-12f), 448.0f);
         const float rs = __fdiv_rn(1.0f, s);
-        uint8_t* dst = a.actq + (int64_t)grow * a.I + ntile * 128 + 64 * wn + 4 * lg;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           float v[4];
 #pragma unroll
           for (int q = 0; q < 4; ++q) v[q] = fminf(fmaxf(div_by_recip(acc[j][mb][q], s, rs), -448.0f), 448.0f);
-          *(uint32_t*)(dst + 16 * j) = pack4_e4m3(v[0], v[1], v[2], v[3]);
+          const int col = 64 * wn + 16 * j + 4 * lg;
+          *(uint32_t*)(stg + lrow * 128 + (((col >> 4) ^ (lrow & 7)) << 4) + (col & 15)) =
+              pack4_e4m3(v[0], v[1], v[2], v[3]);
         }
-        if (wn == 0 && lg == 0) a.acts[(int64_t)grow * IB + ntile] = s;
+        if (wn == 0 && lg == 0 && row0 + lrow < row_end) a.acts[(int64_t)(row0 + lrow) * IB + ntile] = s;
+      }
+      __syncthreads();
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int r = 64 * i + ((int)threadIdx.x >> 3), c = (int)threadIdx.x & 7;
+        if (row0 + r < row_end)
+          *(i32x4*)(a.actq + (int64_t)(row0 + r) * a.I + ntile * 128 + c * 16) =
+              *(const i32x4*)(stg + r * 128 + ((c ^ (r & 7)) << 4));
       }
     } else {
-      const bool vec_ok = (a.N & 3) == 0;
       const float* eX = (const float*)(smem + kTgLdsEpi) + buf * 3 * 256;
+      // each wave's 128 x 64 output block goes through its 8 KB of the idle
+      // pipeline stage in two column halves ([m][64 columns], 16-byte chunk c of
+      // row m at c ^ (m & 7)), so every global store writes whole 128-byte
+      // row segments; rows of 8-aligned N only (others store directly)
+      uint8_t* stg = smem + (wave < 4 ? kTgLdsW : kTgLdsX) + (st ^ 1) * (kTgBN * kTgBK) + (wave & 3) * 8192;
+      const bool staged = (a.N & 7) == 0;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int nl = 128 * wn + 16 * j + 4 * lg;  // tile column of q = 0
-        const int n = ntile * kTgBN + nl;
-        if (n >= a.N) continue;
-        const f32x4 wsc = *(const f32x4*)(eX + 256 + nl);
-        const f32x4 bv = *(const f32x4*)(eX + 512 + nl);
+      for (int half = 0; half < 2; ++half) {
 #pragma unroll
-        for (int mb = 0; mb < 4; ++mb) {
-          const int grow = row0 + 64 * wm + 16 * mb + lr;
-          if (grow >= row_end) continue;
-          const float xsc = eX[64 * wm + 16 * mb + lr];
-          uint16_t o[4];
+        for (int jj = 0; jj < 4; ++jj) {
+          const int j = 4 * half + jj;
+          const int nl = 128 * wn + 16 * j + 4 * lg;  // tile column of q = 0
+          const int n = ntile * kTgBN + nl;
+          const f32x4 wsc = *(const f32x4*)(eX + 256 + nl);
+          const f32x4 bv = *(const f32x4*)(eX + 512 + nl);
 #pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            float v = (float)acc[j][mb][q];
-            if (!BLOCK) v = __fmul_rn(__fmul_rn(v, xsc), wsc[q]);
-            if (a.bias_dtype != KQ_DTYPE_NONE) v = __fadd_rn(v, bv[q]);
-            o[q] = tg_to_out(v, a.out_dtype);
-          }
-          uint16_t* dst = (uint16_t*)a.out + (int64_t)grow * a.N + n;
-          if (vec_ok) {
-            *(u32x2*)dst = u32x2{(uint32_t)o[0] | ((uint32_t)o[1] << 16), (uint32_t)o[2] | ((uint32_t)o[3] << 16)};
-          } else {
+          for (int mb = 0; mb < 4; ++mb) {
+            const int ml = 16 * mb + lr;  // row within the wave's block
+            const int grow = row0 + 64 * wm + ml;
+            const float xsc = BLOCK ? 1.0f : eX[64 * wm + ml];
+            uint16_t o[4];
 #pragma unroll
-            for (int q = 0; q < 4; ++q)
-              if (n + q < a.N) dst[q] = o[q];
-          }
-          if constexpr (FMT == kTgI8) {
-            if (a.acc_out) {
-              int32_t* ad = a.acc_out + (int64_t)grow * a.N + n;
-              if (vec_ok) {
-                *(i32x4*)ad = acc[j][mb];
-              } else {
+            for (int q = 0; q < 4; ++q) {
+              float v = (float)acc[j][mb][q];
+              if (!BLOCK) v = __fmul_rn(__fmul_rn(v, xsc), wsc[q]);
+              if (a.bias_dtype != KQ_DTYPE_NONE) v = __fadd_rn(v, bv[q]);
+              o[q] = tg_to_out(v, a.out_dtype);
+            }
+            const u32x2 word = u32x2{(uint32_t)o[0] | ((uint32_t)o[1] << 16), (uint32_t)o[2] | ((uint32_t)o[3] << 16)};
+            if (staged) {
+              const int cb = 32 * jj + 8 * lg;  // byte column within the 128-byte row
+              *(u32x2*)(stg + ml * 128 + (((cb >> 4) ^ (ml & 7)) << 4) + (cb & 15)) = word;
+            } else if (grow < row_end) {
+              uint16_t* dst = (uint16_t*)a.out + (int64_t)grow * a.N + n;
+#pragma unroll
+              for (int q = 0; q < 4; ++q)
+                if (n + q < a.N) dst[q] = o[q];
+            }
+            if constexpr (FMT == kTgI8) {
+              if (a.acc_out && grow < row_end) {
+                int32_t* ad = a.acc_out + (int64_t)grow * a.N + n;
 #pragma unroll
                 for (int q = 0; q < 4; ++q)
                   if (n + q < a.N) ad[q] = acc[j][mb][q];
               }
             }
+          }
+        }
+        if (staged) {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            const int ml = 8 * i + (lane >> 3), c = lane & 7;
+            const int grow = row0 + 64 * wm + ml;
+            const int n = ntile * kTgBN + 128 * wn + 64 * half + 8 * c;
+            const i32x4 v = *(const i32x4*)(stg + ml * 128 + ((c ^ (ml & 7)) << 4));
+            if (grow < row_end && n < a.N) *(i32x4*)((uint16_t*)a.out + (int64_t)grow * a.N + n) = v;
           }
         }
       }
