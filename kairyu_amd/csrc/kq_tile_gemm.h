@@ -52,6 +52,7 @@ constexpr int kTgBK = 128;        // K bytes per pipeline stage (one block-scale
 constexpr int kTgThreads = 512;
 constexpr int kTgMaxKB = 128;     // K <= 16384 for block scaling (weight scale rows in LDS)
 constexpr int32_t kTgOob = (int32_t)0x80000000u;  // buffer offset past every resource: reads 0
+constexpr int kTgGroupM = 8;  // dense tile order: row tiles per group
 
 enum { kTgFp8 = 0, kTgI8 = 1 };
 enum { kTgEpiStore = 0, kTgEpiSwiGluQuant = 1 };
@@ -182,14 +183,21 @@ tile_gemm_kernel(TileGemmArgs a) {
   };
   auto tile_of = [&](int tt, int tab) -> TgTile {
     TgTile r;
-    r.ntile = tt % a.ntiles;
     if (a.mtile_table) {
+      r.ntile = tt % a.ntiles;
       r.e = __builtin_amdgcn_readlane(tab, 0);
       r.row0 = __builtin_amdgcn_readlane(tab, 1);
       r.row_end = __builtin_amdgcn_readlane(tab, 2);
     } else {
+      // dense: groups of kTgGroupM row tiles, row tile fastest, so an XCD's
+      // contiguous range of tiles covers a near-square block of the output
+      // (its operand rows come through its own L2 once) instead of a few row
+      // tiles against every weight row
+      const int gsz = kTgGroupM * a.ntiles, g = tt / gsz, rr = tt - g * gsz;
+      const int gm = min(kTgGroupM, a.mtiles - g * kTgGroupM);
+      r.ntile = rr / gm;
       r.e = 0;
-      r.row0 = (tt / a.ntiles) * kTgBM;
+      r.row0 = (g * kTgGroupM + rr % gm) * kTgBM;
       r.row_end = min(a.M, r.row0 + kTgBM);
     }
     return r;

@@ -221,6 +221,132 @@ w8a8_skinny_kernel(const uint8_t* __restrict__ xq, const uint8_t* __restrict__ w
     }
 }
 
+// ------------------------------------------------------------------ decode
+// M <= 16, K a multiple of 128: a workgroup owns 16 output columns, its NW
+// waves split K into contiguous ranges of 128-byte stages.  Each wave keeps a
+// private ring of R LDS stages; one stage holds 128 bytes of K for the 16
+// weight rows and the (up to) 16 activation rows, fetched by LDS DMA with 8
+// rows x 128 bytes per instruction (whole cache lines, where direct MFMA
+// fragment loads touch 16 half-lines each), and read back as MFMA fragments
+// through the tile engine's chunk swizzle.  No barrier in the K loop: a wave
+// only waits (vmcnt) for its own stage.  Rows beyond M or N load as zeros
+// (buffer offsets past the resource), so no lane branches on shape.
+template <int N_>
+KQ_DEV void wait_vm() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N_) : "memory");
+}
+
+constexpr int kDecStage = 4096;  // 2 KB weight block + 2 KB activation block
+
+template <int FMT, int R, int NW, int XH>
+__global__ void __launch_bounds__(64 * NW)
+w8a8_decode_kernel(const uint8_t* __restrict__ xq, const uint8_t* __restrict__ w, int K, Epi ep) {
+  constexpr int TF = FMT == kFmtFp8 ? kTgFp8 : kTgI8;
+  constexpr int OPS = 2 + XH;  // DMA instructions per stage
+  using Acc = typename W8Traits<FMT>::Acc;
+  __shared__ __attribute__((aligned(16))) uint8_t ring[NW * R * kDecStage];
+  __shared__ uint32_t red[(NW > 1 ? NW - 1 : 1) * 4 * 64];
+  const int lane = lane_id();
+  const int wave = __builtin_amdgcn_readfirstlane(wave_id());
+  const int j = lane & 15, kg = lane >> 4;
+  const int n0 = blockIdx.x * kSkinnyCols;
+  const int nst = K / 128;
+  const int per_wave = (nst + NW - 1) / NW;
+  const int sbeg = wave * per_wave;
+  const int nmy = max(0, min(nst, sbeg + per_wave) - sbeg);
+  const i32x4 rw = make_rsrc(w + (int64_t)n0 * K, (uint32_t)(min(kSkinnyCols, ep.N - n0) * K));
+  const i32x4 rx = make_rsrc(xq, (uint32_t)(ep.M * K));
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)ring +
+                        wave * R * kDecStage;
+  // DMA lane -> (row 8h + lane/8, physical chunk lane%8 holding logical chunk c)
+  int32_t vw[2], vx[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int r = 8 * h + (lane >> 3), c = tg_chunk<TF>(r, lane & 7);
+    vw[h] = r * K + c * 16;
+    vx[h] = r < ep.M ? r * K + c * 16 : kTgOob;
+  }
+  auto issue = [&](int st, int q) {
+    const uint32_t b = lds0 + q * kDecStage;
+    const int32_t so = __builtin_amdgcn_readfirstlane(st * 128);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) tg_dma16(rw, b + h * 1024, vw[h], so);
+#pragma unroll
+    for (int h = 0; h < XH; ++h) tg_dma16(rx, b + 2048 + h * 1024, vx[h], so);
+  };
+  const uint8_t* mine = ring + wave * R * kDecStage;
+  if constexpr (XH == 1) {  // activation rows 8..15 are never loaded: zero once
+#pragma unroll
+    for (int q = 0; q < R; ++q) *(i32x4*)(mine + q * kDecStage + 3072 + lane * 16) = i32x4{0, 0, 0, 0};
+  }
+  const int o_lo = j * 128 + (tg_chunk<TF>(j, FMT == kFmtFp8 ? 2 * kg : kg) << 4);
+  const int o_hi = j * 128 + (tg_chunk<TF>(j, FMT == kFmtFp8 ? 2 * kg + 1 : 4 + kg) << 4);
+
+  Acc acc = Acc{0, 0, 0, 0};
+#pragma unroll
+  for (int i = 0; i < R - 1; ++i)
+    if (i < nmy) issue(sbeg + i, i);
+  for (int i = 0; i < nmy; ++i) {
+    // stage i + R - 1 reuses the slot read in iteration i - 1 (its reads are
+    // complete: their MFMA has consumed them)
+    if (i + R - 1 < nmy) issue(sbeg + i + R - 1, (i + R - 1) % R);
+    const int ahead = min(R - 1, nmy - 1 - i);  // stages issued after stage i
+    if (ahead >= 3) wait_vm<3 * OPS>();
+    else if (ahead == 2) wait_vm<2 * OPS>();
+    else if (ahead == 1) wait_vm<OPS>();
+    else wait_vm<0>();
+    const uint8_t* q = mine + (i % R) * kDecStage;
+    const i32x4 wl = *(const i32x4*)(q + o_lo), wh = *(const i32x4*)(q + o_hi);
+    const i32x4 xl = *(const i32x4*)(q + 2048 + o_lo), xh = *(const i32x4*)(q + 2048 + o_hi);
+    if constexpr (FMT == kFmtFp8) {
+      acc = mfma_fp8(i32x8{xl[0], xl[1], xl[2], xl[3], xh[0], xh[1], xh[2], xh[3]},
+                     i32x8{wl[0], wl[1], wl[2], wl[3], wh[0], wh[1], wh[2], wh[3]}, acc);
+    } else {
+      acc = mfma_i8(xl, wl, acc);
+      acc = mfma_i8(xh, wh, acc);
+    }
+  }
+
+  // fixed-order reduction of the waves' K ranges (wave 0 first)
+  if (wave > 0) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) red[((wave - 1) * 4 + r) * 64 + lane] = acc_bits(acc, r);
+  }
+  __syncthreads();
+  if (wave != 0) return;
+  for (int w2 = 1; w2 < NW; ++w2)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const uint32_t bits = red[((w2 - 1) * 4 + r) * 64 + lane];
+      if constexpr (FMT == kFmtI8) acc[r] += (int)bits;
+      else acc[r] = __fadd_rn(acc[r], __uint_as_float(bits));
+    }
+#pragma unroll
+  for (int r = 0; r < 4; ++r) epi_store<FMT>(ep, kg * 4 + r, n0 + j, acc, r);
+}
+
+template <int FMT, int R, int NW>
+static void launch_decode_nw(const uint8_t* xq, const uint8_t* w, int K, const Epi& ep,
+                             hipStream_t stream) {
+  const dim3 grid((ep.N + kSkinnyCols - 1) / kSkinnyCols), block(64 * NW);
+  if (ep.M <= 8)
+    hipLaunchKernelGGL((w8a8_decode_kernel<FMT, R, NW, 1>), grid, block, 0, stream, xq, w, K, ep);
+  else
+    hipLaunchKernelGGL((w8a8_decode_kernel<FMT, R, NW, 2>), grid, block, 0, stream, xq, w, K, ep);
+}
+
+// Waves per workgroup from the stage count (each wave keeps >= ~4 stages in
+// its range); rings of 4 stages (2 for the 2-wave form, whose short ranges
+// gain nothing from a deeper ring).
+template <int FMT>
+static void launch_decode(const uint8_t* xq, const uint8_t* w, int K, const Epi& ep,
+                          hipStream_t stream) {
+  const int nst = K / 128;
+  if (nst >= 64) launch_decode_nw<FMT, 4, 8>(xq, w, K, ep, stream);
+  else if (nst >= 32) launch_decode_nw<FMT, 4, 4>(xq, w, K, ep, stream);
+  else launch_decode_nw<FMT, 2, 2>(xq, w, K, ep, stream);
+}
+
 // ------------------------------------------------------------------- tiled
 constexpr int kTile = 128;      // BM = BN = BK(bytes) = 128
 constexpr int kTileBytes = kTile * kTile;
@@ -407,7 +533,9 @@ static int run_w8a8(const char* what, const uint8_t* xq, const uint8_t* w, int64
     set_error("%s: weight or activation exceeds the 4 GiB addressing of the skinny kernel", what);
     return KQ_EINVAL;
   }
-  if (m <= 16) launch_skinny<FMT, 1>(xq, w, K, ep, workspace, ws_bytes, stream);
+  if (m <= 16 && K % 128 == 0 && (n + kSkinnyCols - 1) / kSkinnyCols >= tg_device_cus())
+    launch_decode<FMT>(xq, w, K, ep, stream);
+  else if (m <= 16) launch_skinny<FMT, 1>(xq, w, K, ep, workspace, ws_bytes, stream);
   else if (m <= 32) launch_skinny<FMT, 2>(xq, w, K, ep, workspace, ws_bytes, stream);
   else if (m <= 64) launch_skinny<FMT, 4>(xq, w, K, ep, workspace, ws_bytes, stream);
   else if (m * k < ((int64_t)1 << 31) && n * k < ((int64_t)1 << 31) &&

@@ -93,6 +93,38 @@ def test_int8_accumulators_and_output_bit_exact_all_paths(cuda, m, out_dtype):
     assert np.array_equal(np32(out), expected)
 
 
+# Decode path (M <= 16, K % 128 == 0, at least one 16-column tile per CU):
+# N = 4104 leaves a partial last tile; K = 1536 / 4096 / 8320 selects the
+# 2-, 4- and 8-wave forms (8320 = 65 stages, uneven across 8 waves); M = 8 / 9
+# straddles the one- and two-instruction activation fetch.
+DECODE_N = 4104
+
+
+@pytest.mark.parametrize("k,m", [(1536, 1), (1536, 16), (4096, 8), (4096, 9), (8320, 5), (8320, 16)])
+def test_int8_decode_path_bit_exact(cuda, k, m):
+    banner(f"int8 decode k={k} m={m}")
+    module = _int8_module(k, DECODE_N, seed=k + m).to(cuda)
+    x = torch.randn(m, k, generator=torch.Generator().manual_seed(k * m)).to(torch.bfloat16)
+    acc = torch.empty(m, DECODE_N, dtype=torch.int32, device=cuda)
+    out = hip.int8_linear_forward(x.to(cuda), module, accumulators=acc)
+    expected, xq, xs, eacc = olinear.int8_forward(
+        np32(x), module.weight.cpu().numpy(), module.weight_scale.cpu().numpy(), np32(module.bias))
+    assert np.array_equal(acc.cpu().numpy().astype(np.int64), eacc)
+    assert np.array_equal(np32(out), expected)
+
+
+@pytest.mark.parametrize("k,m,per_channel", [(1536, 1, True), (4096, 8, False), (4096, 9, True),
+                                             (8320, 16, True), (8320, 3, False)])
+def test_fp8_decode_path_matches_oracle(cuda, k, m, per_channel):
+    banner(f"fp8 decode k={k} m={m} per_channel={per_channel}")
+    module = _fp8_module(k, DECODE_N, seed=k + m, per_channel=per_channel).to(cuda)
+    x = torch.randn(m, k, generator=torch.Generator().manual_seed(k * m)).to(torch.bfloat16)
+    out = module(x.to(cuda))
+    expected, _, _, pre = olinear.fp8_forward(np32(x), bits(module.weight), np32(module.weight_scale),
+                                              np32(module.bias))
+    assert_close_fp(np32(out), pre, label=f"k={k} m={m}")
+
+
 def test_int8_generic_k_path(cuda):
     banner("int8 generic k")
     module = _int8_module(72, 24, seed=3).to(cuda)
