@@ -193,12 +193,15 @@ struct RowPlan {
   int threads, nch;
 };
 
-// About 256 threads per row: a row's load -> amax -> quantize -> store chain is
-// latency-bound, so several rows per CU must be in flight at once.
-static RowPlan plan_rows(int64_t k) {
+// A row's load -> amax -> quantize -> store chain is latency-bound.  With at
+// least one row per CU, about 256 threads per row keep several rows in flight
+// on every CU; with fewer rows than CUs (decode batches) each row has a CU to
+// itself, so up to 1024 threads per row shorten its serial chain instead.
+static RowPlan plan_rows(int64_t rows, int64_t k) {
   const int64_t chunks = (k + 7) / 8;
+  const int64_t tmax = rows < 256 ? 1024 : 256;
   RowPlan p{};
-  p.nch = chunks <= 256 ? 1 : (chunks <= 512 ? 2 : (chunks <= 1024 ? 4 : 8));
+  p.nch = chunks <= tmax ? 1 : (chunks <= 2 * tmax ? 2 : (chunks <= 4 * tmax ? 4 : 8));
   const int64_t per = (chunks + p.nch - 1) / p.nch;
   p.threads = (int)std::min<int64_t>(1024, std::max<int64_t>(64, (per + 63) / 64 * 64));
   return p;
@@ -235,7 +238,7 @@ extern "C" int kq_row_amax(const void* x, int x_dtype, int64_t rows, int64_t k, 
   int rc = check_rows("kq_row_amax", x, x_dtype, rows, k, ldx);
   if (rc) return rc;
   if (rows == 0) return KQ_OK;
-  const RowPlan p = plan_rows(k);
+  const RowPlan p = plan_rows(rows, k);
   const bool v = vec_ok(x, ldx);
   const dim3 g((unsigned)rows), b(p.threads);
   hipStream_t st = (hipStream_t)stream;
@@ -254,7 +257,7 @@ extern "C" int kq_act_quant_i8(const void* x, int x_dtype, int64_t rows, int64_t
   int rc = check_rows("kq_act_quant_i8", x, x_dtype, rows, k, ldx);
   if (rc) return rc;
   if (rows == 0) return KQ_OK;
-  const RowPlan p = plan_rows(k);
+  const RowPlan p = plan_rows(rows, k);
   const bool v = vec_ok(x, ldx);
   const dim3 g((unsigned)rows), b(p.threads);
   hipStream_t st = (hipStream_t)stream;
@@ -278,7 +281,7 @@ extern "C" int kq_act_quant_fp8(const void* x, int x_dtype, int64_t rows, int64_
     return KQ_EINVAL;
   }
   if (rows == 0) return KQ_OK;
-  const RowPlan p = plan_rows(k);
+  const RowPlan p = plan_rows(rows, k);
   const bool v = vec_ok(x, ldx);
   const dim3 g((unsigned)rows), b(p.threads);
   hipStream_t st = (hipStream_t)stream;
