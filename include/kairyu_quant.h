@@ -17,8 +17,9 @@
  *     marks an absent optional operand (bias).
  *   - FP8 means OCP e4m3fn bytes (torch.float8_e4m3fn).
  *   - `workspace` is scratch device memory (split-K partial sums, the
- *     act-order activation gather).  It may be NULL for the W8A8 entry points
- *     (no split-K then); W4A16 calls need kq_w4a16_workspace_size() bytes.
+ *     act-order activation gather).  It may be NULL or short for the W8A8
+ *     entry points (no split-K then; kq_w8a8_workspace_size() bytes enable
+ *     every split-K form); W4A16 calls need kq_w4a16_workspace_size() bytes.
  *     Calls that share one workspace must be ordered on one stream.
  */
 #ifndef KAIRYU_QUANT_H
@@ -92,6 +93,12 @@ int kq_w8a8_fp8_gemm(const uint8_t* xq, const float* xscale, const uint8_t* w,
                      const float* wscale, int wscale_per_channel, const void* bias,
                      int bias_dtype, void* out, int out_dtype, int64_t m, int64_t n,
                      int64_t k, void* workspace, size_t workspace_bytes, void* stream);
+
+/* Bytes of workspace with which every split-K form of the two W8A8 entry
+ * points is available for this shape (0: none applies).  No counterpart in
+ * the reference (its GPU path calls torch._scaled_mm / Triton, which allocate
+ * through torch). */
+size_t kq_w8a8_workspace_size(int64_t m, int64_t n, int64_t k);
 
 /* AWQ W4A16 ("gemm" layout): qweight int32 [k, n/8] packed along n in order
  * [0,2,4,6,1,3,5,7], qzeros int32 [k/g, n/8] same packing, scales fp16 [k/g, n].

@@ -47,6 +47,7 @@ _SIGNATURES: dict[str, list] = {
     "kq_act_quant_fp8": [_P, _I, _I64, _I64, _I64, _P, _I, _P, _P, _P],
     "kq_w8a8_i8_gemm": [_P, _P, _P, _P, _P, _I, _P, _I, _P, _I64, _I64, _I64, _P, _SZ, _P],
     "kq_w8a8_fp8_gemm": [_P, _P, _P, _P, _I, _P, _I, _P, _I, _I64, _I64, _I64, _P, _SZ, _P],
+    "kq_w8a8_workspace_size": [_I64, _I64, _I64],
     "kq_w4a16_awq_gemm": [_P, _I, _P, _P, _P, _P, _I, _P, _I64, _I64, _I64, _I, _P, _SZ, _P],
     "kq_w4a16_gptq_gemm": [
         _P, _I, _P, _P, _P, _P, _P, _I, _P, _I, _P, _I64, _I64, _I64, _I, _P, _SZ, _P,
@@ -91,6 +92,7 @@ def _load() -> ctypes.CDLL:
             fn.argtypes = argtypes
             fn.restype = {"kq_last_error": ctypes.c_char_p,
                           "kq_w4a16_workspace_size": ctypes.c_size_t,
+                          "kq_w8a8_workspace_size": ctypes.c_size_t,
                           "kq_moe_workspace_size": ctypes.c_size_t}.get(name, ctypes.c_int)
         _lib = lib
         return lib

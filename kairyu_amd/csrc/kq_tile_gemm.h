@@ -89,6 +89,9 @@ struct TileGemmArgs {
   const void* bias;          // [N] or null
   int bias_dtype;
   int32_t* acc_out;          // INT8: raw int32 accumulators [M][N] or null
+  int ksplit;                // dense, per-channel scales only: K split across this many
+                             // work units per tile (0/1: none); each stores raw 32-bit
+  uint32_t* partials;        // accumulators to partials[split][M][N], reduced afterwards
   uint8_t* actq;             // SwiGLU: e4m3 activations [rows][I]
   float* acts;               // SwiGLU: their 1x128 block scales [rows][I/128]
 };
@@ -141,6 +144,7 @@ KQ_DEV TgFrag tg_load(const uint8_t* blk, int off_lo, int off_hi) {
 // Wave-uniform description of one tile.
 struct TgTile {
   int e, row0, row_end, ntile;
+  int split, kb0, kb1;  // K blocks [kb0, kb1) of this work unit
 };
 
 template <int FMT, bool BLOCK, int EPI>
@@ -159,7 +163,9 @@ tile_gemm_kernel(TileGemmArgs a) {
   const int NB = (a.N + 127) / 128;
 
   const int mt_used = a.mtile_count ? __builtin_amdgcn_readfirstlane(*a.mtile_count) : a.mtiles;
-  const int total = min(mt_used, a.mtiles) * a.ntiles;
+  const int ksplit = (!BLOCK && EPI == kTgEpiStore && !a.mtile_table && a.ksplit > 1) ? a.ksplit : 1;
+  const int tiles = min(mt_used, a.mtiles) * a.ntiles;
+  const int total = tiles * ksplit;
   const int xcd = blockIdx.x & 7, per = gridDim.x >> 3, slot = blockIdx.x >> 3;
   const int t_lo = (int)((int64_t)total * xcd / 8), t_hi = (int)((int64_t)total * (xcd + 1) / 8);
   int t = t_lo + slot;
@@ -179,10 +185,15 @@ tile_gemm_kernel(TileGemmArgs a) {
   // row, 0); lane l < 3 of a table word holds entry word l.
   auto load_tab = [&](int tt) -> int {
     if (!a.mtile_table) return 0;
-    return kq_rbl_i32(rtab, (4 * (tt / a.ntiles) + (lane & 3)) * 4, 0, 0);
+    return kq_rbl_i32(rtab, (4 * ((tt % tiles) / a.ntiles) + (lane & 3)) * 4, 0, 0);
   };
   auto tile_of = [&](int tt, int tab) -> TgTile {
     TgTile r;
+    // split s of every tile before split s + 1: an XCD's range shares K blocks
+    r.split = tt / tiles;
+    tt -= r.split * tiles;
+    r.kb0 = (int)((int64_t)KB * r.split / ksplit);
+    r.kb1 = (int)((int64_t)KB * (r.split + 1) / ksplit);
     if (a.mtile_table) {
       r.ntile = tt % a.ntiles;
       r.e = __builtin_amdgcn_readlane(tab, 0);
@@ -306,7 +317,7 @@ tile_gemm_kernel(TileGemmArgs a) {
   set_offsets(cur);
   int buf = 0, st = 0;
   stage_ws(buf);
-  issue(0, st);
+  issue(cur.kb0, st);
   int tn = t + per;
   int pf_tab = tn < t_hi ? load_tab(tn) : 0;
   __builtin_amdgcn_s_waitcnt(0);
@@ -332,8 +343,14 @@ tile_gemm_kernel(TileGemmArgs a) {
 #pragma unroll
       for (int mb = 0; mb < 4; ++mb) acc[j][mb] = Acc{0, 0, 0, 0};
 
-    for (int kb = 0; kb < KB; ++kb) {
-      if (kb + 1 < KB) issue(kb + 1, st ^ 1);
+    // The next tile's prefetch loads are still in flight here.  Where the
+    // register allocator reuses one of their destination registers inside the
+    // K loop (the store epilogue variants), the compiler would otherwise wait
+    // for all vector-memory operations (the next block's copies included) in
+    // every K step; one wait per tile here lets it drop that.
+    if constexpr (EPI == kTgEpiStore) __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    for (int kb = cur.kb0; kb < cur.kb1; ++kb) {
+      if (kb + 1 < cur.kb1) issue(kb + 1, st ^ 1);
       const uint8_t* sW = smem + kTgLdsW + st * (kTgBN * kTgBK) + (128 * wn) * kTgBK;
       const uint8_t* sX = smem + kTgLdsX + st * (kTgBM * kTgBK) + (64 * wm) * kTgBK;
       float prod[2][4];
@@ -399,7 +416,7 @@ tile_gemm_kernel(TileGemmArgs a) {
       // the next tile's first K block loads while this tile's epilogue runs
       set_offsets(nxt);
       stage_ws(buf ^ 1);
-      issue(0, st);
+      issue(nxt.kb0, st);
     }
 
     // ------------------------------------------------------------ epilogue
@@ -459,6 +476,34 @@ tile_gemm_kernel(TileGemmArgs a) {
         if (row0 + r < row_end)
           *(i32x4*)(a.actq + (int64_t)(row0 + r) * a.I + ntile * 128 + c * 16) =
               *(const i32x4*)(stg + r * 128 + ((c ^ (r & 7)) << 4));
+      }
+    } else if (ksplit > 1) {
+      // raw 32-bit accumulators of this work unit's K range; a reduce pass
+      // sums the splits in order and applies the scales
+      uint32_t* pb = a.partials + (int64_t)cur.split * a.M * a.N;
+      const bool vec = (a.N & 3) == 0;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int n = ntile * kTgBN + 128 * wn + 16 * j + 4 * lg;
+#pragma unroll
+        for (int mb = 0; mb < 4; ++mb) {
+          const int grow = row0 + 64 * wm + 16 * mb + lr;
+          if (grow >= row_end) continue;
+          uint32_t v[4];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            if constexpr (FMT == kTgI8) v[q] = (uint32_t)(int)acc[j][mb][q];
+            else v[q] = __float_as_uint((float)acc[j][mb][q]);
+          }
+          uint32_t* dst = pb + (int64_t)grow * a.N + n;
+          if (vec && n + 3 < a.N) {
+            *(u32x4*)dst = u32x4{v[0], v[1], v[2], v[3]};
+          } else {
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+              if (n + q < a.N) dst[q] = v[q];
+          }
+        }
       }
     } else {
       const float* eX = (const float*)(smem + kTgLdsEpi) + buf * 3 * 256;
@@ -531,190 +576,6 @@ tile_gemm_kernel(TileGemmArgs a) {
   }
 }
 
-// Four-wave variant for the plain (unscaled K loop) FP8 / INT8 GEMM: each
-// wave owns 128 weight rows x 128 activation rows, so its 256 accumulators can
-// live in AGPRs (the MFMA accumulates there in place) and the CU reads each
-// operand block from LDS twice instead of four / two times (128 KB of
-// ds_read per K block instead of 192 KB).  One wave per SIMD: the 64
-// independent MFMAs of a K block keep the matrix pipe fed.  Same tiles,
-// persistent XCD order, LDS map, DMA pipeline and epilogue as above.
-constexpr int kTg4Threads = 256;
-
-template <int FMT>
-__global__ void __launch_bounds__(kTg4Threads)
-tile_gemm4_kernel(TileGemmArgs a) {
-  using Acc = typename TgTraits<FMT>::Acc;
-  __shared__ __attribute__((aligned(16))) uint8_t smem[kTgLdsBytes];
-  const int lane = lane_id();
-  const int wave = __builtin_amdgcn_readfirstlane(wave_id());
-  const int wn = wave >> 1, wm = wave & 1;
-  const int lr = lane & 15, lg = lane >> 4;
-  const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)smem;
-  const int K = a.K;
-  const int KB = (K + kTgBK - 1) / kTgBK;
-  const int ktail = K - (KB - 1) * kTgBK;
-
-  const int total = a.mtiles * a.ntiles;
-  const int xcd = blockIdx.x & 7, per = gridDim.x >> 3, slot = blockIdx.x >> 3;
-  const int t_lo = (int)((int64_t)total * xcd / 8), t_hi = (int)((int64_t)total * (xcd + 1) / 8);
-  int t = t_lo + slot;
-  if (t >= t_hi) return;
-
-  const i32x4 rx = make_rsrc(a.x, (uint32_t)((uint64_t)a.x_rows * K));
-  const i32x4 rw = make_rsrc(a.w, (uint32_t)((uint64_t)a.N * K));
-  const int o_lo = lr * kTgBK + (tg_chunk<FMT>(lr, FMT == kTgFp8 ? 2 * lg : lg) << 4);
-  const int o_hi = lr * kTgBK + (tg_chunk<FMT>(lr, FMT == kTgFp8 ? 2 * lg + 1 : 4 + lg) << 4);
-
-  // DMA state: this wave fills 1 KB blocks 8*wave+i of each 32 KB stage
-  int32_t w_off[8], x_off[8];
-  float pf_exs = 1.0f, pf_ews = 1.0f, pf_eb = 0.0f;
-  auto set_tile = [&](int tt) {
-    const int mtile = tt / a.ntiles, ntile = tt % a.ntiles;
-    const int row0 = mtile * kTgBM, row_end = min(a.M, row0 + kTgBM);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int p = (wave * 8 + i) * 64 + lane, row = p >> 3;
-      const int c = tg_chunk<FMT>(row, p & 7);
-      const int n = ntile * kTgBN + row, r = row0 + row;
-      w_off[i] = n < a.N ? n * K + c * 16 : kTgOob;
-      x_off[i] = r < row_end ? r * K + c * 16 : kTgOob;
-    }
-    // epilogue constants of tile row / column t (one per thread)
-    const int tr = (int)threadIdx.x, r = row0 + tr, n = min(ntile * kTgBN + tr, a.N - 1);
-    pf_exs = r < row_end ? a.xs[r] : 0.0f;
-    pf_ews = a.ws_per_channel ? a.ws[n] : a.ws[0];
-    pf_eb = a.bias_dtype != KQ_DTYPE_NONE ? load_as_f32(a.bias, a.bias_dtype, n) : 0.0f;
-  };
-  auto stage_consts = [&](int buf) {
-    float* e = (float*)(smem + kTgLdsEpi) + buf * 3 * 256 + (int)threadIdx.x;
-    e[0] = pf_exs;
-    e[256] = pf_ews;
-    e[512] = pf_eb;
-  };
-  auto issue = [&](int kb, int st) {
-    const uint32_t lw = lds0 + kTgLdsW + st * (kTgBN * kTgBK) + wave * 8192;
-    const uint32_t lx = lds0 + kTgLdsX + st * (kTgBM * kTgBK) + wave * 8192;
-    const int soff = kb * kTgBK;
-    if (kb == KB - 1 && ktail < kTgBK) {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int row = (wave * 8 + i) * 8 + (lane >> 3);
-        const bool ok = tg_chunk<FMT>(row, lane & 7) * 16 < ktail;
-        tg_dma16(rw, lw + i * 1024, ok ? w_off[i] : kTgOob, soff);
-        tg_dma16(rx, lx + i * 1024, ok ? x_off[i] : kTgOob, soff);
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        tg_dma16(rw, lw + i * 1024, w_off[i], soff);
-        tg_dma16(rx, lx + i * 1024, x_off[i], soff);
-      }
-    }
-  };
-
-  set_tile(t);
-  int buf = 0, st = 0;
-  stage_consts(buf);
-  issue(0, st);
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-
-  while (true) {
-    const int tn = t + per;
-    const bool has_next = tn < t_hi;
-    Acc acc[8][8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j)
-#pragma unroll
-      for (int mb = 0; mb < 8; ++mb) acc[j][mb] = Acc{0, 0, 0, 0};
-
-    for (int kb = 0; kb < KB; ++kb) {
-      if (kb + 1 < KB) issue(kb + 1, st ^ 1);
-      const uint8_t* sW = smem + kTgLdsW + st * (kTgBN * kTgBK) + (128 * wn) * kTgBK;
-      const uint8_t* sX = smem + kTgLdsX + st * (kTgBM * kTgBK) + (128 * wm) * kTgBK;
-      TgFrag xf[8];
-#pragma unroll
-      for (int mb = 0; mb < 8; ++mb) xf[mb] = tg_load(sX + mb * 16 * kTgBK, o_lo, o_hi);
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const TgFrag wf = tg_load(sW + j * 16 * kTgBK, o_lo, o_hi);
-#pragma unroll
-        for (int mb = 0; mb < 8; ++mb) {
-          if constexpr (FMT == kTgI8) {
-            acc[j][mb] = mfma_i8(wf.lo, xf[mb].lo, acc[j][mb]);
-            acc[j][mb] = mfma_i8(wf.hi, xf[mb].hi, acc[j][mb]);
-          } else {
-            const i32x8 A = i32x8{wf.lo[0], wf.lo[1], wf.lo[2], wf.lo[3], wf.hi[0], wf.hi[1], wf.hi[2], wf.hi[3]};
-            const i32x8 B = i32x8{xf[mb].lo[0], xf[mb].lo[1], xf[mb].lo[2], xf[mb].lo[3],
-                                  xf[mb].hi[0], xf[mb].hi[1], xf[mb].hi[2], xf[mb].hi[3]};
-            acc[j][mb] = mfma_fp8(A, B, acc[j][mb]);
-          }
-        }
-      }
-      __builtin_amdgcn_s_waitcnt(0);
-      __syncthreads();
-      st ^= 1;
-    }
-
-    const int ntile = t % a.ntiles;
-    const int row0 = (t / a.ntiles) * kTgBM, row_end = min(a.M, row0 + kTgBM);
-    if (has_next) {
-      set_tile(tn);        // the next tile's first K block loads under this epilogue
-      issue(0, st);
-      stage_consts(buf ^ 1);
-    }
-    const bool vec_ok = (a.N & 3) == 0;
-    const float* eX = (const float*)(smem + kTgLdsEpi) + buf * 3 * 256;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int nl = 128 * wn + 16 * j + 4 * lg;
-      const int n = ntile * kTgBN + nl;
-      if (n >= a.N) continue;
-      const f32x4 wsc = *(const f32x4*)(eX + 256 + nl);
-      const f32x4 bv = *(const f32x4*)(eX + 512 + nl);
-#pragma unroll
-      for (int mb = 0; mb < 8; ++mb) {
-        const int ml = 128 * wm + 16 * mb + lr;
-        const int grow = row0 + ml;
-        if (grow >= row_end) continue;
-        const float xsc = eX[ml];
-        uint16_t o[4];
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          float v = __fmul_rn(__fmul_rn((float)acc[j][mb][q], xsc), wsc[q]);
-          if (a.bias_dtype != KQ_DTYPE_NONE) v = __fadd_rn(v, bv[q]);
-          o[q] = tg_to_out(v, a.out_dtype);
-        }
-        uint16_t* dst = (uint16_t*)a.out + (int64_t)grow * a.N + n;
-        if (vec_ok) {
-          *(u32x2*)dst = u32x2{(uint32_t)o[0] | ((uint32_t)o[1] << 16), (uint32_t)o[2] | ((uint32_t)o[3] << 16)};
-        } else {
-#pragma unroll
-          for (int q = 0; q < 4; ++q)
-            if (n + q < a.N) dst[q] = o[q];
-        }
-        if constexpr (FMT == kTgI8) {
-          if (a.acc_out) {
-            int32_t* ad = a.acc_out + (int64_t)grow * a.N + n;
-            if (vec_ok) {
-              *(i32x4*)ad = acc[j][mb];
-            } else {
-#pragma unroll
-              for (int q = 0; q < 4; ++q)
-                if (n + q < a.N) ad[q] = acc[j][mb][q];
-            }
-          }
-        }
-      }
-    }
-    if (!has_next) break;
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    t = tn;
-    buf ^= 1;
-  }
-}
-
 // ------------------------------------------------------------------ host
 static inline int tg_device_cus() {
   static int cached[64] = {0};
@@ -734,7 +595,7 @@ static inline int tg_device_cus() {
 // multiple of 8 so every XCD gets the same number of workgroups.
 template <int FMT, bool BLOCK, int EPI>
 static void tg_launch(const TileGemmArgs& a, hipStream_t stream) {
-  const int64_t max_total = (int64_t)a.mtiles * a.ntiles;
+  const int64_t max_total = (int64_t)a.mtiles * a.ntiles * (a.ksplit > 1 ? a.ksplit : 1);
   int64_t grid = max_total < tg_device_cus() ? max_total : tg_device_cus();
   grid = (grid + 7) / 8 * 8;
   hipLaunchKernelGGL((tile_gemm_kernel<FMT, BLOCK, EPI>), dim3((unsigned)grid), dim3(kTgThreads), 0,

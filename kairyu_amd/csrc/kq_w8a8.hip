@@ -507,6 +507,24 @@ static void launch_skinny(const uint8_t* xq, const uint8_t* w, int K, const Epi&
   }
 }
 
+// Work units per 256x256 tile for the tile engine at M > 64, 0 when it does
+// not apply: 1 with at least one tile per CU; otherwise the K range is split
+// (2..4 ways, >= 8 K blocks each) when that fills at least half the CUs and
+// the workspace holds the fp32/int32 partials.  Shapes it declines take the
+// 128x128 kernel.
+static int tile_engine_splits(int64_t m, int64_t n, int K, const void* workspace, size_t ws_bytes) {
+  if (m * K >= ((int64_t)1 << 31) || n * K >= ((int64_t)1 << 31)) return 0;
+  const int64_t tiles = ((m + kTgBM - 1) / kTgBM) * ((n + kTgBN - 1) / kTgBN);
+  const int cus = tg_device_cus();
+  if (tiles >= cus) return 1;
+  const int kb = (K + kTgBK - 1) / kTgBK;
+  for (int s = (int)std::min<int64_t>(4, cus / tiles); s >= 2; --s)
+    if (kb / s >= 8 && tiles * s * 2 >= cus && workspace &&
+        (size_t)s * (size_t)(m * n) * 4 <= ws_bytes)
+      return s;
+  return 0;
+}
+
 template <int FMT>
 static int run_w8a8(const char* what, const uint8_t* xq, const uint8_t* w, int64_t m,
                     int64_t n, int64_t k, const Epi& ep, void* workspace, size_t ws_bytes,
@@ -538,10 +556,10 @@ static int run_w8a8(const char* what, const uint8_t* xq, const uint8_t* w, int64
   else if (m <= 16) launch_skinny<FMT, 1>(xq, w, K, ep, workspace, ws_bytes, stream);
   else if (m <= 32) launch_skinny<FMT, 2>(xq, w, K, ep, workspace, ws_bytes, stream);
   else if (m <= 64) launch_skinny<FMT, 4>(xq, w, K, ep, workspace, ws_bytes, stream);
-  else if (m * k < ((int64_t)1 << 31) && n * k < ((int64_t)1 << 31) &&
-           ((m + kTgBM - 1) / kTgBM) * ((n + kTgBN - 1) / kTgBN) >= tg_device_cus()) {
+  else if (const int splits = tile_engine_splits(m, n, K, workspace, ws_bytes)) {
     // persistent 256x256 MFMA tiles (kq_tile_gemm.h), scales in the epilogue;
-    // shapes with fewer 256x256 tiles than CUs keep the 128x128 kernel below
+    // with fewer tiles than CUs each tile's K range is split over `splits`
+    // work units whose raw accumulators the split-K reduce sums in order
     TileGemmArgs a{};
     a.x = xq; a.x_rows = (int)m; a.xs = ep.xscale; a.gather = nullptr; a.topk = 1;
     a.w = w; a.ws = ep.wscale; a.ws_per_channel = ep.ws_per_channel;
@@ -551,7 +569,14 @@ static int run_w8a8(const char* what, const uint8_t* xq, const uint8_t* w, int64
     a.ntiles = (int)((n + kTgBN - 1) / kTgBN);
     a.out = ep.out; a.out_dtype = ep.out_dtype; a.bias = ep.bias; a.bias_dtype = ep.bias_dtype;
     a.acc_out = ep.acc_out;
+    a.ksplit = splits;
+    a.partials = splits > 1 ? (uint32_t*)workspace : nullptr;
     tg_launch<FMT == kFmtI8 ? kTgI8 : kTgFp8, false, kTgEpiStore>(a, stream);
+    if (splits > 1) {
+      ReduceArgs r{workspace, splits, ep.M, ep.N, ep.xscale, ep.wscale, ep.ws_per_channel,
+                   ep.bias, ep.bias_dtype, ep.out, ep.out_dtype, ep.acc_out};
+      launch_splitk_reduce(FMT == kFmtI8 ? kReduceI8 : kReduceFp8, r, stream);
+    }
   } else {
     const int tiles_m = (int)((m + kTile - 1) / kTile);
     const int tiles_n = (int)((n + kTile - 1) / kTile);
@@ -564,6 +589,22 @@ static int run_w8a8(const char* what, const uint8_t* xq, const uint8_t* w, int64
 }  // namespace kq
 
 using namespace kq;
+
+extern "C" size_t kq_w8a8_workspace_size(int64_t m, int64_t n, int64_t k) {
+  if (m <= 0 || n <= 0 || k <= 0 || m > 0x7fffffff || n > 0x7fffffff || k > 0x7fffffff) return 0;
+  const size_t plane = (size_t)m * (size_t)n * 4;
+  if (m <= 64) {
+    // skinny split-K as launch_skinny doubles it (the INT8 K step is the
+    // smaller one, so it bounds both formats)
+    const int64_t tiles = (n + kSkinnyCols - 1) / kSkinnyCols;
+    const int64_t nsteps = (k + W8Traits<kFmtI8>::kStep - 1) / W8Traits<kFmtI8>::kStep;
+    int64_t s = 1;
+    while (tiles * s < 256 && nsteps / (s * 2 * kSkinnyWaves) >= 2) s *= 2;
+    return s > 1 ? plane * (size_t)s : 0;
+  }
+  const int s = tile_engine_splits(m, n, (int)k, (const void*)1, (size_t)-1);
+  return s > 1 ? plane * (size_t)s : 0;
+}
 
 extern "C" int kq_w8a8_i8_gemm(const int8_t* xq, const float* xscale, const int8_t* w,
                                const float* wscale, const void* bias, int bias_dtype,

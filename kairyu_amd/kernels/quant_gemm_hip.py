@@ -132,6 +132,13 @@ def _workspace(device: torch.device, nbytes: int = 0) -> torch.Tensor:
     return _native.workspace(device, nbytes)
 
 
+def _w8a8_workspace(device: torch.device, m: int, n: int, k: int) -> torch.Tensor:
+    """Workspace with room for every split-K form of a W8A8 call of this shape
+    (decode split-K partials, prefill tile-engine partials)."""
+
+    return _workspace(device, int(_native.library().kq_w8a8_workspace_size(m, n, k)))
+
+
 def _w4_workspace(device: torch.device, m: int, n: int, k: int, mode: int) -> torch.Tensor:
     need = int(_native.library().kq_w4a16_workspace_size(m, n, k, mode))
     return _workspace(device, need)
@@ -208,8 +215,8 @@ def fp8_linear_forward(
     )
     weight_scale = _f32(module.weight_scale)
     bias = _bias(module, add_bias)
-    ws = _workspace(x.device)
     m, k = flat.shape
+    ws = _w8a8_workspace(x.device, m, module.out_features, k)
     _native.call(
         "kq_w8a8_fp8_gemm",
         x_q.data_ptr(), x_scale.data_ptr(), module.weight.data_ptr(), weight_scale.data_ptr(),
@@ -230,8 +237,8 @@ def int8_linear_forward(x: torch.Tensor, module, *, add_bias: bool = True,
     x_q, x_scale = _quantize_activation(flat, torch.int8, 127.0)
     weight_scale = _f32(module.weight_scale)
     bias = _bias(module, add_bias)
-    ws = _workspace(x.device)
     m, k = flat.shape
+    ws = _w8a8_workspace(x.device, m, module.out_features, k)
     if accumulators is not None and (
         accumulators.dtype != torch.int32
         or tuple(accumulators.shape) != (m, module.out_features)

@@ -125,6 +125,48 @@ def test_fp8_decode_path_matches_oracle(cuda, k, m, per_channel):
     assert_close_fp(np32(out), pre, label=f"k={k} m={m}")
 
 
+# Prefill with fewer 256x256 tiles than CUs: the tile engine splits each
+# tile's K range over 2..4 work units and a reduce pass sums the raw partials
+# in split order (shapes for 4 / 3 / 2 splits on 256 CUs; the second one is
+# ragged in M, N (N % 8 != 0) and K).
+SPLITK_SHAPES = [(1024, 2048, 4096), (1000, 2044, 4160), (1280, 4096, 3072), (1024, 8192, 2048)]
+
+
+@pytest.mark.parametrize("m,n,k", SPLITK_SHAPES)
+def test_int8_tile_engine_split_k_bit_exact(cuda, m, n, k):
+    banner(f"int8 split-k m={m} n={n} k={k}")
+    module = _int8_module(k, n, seed=m + n).to(cuda)
+    x = torch.randn(m, k, generator=torch.Generator().manual_seed(k)).to(torch.bfloat16)
+    acc = torch.empty(m, n, dtype=torch.int32, device=cuda)
+    out = hip.int8_linear_forward(x.to(cuda), module, accumulators=acc)
+    expected, xq, xs, eacc = olinear.int8_forward(
+        np32(x), module.weight.cpu().numpy(), module.weight_scale.cpu().numpy(), np32(module.bias))
+    assert np.array_equal(acc.cpu().numpy().astype(np.int64), eacc)
+    assert np.array_equal(np32(out), expected)
+
+
+@pytest.mark.parametrize("m,n,k", SPLITK_SHAPES[:2])
+def test_fp8_tile_engine_split_k_matches_oracle(cuda, m, n, k):
+    banner(f"fp8 split-k m={m} n={n} k={k}")
+    module = _fp8_module(k, n, seed=m + n).to(cuda)
+    x = torch.randn(m, k, generator=torch.Generator().manual_seed(k)).to(torch.bfloat16)
+    out = module(x.to(cuda))
+    expected, _, _, pre = olinear.fp8_forward(np32(x), bits(module.weight), np32(module.weight_scale),
+                                              np32(module.bias))
+    assert_close_fp(np32(out), pre, label=f"m={m} n={n} k={k}")
+
+
+def test_w8a8_workspace_size_covers_split_k(cuda):
+    lib = hip._native.library()
+    cus = torch.cuda.get_device_properties(cuda).multi_processor_count
+    # C3 prefill: 8 x 16 tiles, split in two on 256 CUs
+    if cus == 256:
+        assert lib.kq_w8a8_workspace_size(2048, 4096, 14336) == 2 * 2048 * 4096 * 4
+    assert lib.kq_w8a8_workspace_size(8192, 4096, 14336) == 0   # a tile per CU already
+    assert lib.kq_w8a8_workspace_size(16, 4096, 14336) == 0     # decode fills the CUs
+    assert lib.kq_w8a8_workspace_size(0, 4096, 14336) == 0
+
+
 def test_int8_generic_k_path(cuda):
     banner("int8 generic k")
     module = _int8_module(72, 24, seed=3).to(cuda)
