@@ -35,6 +35,7 @@
 //     lane jj: base + 8*(jj%8) + 4*(jj/8) + i.
 #include "kq_common.h"
 #include "kq_splitk.h"
+#include "kq_tile_gemm.h"  // LDS-DMA helpers (tg_dma16 / tg_dma4), kTgOob
 
 #include <algorithm>
 
@@ -637,6 +638,231 @@ w4a16_gemv_kernel(W4Args a, GvPlan p) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Prefill GEMM (M > 16, load-time tiled weights, K % 128 == 0, group_size a
+// multiple of 128).  Output tile BM = 16*TM*WM activation rows x BN =
+// 16*TN*(8/WM) columns, 8 waves as WM x (8/WM); wave (wm, wn) owns TM row
+// blocks x TN column tiles of 16.  K advances 128 per stage; a stage holds
+//   x16  BM rows x 256 bytes (fp16, k in MFMA order, 16-byte chunk c of row r
+//        at c ^ (r & 15): the 16 lanes of one k-group read 16 banks),
+//   W    BN/16 column tiles x 1 KB (their tiled words of the stage's 4 steps),
+//   the stage's group scales (BN fp16) and zero words (BN/8),
+// all copied global -> LDS with buffer_load ... lds through a 3-stage ring:
+// stage k+2 is in flight while k computes (one barrier per stage).  The
+// dequantized weights are the MFMA A operand (v_mfma_f32_16x16x32_f16), x the
+// B operand, so a lane's four results are four consecutive columns of one row.
+// Dequantization is the GEMV's (exact fp16((q-z)*s)).  x16 is written by
+// w4a16_prep_x_mma_kernel: fp16, act-order gathered, and each 8-k chunk in
+// the [0,4,1,5,2,6,3,7] order of the weight nibble pairs.
+constexpr int kW4pStages = 3;
+
+template <int TM, int TN, int WM>
+struct W4pShape {
+  static constexpr int WN = 8 / WM;
+  static constexpr int BM = 16 * TM * WM;
+  static constexpr int BN = 16 * TN * WN;
+  static constexpr int XBytes = BM * 256;
+  static constexpr int WBytes = BN * 64;           // BN/16 tiles x 1 KB
+  static constexpr int SBytes = BN * 2;            // scales
+  static constexpr int ZBytes = BN / 2;            // zero words (BN/8 x 4)
+  static constexpr int Stage = XBytes + WBytes + SBytes + 256;  // zeros padded to one DMA4
+  static constexpr int XOps = BM / 4 / 8;          // 1 KB DMA16 per wave per stage
+  static constexpr int WOps = BN / 16 / 8;
+  static constexpr int SOps = SBytes / 256;        // DMA4 (256 bytes) instructions
+  static constexpr int Ops = XOps + WOps + 1;      // + one DMA4 per wave (scales, zeros or spare)
+  static_assert(XOps >= 1 && WOps >= 1 && SOps + 1 <= 8, "tile shape");
+};
+
+template <int TM, int TN, int WM>
+__global__ void __launch_bounds__(512)
+w4a16_prefill_kernel(W4Args a, int mblocks, int tiles) {
+  using S = W4pShape<TM, TN, WM>;
+  __shared__ __attribute__((aligned(16))) uint8_t smem[kW4pStages * S::Stage + 8 * 256];
+  const int lane = lane_id();
+  const int wave = __builtin_amdgcn_readfirstlane(wave_id());
+  const int wm = wave / S::WN, wn = wave % S::WN;
+  const int c = lane & 15, g = lane >> 4;
+  // XCD-contiguous tile ranges (row block fastest: an XCD's consecutive tiles
+  // share weight tiles in its L2)
+  const int per = (tiles + 7) / 8;
+  const int t = (blockIdx.x & 7) * per + (blockIdx.x >> 3);
+  if (t >= tiles) return;
+  const int mb = t % mblocks, nb = t / mblocks;
+  const int m0 = mb * S::BM, n0 = nb * S::BN;
+  const int K = a.K, nst = K / 128;
+  const int npad = (a.N + 15) / 16 * 16;
+  const int ngroups = K / a.G;
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)smem;
+
+  // buffer resources: reads past them return zeros
+  const i32x4 rx = make_rsrc(a.x, (uint32_t)((uint64_t)a.M * K * 2));
+  const i32x4 rw = make_rsrc(a.qw, (uint32_t)((uint64_t)(K / 8) * npad * 4));
+  const i32x4 rs = make_rsrc(a.sc, (uint32_t)((uint64_t)ngroups * a.N * 2));
+  const i32x4 rz = make_rsrc(a.qz, (uint32_t)((uint64_t)ngroups * (a.N / 8) * 4));
+
+  // per-lane DMA offsets (stage-independent parts)
+  int32_t xoff[S::XOps];
+#pragma unroll
+  for (int i = 0; i < S::XOps; ++i) {
+    const int blk = wave * S::XOps + i;           // 1 KB = 4 rows x 256 bytes
+    const int r = blk * 4 + (lane >> 4), pc = lane & 15;
+    const int lc = pc ^ (r & 15);                 // logical 16-byte chunk (8 k)
+    xoff[i] = m0 + r < a.M ? ((m0 + r) * K + lc * 8) * 2 : kTgOob;
+  }
+  int32_t woff[S::WOps];
+#pragma unroll
+  for (int i = 0; i < S::WOps; ++i) {
+    const int u = n0 / 16 + wave * S::WOps + i;   // column tile
+    woff[i] = u * 16 < a.N ? u * (K * 8) + lane * 16 : kTgOob;
+  }
+  // one DMA4 per wave: waves < SOps copy 256 bytes of scales, wave SOps the
+  // zero words, the rest a spare (out of range -> zeros) so that every wave
+  // issues S::Ops instructions per stage
+  int32_t aoff;
+  i32x4 ra;
+  uint32_t alds;
+  if (wave < S::SOps) {
+    ra = rs;
+    aoff = n0 + wave * 128 + 2 * lane < a.N ? (n0 + wave * 128 + 2 * lane) * 2 : kTgOob;
+    alds = S::XBytes + S::WBytes + wave * 256;
+  } else {
+    ra = rz;
+    aoff = (wave == S::SOps && lane < S::BN / 8 && n0 + lane * 8 < a.N) ? (n0 / 8 + lane) * 4 : kTgOob;
+    alds = wave == S::SOps ? S::XBytes + S::WBytes + S::SBytes : kW4pStages * S::Stage + wave * 256 - 0;
+  }
+  auto issue = [&](int kb, int slot) {
+    const uint32_t b = lds0 + slot * S::Stage;
+#pragma unroll
+    for (int i = 0; i < S::XOps; ++i) tg_dma16(rx, b + (wave * S::XOps + i) * 1024, xoff[i], kb * 256);
+#pragma unroll
+    for (int i = 0; i < S::WOps; ++i) tg_dma16(rw, b + S::XBytes + (wave * S::WOps + i) * 1024, woff[i], kb * 1024);
+    const int grp = (kb * 128) / a.G;
+    const int32_t so = wave < S::SOps ? grp * a.N * 2 : grp * (a.N / 8) * 4;
+    const uint32_t dst = wave <= S::SOps ? b + alds : lds0 + alds;
+    tg_dma4(ra, dst, aoff, so);
+  };
+
+  NibbleConsts nc;
+  nc.m0 = __builtin_amdgcn_readfirstlane(0x000f000fu);
+  nc.m1 = __builtin_amdgcn_readfirstlane(0x00f000f0u);
+  nc.c0 = 0x64006400u + (uint32_t)(lane & 0);
+  nc.c1 = 0x54005400u + (uint32_t)(lane & 0);
+  const uint32_t zsh = 4u * (uint32_t)(c & 7);
+
+  f32x4 acc[TN][TM];
+#pragma unroll
+  for (int tn = 0; tn < TN; ++tn)
+#pragma unroll
+    for (int i = 0; i < TM; ++i) acc[tn][i] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  issue(0, 0);
+  if (nst > 1) issue(1, 1);
+  if (nst > 1) __builtin_amdgcn_s_waitcnt(S::Ops == 4 ? 0x0004 : (S::Ops == 6 ? 0x0006 : 0x0007));
+  else __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+
+  for (int kb = 0; kb < nst; ++kb) {
+    const int slot = kb % kW4pStages;
+    if (kb + 2 < nst) issue(kb + 2, (kb + 2) % kW4pStages);
+    const uint8_t* st = smem + slot * S::Stage;
+    // this stage's scales and zeros of the wave's column tiles (one group)
+    uint32_t zq0[TN], zq1[TN], sq[TN];
+#pragma unroll
+    for (int tn = 0; tn < TN; ++tn) {
+      const int col = (wn * TN + tn) * 16 + c;
+      const uint32_t sv = *(const uint16_t*)(st + S::XBytes + S::WBytes + col * 2);
+      const uint32_t zw = *(const uint32_t*)(st + S::XBytes + S::WBytes + S::SBytes + (col >> 3) * 4);
+      const uint32_t z = ((zw >> zsh) & 0xfu) + a.zoff;
+      zq0[tn] = nc.c0 + z * 0x00010001u;
+      zq1[tn] = nc.c1 + z * 0x00100010u;
+      sq[tn] = sv * 0x00010001u;
+    }
+#pragma unroll
+    for (int s4 = 0; s4 < 4; ++s4) {
+      u32x4 A[TN];
+#pragma unroll
+      for (int tn = 0; tn < TN; ++tn) {
+        const uint32_t w = *(const uint32_t*)(st + S::XBytes + (wn * TN + tn) * 1024 + s4 * 256 + lane * 4);
+        const uint32_t y = w >> 8;
+        A[tn] = u32x4{pk_sub_mul(and_or(w, nc.m0, nc.c0), zq0[tn], sq[tn]),
+                      pk_sub_mul(and_or(w, nc.m1, nc.c1), zq1[tn], sq[tn]),
+                      pk_sub_mul(and_or(y, nc.m0, nc.c0), zq0[tn], sq[tn]),
+                      pk_sub_mul(and_or(y, nc.m1, nc.c1), zq1[tn], sq[tn])};
+      }
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        const int r = (wm * TM + i) * 16 + c;
+        const u32x4 B = *(const u32x4*)(st + r * 256 + (((s4 * 4 + g) ^ c) << 4));
+#pragma unroll
+        for (int tn = 0; tn < TN; ++tn) acc[tn][i] = mfma_f16(as_f16x8(A[tn]), as_f16x8(B), acc[tn][i]);
+      }
+    }
+    // stage kb+1 landed (stage kb+2's copies may stay in flight), and every
+    // wave is done with stage kb before it is refilled
+    if (kb + 2 < nst) __builtin_amdgcn_s_waitcnt(S::Ops == 4 ? 0x0004 : (S::Ops == 6 ? 0x0006 : 0x0007));
+    else __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+  }
+
+  // epilogue: lane (c, g) of block (tn, i) holds rows m = .. + c, columns
+  // n = .. + 4g .. 4g+3
+#pragma unroll
+  for (int tn = 0; tn < TN; ++tn) {
+    const int n = n0 + (wn * TN + tn) * 16 + 4 * g;
+    float bv[4] = {0.f, 0.f, 0.f, 0.f};
+    if (a.bias_dtype != KQ_DTYPE_NONE)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) bv[q] = n + q < a.N ? load_as_f32(a.bias, a.bias_dtype, n + q) : 0.f;
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      const int m = m0 + (wm * TM + i) * 16 + c;
+      if (m >= a.M) continue;
+      uint16_t o[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        float v = acc[tn][i][q];
+        if (a.bias_dtype != KQ_DTYPE_NONE) v = __fadd_rn(v, bv[q]);
+        o[q] = f32_to_out(v, a.out_dtype);
+      }
+      uint16_t* dst = a.out + (int64_t)m * a.N + n;
+      if (n + 3 < a.N) {
+        *(u32x2*)dst = u32x2{(uint32_t)o[0] | ((uint32_t)o[1] << 16), (uint32_t)o[2] | ((uint32_t)o[3] << 16)};
+      } else {
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          if (n + q < a.N) dst[q] = o[q];
+      }
+    }
+  }
+}
+
+// x16[m][8j + e] = fp16(x[m][perm(8j + o[e])]) with o = [0,4,1,5,2,6,3,7]
+// (perm = identity when null): the prefill kernel's activation operand.
+__global__ void __launch_bounds__(256)
+w4a16_prep_x_mma_kernel(const uint16_t* __restrict__ x, int dtype, int ldx,
+                        const int32_t* __restrict__ perm, int M, int K, uint16_t* __restrict__ x16) {
+  const int64_t idx = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 8;
+  if (idx >= (int64_t)M * K) return;
+  const int m = (int)(idx / K), k0 = (int)(idx % K);
+  const uint16_t* row = x + (int64_t)m * ldx;
+  uint16_t h[8];
+  if (perm) {
+    const i32x4 p0 = *(const i32x4*)(perm + k0);
+    const i32x4 p1 = *(const i32x4*)(perm + k0 + 4);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      h[e] = act_bits(row[p0[e]], dtype);
+      h[e + 4] = act_bits(row[p1[e]], dtype);
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) h[e] = act_bits(row[k0 + e], dtype);
+  }
+  const u32x4 v{(uint32_t)h[0] | ((uint32_t)h[4] << 16), (uint32_t)h[1] | ((uint32_t)h[5] << 16),
+                (uint32_t)h[2] | ((uint32_t)h[6] << 16), (uint32_t)h[3] | ((uint32_t)h[7] << 16)};
+  *(u32x4*)(x16 + idx) = v;
+}
+
 // x16[m][j] = fp16(x[m][perm[j]]) (act-order gather + W4A16 activation
 // conversion); each thread writes 8 consecutive outputs with one 16-byte store.
 __global__ void __launch_bounds__(64)
@@ -820,6 +1046,31 @@ static bool gv_plan(const W4Args& a, int fmt, int gmode, GvPlan* p, int* S, int*
   return true;
 }
 
+// Prefill GEMM conditions: tiled weights, M above the GEMV's range, whole
+// 128-k stages and groups, 32-bit byte offsets for x16 and the tiled weights.
+static bool prefill_applies(const W4Args& a, int gmode) {
+  return a.layout == kLayoutTiles && a.M > 16 && gmode != kGroupsPerK && a.K % 128 == 0 &&
+         a.G % 128 == 0 && (int64_t)a.M * a.K < ((int64_t)1 << 30) &&
+         (uint64_t)(a.K / 8) * (uint64_t)((a.N + 15) / 16 * 16) * 4u < ((uint64_t)1 << 31);
+}
+
+template <int TM, int TN, int WM>
+static void launch_prefill_shape(const W4Args& a, hipStream_t stream) {
+  using S = W4pShape<TM, TN, WM>;
+  const int mblocks = (a.M + S::BM - 1) / S::BM;
+  const int tiles = mblocks * ((a.N + S::BN - 1) / S::BN);
+  const int grid = 8 * ((tiles + 7) / 8);
+  hipLaunchKernelGGL((w4a16_prefill_kernel<TM, TN, WM>), dim3(grid), dim3(512), 0, stream, a, mblocks,
+                     tiles);
+}
+
+// 64 x 128 tiles up to M = 64 (twice the column tiles of 256-wide ones, and
+// no idle activation rows), 128 x 256 beyond.
+static void launch_prefill(const W4Args& a, hipStream_t stream) {
+  if (a.M <= 64) launch_prefill_shape<4, 1, 1>(a, stream);
+  else launch_prefill_shape<4, 4, 2>(a, stream);
+}
+
 template <int XDT, int S, int SPG>
 static void launch_gv_s(const W4Args& a, const GvPlan& p, int layout, hipStream_t st) {
   const bool one = (p.units + p.wgs - 1) / p.wgs <= GvShape<S, SPG>::kOneRound;
@@ -902,6 +1153,23 @@ static int run_w4(const char* what, int fmt, W4Args a, int gmode, void* workspac
     launch_gv(a, gp, xdt, gv_s, gv_spg, a.layout, stream);
     return check_launch(what);
   }
+  if (prefill_applies(a, gmode)) {
+    const size_t x16_bytes = (size_t)a.M * a.K * 2;
+    if (workspace == nullptr || ws_bytes < x16_bytes) {
+      set_error("%s: workspace of %zu bytes is smaller than the %zu bytes this call needs", what,
+                workspace ? ws_bytes : (size_t)0, x16_bytes);
+      return KQ_EWORKSPACE;
+    }
+    uint16_t* x16 = (uint16_t*)workspace;
+    const int64_t threads = (int64_t)a.M * a.K / 8;
+    hipLaunchKernelGGL(w4a16_prep_x_mma_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0,
+                       stream, a.x, a.x_dtype, a.ldx, gmode == kGroupsPermuted ? a.perm : nullptr,
+                       a.M, a.K, x16);
+    a.x = x16;
+    a.ldx = a.K;
+    launch_prefill(a, stream);
+    return check_launch(what);
+  }
   W4Plan p = plan_w4(a.M, a.N, a.K, needs_x16, ws_bytes, workspace != nullptr);
   if (p.x16_bytes + p.partial_bytes > (workspace ? ws_bytes : 0)) {
     set_error("%s: workspace of %zu bytes is smaller than the %zu bytes this call needs", what,
@@ -951,7 +1219,9 @@ extern "C" size_t kq_w4a16_workspace_size(int64_t m, int64_t n, int64_t k, int g
   // a generous workspace lets the planner choose split-K freely
   const W4Plan p = plan_w4((int)m, (int)n, (int)k, gidx_mode == kGroupsPermuted,
                            (size_t)1 << 40, true);
-  return p.x16_bytes + p.partial_bytes;
+  // the prefill GEMM (M > 16, tiled weights) stages fp16 x in the workspace
+  const size_t x16 = m > 16 ? ((size_t)m * (size_t)k * 2 + 255) / 256 * 256 : 0;
+  return std::max(p.x16_bytes + p.partial_bytes, x16);
 }
 
 extern "C" int kq_w4a16_awq_gemm(const void* x, int x_dtype, const int32_t* qweight,

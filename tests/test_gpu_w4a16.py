@@ -142,6 +142,29 @@ def test_awq_all_paths(cuda, m, dtype):
     assert_close_fp(np32(out), _oracle(module, x), label=f"m={m}")
 
 
+# Prefill GEMM (M > 16, tiled weights, K and group multiples of 128): 64x128
+# tiles up to M = 64, 128x256 beyond; N = 392 ends in a half-used 16-column
+# tile and a partial 128/256-column tile, M = 17 / 65 / 300 partial row tiles.
+@pytest.mark.parametrize("kind", ["awq", "gptq", "gptq_act_order"])
+@pytest.mark.parametrize("m", [17, 64, 65, 300])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_prefill_gemm_matches_oracle(cuda, kind, m, dtype):
+    banner(f"w4a16 prefill {kind} m={m} {dtype}")
+    k, n, group = 1024, 392, 128
+    g = torch.Generator().manual_seed(1000 + m)
+    if kind == "awq":
+        module = _awq_module(k, n, group=group, seed=m, random_packed=True)
+    else:
+        g_idx = (torch.randperm(k, generator=g) // group).to(torch.int32) if kind == "gptq_act_order" \
+            else (torch.arange(k) // group).to(torch.int32)
+        module = _gptq_module(k, n, group=group, seed=m, g_idx=g_idx, random_packed=True)
+        module.g_idx.copy_(g_idx)
+    module = module.to(cuda)
+    x = torch.randn(m, k, generator=g).to(dtype)
+    out = module(x.to(cuda))
+    assert_close_fp(np32(out), _oracle(module, x), label=f"{kind} m={m}")
+
+
 @pytest.mark.parametrize("mode", ["uniform", "act_order", "arbitrary"])
 @pytest.mark.parametrize("m", [1, 16, 33, 100])
 def test_gptq_group_modes(cuda, mode, m):
