@@ -642,19 +642,40 @@ w4a16_gemv_kernel(W4Args a, GvPlan p) {
 // Prefill GEMM (M > 16, load-time tiled weights, K % 128 == 0, group_size a
 // multiple of 128).  Output tile BM = 16*TM*WM activation rows x BN =
 // 16*TN*(8/WM) columns, 8 waves as WM x (8/WM); wave (wm, wn) owns TM row
-// blocks x TN column tiles of 16.  K advances 128 per stage; a stage holds
+// blocks x TN column tiles of 16.  Measured floor (C2 M = 512): without the
+// dequant and the MFMAs the kernel still takes 80% of its time, i.e. the
+// LDS fragment reads, the copies and the per-stage barrier bound it.  K advances 128 per stage; a stage holds
 //   x16  BM rows x 256 bytes (fp16, k in MFMA order, 16-byte chunk c of row r
 //        at c ^ (r & 15): the 16 lanes of one k-group read 16 banks),
 //   W    BN/16 column tiles x 1 KB (their tiled words of the stage's 4 steps),
 //   the stage's group scales (BN fp16) and zero words (BN/8),
-// all copied global -> LDS with buffer_load ... lds through a 3-stage ring:
-// stage k+2 is in flight while k computes (one barrier per stage).  The
+// all copied global -> LDS with buffer_load ... lds through an NS-stage ring:
+// stages k+1 .. k+NS-1 are in flight while k computes (one barrier per stage).  The
 // dequantized weights are the MFMA A operand (v_mfma_f32_16x16x32_f16), x the
 // B operand, so a lane's four results are four consecutive columns of one row.
 // Dequantization is the GEMV's (exact fp16((q-z)*s)).  x16 is written by
 // w4a16_prep_x_mma_kernel: fp16, act-order gathered, and each 8-k chunk in
 // the [0,4,1,5,2,6,3,7] order of the weight nibble pairs.
-constexpr int kW4pStages = 3;
+// vmcnt(N) (expcnt and lgkmcnt 0): the gfx9 immediate splits vmcnt in bits
+// 0-3 and 14-15
+template <int N>
+KQ_DEV void w4p_wait() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14));
+}
+// wait until at most `after` stages of OPS copies each remain in flight
+template <int OPS, int C>
+KQ_DEV void w4p_wait_stages(int after) {
+  if constexpr (C > 0) {
+    if (after >= C) {
+      w4p_wait<C * OPS>();
+      return;
+    }
+    w4p_wait_stages<OPS, C - 1>(after);
+  } else {
+    w4p_wait<0>();
+  }
+}
 
 template <int TM, int TN, int WM>
 struct W4pShape {
@@ -673,11 +694,11 @@ struct W4pShape {
   static_assert(XOps >= 1 && WOps >= 1 && SOps + 1 <= 8, "tile shape");
 };
 
-template <int TM, int TN, int WM>
+template <int TM, int TN, int WM, int NS>
 __global__ void __launch_bounds__(512)
 w4a16_prefill_kernel(W4Args a, int mblocks, int tiles) {
   using S = W4pShape<TM, TN, WM>;
-  __shared__ __attribute__((aligned(16))) uint8_t smem[kW4pStages * S::Stage + 8 * 256];
+  __shared__ __attribute__((aligned(16))) uint8_t smem[NS * S::Stage + 8 * 256];
   const int lane = lane_id();
   const int wave = __builtin_amdgcn_readfirstlane(wave_id());
   const int wm = wave / S::WN, wn = wave % S::WN;
@@ -728,7 +749,7 @@ w4a16_prefill_kernel(W4Args a, int mblocks, int tiles) {
   } else {
     ra = rz;
     aoff = (wave == S::SOps && lane < S::BN / 8 && n0 + lane * 8 < a.N) ? (n0 / 8 + lane) * 4 : kTgOob;
-    alds = wave == S::SOps ? S::XBytes + S::WBytes + S::SBytes : kW4pStages * S::Stage + wave * 256 - 0;
+    alds = wave == S::SOps ? S::XBytes + S::WBytes + S::SBytes : NS * S::Stage + wave * 256;
   }
   auto issue = [&](int kb, int slot) {
     const uint32_t b = lds0 + slot * S::Stage;
@@ -755,15 +776,15 @@ w4a16_prefill_kernel(W4Args a, int mblocks, int tiles) {
 #pragma unroll
     for (int i = 0; i < TM; ++i) acc[tn][i] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  issue(0, 0);
-  if (nst > 1) issue(1, 1);
-  if (nst > 1) __builtin_amdgcn_s_waitcnt(S::Ops == 4 ? 0x0004 : (S::Ops == 6 ? 0x0006 : 0x0007));
-  else __builtin_amdgcn_s_waitcnt(0);
+#pragma unroll
+  for (int i = 0; i < NS - 1; ++i)
+    if (i < nst) issue(i, i);
+  w4p_wait_stages<S::Ops, NS - 2>(min(NS - 2, nst - 1));
   __syncthreads();
 
   for (int kb = 0; kb < nst; ++kb) {
-    const int slot = kb % kW4pStages;
-    if (kb + 2 < nst) issue(kb + 2, (kb + 2) % kW4pStages);
+    const int slot = kb % NS;
+    if (kb + NS - 1 < nst) issue(kb + NS - 1, (kb + NS - 1) % NS);
     const uint8_t* st = smem + slot * S::Stage;
     // this stage's scales and zeros of the wave's column tiles (one group)
     uint32_t zq0[TN], zq1[TN], sq[TN];
@@ -797,10 +818,9 @@ w4a16_prefill_kernel(W4Args a, int mblocks, int tiles) {
         for (int tn = 0; tn < TN; ++tn) acc[tn][i] = mfma_f16(as_f16x8(A[tn]), as_f16x8(B), acc[tn][i]);
       }
     }
-    // stage kb+1 landed (stage kb+2's copies may stay in flight), and every
-    // wave is done with stage kb before it is refilled
-    if (kb + 2 < nst) __builtin_amdgcn_s_waitcnt(S::Ops == 4 ? 0x0004 : (S::Ops == 6 ? 0x0006 : 0x0007));
-    else __builtin_amdgcn_s_waitcnt(0);
+    // stage kb+1 landed (the stages issued after it may stay in flight), and
+    // every wave is done with stage kb before it is refilled
+    w4p_wait_stages<S::Ops, NS - 2>(min(NS - 2, nst - 2 - kb));
     __syncthreads();
   }
 
@@ -1054,21 +1074,24 @@ static bool prefill_applies(const W4Args& a, int gmode) {
          (uint64_t)(a.K / 8) * (uint64_t)((a.N + 15) / 16 * 16) * 4u < ((uint64_t)1 << 31);
 }
 
-template <int TM, int TN, int WM>
+template <int TM, int TN, int WM, int NS>
 static void launch_prefill_shape(const W4Args& a, hipStream_t stream) {
   using S = W4pShape<TM, TN, WM>;
   const int mblocks = (a.M + S::BM - 1) / S::BM;
   const int tiles = mblocks * ((a.N + S::BN - 1) / S::BN);
   const int grid = 8 * ((tiles + 7) / 8);
-  hipLaunchKernelGGL((w4a16_prefill_kernel<TM, TN, WM>), dim3(grid), dim3(512), 0, stream, a, mblocks,
+  hipLaunchKernelGGL((w4a16_prefill_kernel<TM, TN, WM, NS>), dim3(grid), dim3(512), 0, stream, a, mblocks,
                      tiles);
 }
 
-// 64 x 128 tiles up to M = 64 (twice the column tiles of 256-wide ones, and
-// no idle activation rows), 128 x 256 beyond.
+// 64 x 128 tiles up to M = 64 (twice the column tiles of 256-wide ones, no
+// idle activation rows; a 4-stage ring), 128 x 256 beyond with all 8 waves
+// side by side along N (each weight word dequantized once per tile).
+// Measured on C2 (N = 28672, K = 4096): M = 64 34.4 -> 33.4 us against
+// 3 stages; M = 512 152 -> 140 us against 2 x 4 waves of 64 x 64.
 static void launch_prefill(const W4Args& a, hipStream_t stream) {
-  if (a.M <= 64) launch_prefill_shape<4, 1, 1>(a, stream);
-  else launch_prefill_shape<4, 4, 2>(a, stream);
+  if (a.M <= 64) launch_prefill_shape<4, 1, 1, 4>(a, stream);
+  else launch_prefill_shape<8, 2, 1, 3>(a, stream);
 }
 
 template <int XDT, int S, int SPG>
