@@ -250,6 +250,38 @@ def test_graph_replays_match_eager(cuda):
         torch.cuda.synchronize()
 
 
+def test_graph_replays_prefill_and_gemv_paths(cuda):
+    """The prefill GEMM (both tile shapes, act-order included) and the decode
+    GEMV captured in one graph; every replay matches eager."""
+    banner("w4a16 graph replay: prefill + gemv")
+    awq = _awq_module(1024, 392, group=128, seed=21, random_packed=True).to(cuda)
+    gptq = _gptq_module(1024, 392, group=128, seed=22, random_packed=True,
+                        g_idx=(torch.randperm(1024) // 128).to(torch.int32)).to(cuda)
+    gemv = _gptq_module(4096, 4096, group=128, seed=23, random_packed=True).to(cuda)
+    cases = ((awq, torch.randn(64, 1024, device=cuda, dtype=torch.float16)),
+             (gptq, torch.randn(300, 1024, device=cuda, dtype=torch.bfloat16)),
+             (gemv, torch.randn(16, 4096, device=cuda, dtype=torch.float16)))
+    eager = [m(x).clone() for m, x in cases]
+    torch.cuda.synchronize()
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        for _ in range(2):
+            for m, x in cases:
+                m(x)
+    torch.cuda.current_stream().wait_stream(stream)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        outs = [m(x) for m, x in cases]
+    for step in range(4):
+        graph.replay()
+        torch.cuda.synchronize()
+        for i, (o, e) in enumerate(zip(outs, eager)):
+            assert torch.equal(o, e), (step, i)
+        gptq(cases[1][1] * 0.5)
+        torch.cuda.synchronize()
+
+
 # Decode GEMV (M <= 16, >= 128 column blocks of 16, group_size % 32 == 0):
 # K tails, per-step / per-window groups, partial last column block, several
 # K chunks per wave, several column blocks per workgroup, act-order gather.

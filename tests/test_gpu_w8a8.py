@@ -332,6 +332,41 @@ def test_rejects_k_mismatch_and_misplaced_payload(cuda):
 
 
 # ------------------------------------------------------------- graphs
+def test_graph_replays_decode_and_split_k_paths(cuda):
+    """The decode kernel (M <= 16, N = 4104) and the tile engine's split-K
+    prefill (M = 1024, N = 2048: partials in the workspace, then the reduce)
+    captured in one graph; every replay matches eager, with other eager work
+    on the shared workspace between replays."""
+    banner("w8a8 graph replay: decode + split-k")
+    dec_i8 = _int8_module(4096, DECODE_N, seed=11).to(cuda)
+    dec_f8 = _fp8_module(4096, DECODE_N, seed=12).to(cuda)
+    sk_i8 = _int8_module(4096, 2048, seed=13).to(cuda)
+    sk_f8 = _fp8_module(4096, 2048, seed=14).to(cuda)
+    xd = torch.randn(16, 4096, device=cuda, dtype=torch.bfloat16)
+    xp = torch.randn(1024, 4096, device=cuda, dtype=torch.bfloat16)
+    mods = ((dec_i8, xd), (dec_f8, xd), (sk_i8, xp), (sk_f8, xp))
+    eager = [m(x).clone() for m, x in mods]
+    torch.cuda.synchronize()
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        for _ in range(2):
+            for m, x in mods:
+                m(x)
+    torch.cuda.current_stream().wait_stream(stream)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        outs = [m(x) for m, x in mods]
+    for step in range(4):
+        graph.replay()
+        torch.cuda.synchronize()
+        for i, (o, e) in enumerate(zip(outs, eager)):
+            assert torch.equal(o, e), (step, i)
+        sk_f8(xp * 0.5)
+        dec_i8(xd * 2.0)
+        torch.cuda.synchronize()
+
+
 def test_graph_replays_match_eager(cuda):
     banner("w8a8 graph replay")
     int8_mod = _int8_module(3584, 160, seed=5).to(cuda)
