@@ -94,6 +94,28 @@ int kq_w8a8_fp8_gemm(const uint8_t* xq, const float* xscale, const uint8_t* w,
                      int bias_dtype, void* out, int out_dtype, int64_t m, int64_t n,
                      int64_t k, void* workspace, size_t workspace_bytes, void* stream);
 
+/* Per-token activation quantization fused with the W8A8 GEMM: x fp16/bf16
+ * [m, k] (row pitch ldx) is quantized exactly as kq_act_quant_i8 /
+ * kq_act_quant_fp8 would (INT8 dynamic; FP8 scale_mode 0 dynamic, 1 static
+ * scale_in[0], 2 per-row scale_in[m]) and multiplied with w as
+ * kq_w8a8_i8_gemm / kq_w8a8_fp8_gemm do.  Small decode batches quantize
+ * inside the GEMM launch; other shapes stage the quantized rows in the
+ * workspace (kq_w8a8_linear_workspace_size bytes).  Replaces the
+ * _quantize_activation + GEMM pair of int8_linear_forward / fp8_linear_forward
+ * (quant_gemm_gpu.py:538-572, :596-687). */
+int kq_w8a8_i8_linear(const void* x, int x_dtype, int64_t ldx, const int8_t* w,
+                      const float* wscale, const void* bias, int bias_dtype, void* out,
+                      int out_dtype, int32_t* acc_out, int64_t m, int64_t n, int64_t k,
+                      void* workspace, size_t workspace_bytes, void* stream);
+int kq_w8a8_fp8_linear(const void* x, int x_dtype, int64_t ldx, const float* scale_in,
+                       int scale_mode, const uint8_t* w, const float* wscale,
+                       int wscale_per_channel, const void* bias, int bias_dtype, void* out,
+                       int out_dtype, int64_t m, int64_t n, int64_t k, void* workspace,
+                       size_t workspace_bytes, void* stream);
+/* Workspace bytes for kq_w8a8_{i8,fp8}_linear of this shape (quantized rows,
+ * row scales, and every split-K form).  No counterpart in the reference. */
+size_t kq_w8a8_linear_workspace_size(int64_t m, int64_t n, int64_t k);
+
 /* Bytes of workspace with which every split-K form of the two W8A8 entry
  * points is available for this shape (0: none applies).  No counterpart in
  * the reference (its GPU path calls torch._scaled_mm / Triton, which allocate

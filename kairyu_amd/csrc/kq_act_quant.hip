@@ -75,11 +75,6 @@ KQ_DEV float block_max(float v, float* red) {
   return r;
 }
 
-// Clamp that keeps NaN (torch.clamp semantics).
-KQ_DEV float clamp_keep_nan(float v, float lim) {
-  return v < -lim ? -lim : (v > lim ? lim : v);
-}
-
 // Single-pass row kernels: each thread holds NCH chunks of 8 elements of the
 // row in registers (chunk c = tid + blockDim.x * i), so the row is read from
 // HBM once; the amax is reduced across the workgroup and the quantized bytes

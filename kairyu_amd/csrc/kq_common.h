@@ -117,6 +117,11 @@ KQ_DEV float div_by_recip(float v, float s, float r) {
 // max(amax, floor) that keeps a NaN amax (torch.clamp / numpy.maximum)
 KQ_DEV float max_keep_nan(float a, float floor) { return a != a ? a : fmaxf(a, floor); }
 
+// Clamp that keeps NaN (torch.clamp semantics).
+KQ_DEV float clamp_keep_nan(float v, float lim) {
+  return v < -lim ? -lim : (v > lim ? lim : v);
+}
+
 KQ_DEV float e4m3_to_f32(uint32_t b) {
   uint32_t s = b & 0x80u, e = (b >> 3) & 0xfu, m = b & 7u;
   float v;

@@ -347,6 +347,246 @@ static void launch_decode(const uint8_t* xq, const uint8_t* w, int K, const Epi&
   else launch_decode_nw<FMT, 2, 2>(xq, w, K, ep, stream);
 }
 
+// ------------------------------------------------------ decode, fused quant
+// Small M with unquantized fp16 / bf16 activations: the per-token quantization
+// runs inside the decode launch.  Every workgroup reads the M rows once for
+// their amax (after its first weight copies are issued), then each wave copies
+// 128-element slices of raw rows 0..3 into its ring next to the weights (one
+// 1 KB instruction per stage), quantizes the first MR rows in place into the
+// fragment layout of the plain decode kernel (64/MR lanes per row, 2*MR
+// elements per lane) and runs the same MFMAs; fragment rows >= MR read a zero
+// block.  The bytes are the per-token quantizers' (kq_act_quant.hip): an
+// element takes the reciprocal path when it is finite and the row scale lies
+// in [2^-60, FLT_MAX] (there both paths give the same byte), otherwise IEEE
+// division -- decided per wave and stage, so they match the quantizer's
+// row-level choice; the row scale enters in the epilogue.
+template <int FMT, int R, int NW, int MR>
+__global__ void __launch_bounds__(64 * NW)
+w8a8_decode_quant_kernel(const uint16_t* __restrict__ x, int x_dtype, int ldx, int scale_mode,
+                         const float* __restrict__ scale_in, const uint8_t* __restrict__ w, int K,
+                         Epi ep) {
+  constexpr int TF = FMT == kFmtFp8 ? kTgFp8 : kTgI8;
+  constexpr int OPS = 3;            // 2 weight + 1 activation DMA instructions per stage
+  constexpr int LPR = 64 / MR;      // quantizing lanes per row
+  constexpr int EPL = 128 / LPR;    // elements per lane and stage
+  constexpr float QMAX = FMT == kFmtFp8 ? 448.0f : 127.0f;
+  using Acc = typename W8Traits<FMT>::Acc;
+  __shared__ __attribute__((aligned(16))) uint8_t ring[NW * R * kDecStage];
+  __shared__ __attribute__((aligned(16))) uint8_t zero_rows[128];
+  __shared__ uint32_t red[(NW > 1 ? NW - 1 : 1) * 4 * 64];
+  __shared__ uint32_t wmax[NW][MR];
+  __shared__ float srow[MR];
+  const int lane = lane_id();
+  const int wave = __builtin_amdgcn_readfirstlane(wave_id());
+  const int j = lane & 15, kg = lane >> 4;
+  const int n0 = blockIdx.x * kSkinnyCols;
+  const int M = ep.M;
+  const int nst = K / 128;
+  const int per_wave = (nst + NW - 1) / NW;
+  const int sbeg = wave * per_wave;
+  const int nmy = max(0, min(nst, sbeg + per_wave) - sbeg);
+  const i32x4 rw = make_rsrc(w + (int64_t)n0 * K, (uint32_t)(min(kSkinnyCols, ep.N - n0) * K));
+  const i32x4 rx = make_rsrc(x, (uint32_t)(((int64_t)(M - 1) * ldx + K) * 2));
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)ring +
+                        wave * R * kDecStage;
+  int32_t vw[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int r = 8 * h + (lane >> 3), c = tg_chunk<TF>(r, lane & 7);
+    vw[h] = r * K + c * 16;
+  }
+  const int xr = lane >> 4;  // raw rows 0..3, 16 chunks of 8 elements each
+  const int32_t vx = xr < M ? (xr * ldx + (lane & 15) * 8) * 2 : kTgOob;
+  auto issue = [&](int st, int q) {
+    const uint32_t b = lds0 + q * kDecStage;
+    const int32_t sw = __builtin_amdgcn_readfirstlane(st * 128);
+    const int32_t sx = __builtin_amdgcn_readfirstlane(st * 256);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) tg_dma16(rw, b + h * 1024, vw[h], sw);
+    tg_dma16(rx, b + 2048, vx, sx);
+  };
+#pragma unroll
+  for (int i = 0; i < R - 1; ++i)
+    if (i < nmy) issue(sbeg + i, i);
+  if (threadIdx.x < 8) *(i32x4*)(zero_rows + threadIdx.x * 16) = i32x4{0, 0, 0, 0};
+
+  // row scales
+  if (scale_mode == 0) {
+#pragma unroll
+    for (int r = 0; r < MR; ++r) {
+      uint32_t mx = 0;
+      if (r < M) {
+        for (int c = (int)threadIdx.x; c < K / 8; c += 64 * NW) {
+          const u32x4 raw = *(const u32x4*)(x + (int64_t)r * ldx + c * 8);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const uint16_t lo = (uint16_t)(raw[e] & 0xffffu), hi = (uint16_t)(raw[e] >> 16);
+            const float flo = x_dtype == KQ_DTYPE_BF16 ? bf16_to_f32(lo) : f16_to_f32(lo);
+            const float fhi = x_dtype == KQ_DTYPE_BF16 ? bf16_to_f32(hi) : f16_to_f32(hi);
+            mx = max(mx, max(__float_as_uint(flo) & 0x7fffffffu, __float_as_uint(fhi) & 0x7fffffffu));
+          }
+        }
+      }
+#pragma unroll
+      for (int off = 32; off > 0; off >>= 1) mx = max(mx, (uint32_t)__shfl_xor((int)mx, off, 64));
+      if (lane == 0) wmax[wave][r] = mx;
+    }
+    __syncthreads();
+    if ((int)threadIdx.x < min(M, MR)) {
+      uint32_t mx = wmax[0][threadIdx.x];
+      for (int w2 = 1; w2 < NW; ++w2) mx = max(mx, wmax[w2][threadIdx.x]);
+      srow[threadIdx.x] = __fdiv_rn(max_keep_nan(__uint_as_float(mx), 1e-12f), QMAX);
+    }
+  } else if ((int)threadIdx.x < min(M, MR)) {
+    srow[threadIdx.x] = scale_mode == 1 ? scale_in[0] : scale_in[threadIdx.x];
+  }
+  __syncthreads();
+
+  // this lane's quantization row and EPL-element slice of every stage
+  const int qr = lane / LPR, qe = (lane % LPR) * EPL;
+  const float s = qr < M ? srow[qr] : 1.0f;
+  const float rs = __fdiv_rn(1.0f, s);
+  const bool s_ok = s >= 0x1p-60f && s <= 3.4028235e38f;
+  const int qdst = 2048 + qr * 128 + (tg_chunk<TF>(qr, qe >> 4) << 4) + (qe & 15);
+  // fragment offsets: rows < MR in the stage, rows >= MR in the zero block
+  const int o_lo = j * 128 + (tg_chunk<TF>(j, FMT == kFmtFp8 ? 2 * kg : kg) << 4);
+  const int o_hi = j * 128 + (tg_chunk<TF>(j, FMT == kFmtFp8 ? 2 * kg + 1 : 4 + kg) << 4);
+  const uint8_t* mine = ring + wave * R * kDecStage;
+
+  Acc acc = Acc{0, 0, 0, 0};
+  for (int i = 0; i < nmy; ++i) {
+    if (i + R - 1 < nmy) issue(sbeg + i + R - 1, (i + R - 1) % R);
+    const int ahead = min(R - 1, nmy - 1 - i);
+    if (ahead >= 3) wait_vm<3 * OPS>();
+    else if (ahead == 2) wait_vm<2 * OPS>();
+    else if (ahead == 1) wait_vm<OPS>();
+    else wait_vm<0>();
+    uint8_t* q = (uint8_t*)mine + (i % R) * kDecStage;
+    {
+      const uint8_t* src = q + 2048 + qr * 256 + qe * 2;
+      uint32_t raw[EPL / 2];
+      if constexpr (EPL == 8) {
+        const u32x4 t = *(const u32x4*)src;
+        raw[0] = t[0]; raw[1] = t[1]; raw[2] = t[2]; raw[3] = t[3];
+      } else if constexpr (EPL == 4) {
+        const u32x2 t = *(const u32x2*)src;
+        raw[0] = t[0]; raw[1] = t[1];
+      } else {
+        raw[0] = *(const uint32_t*)src;
+      }
+      float v[EPL];
+#pragma unroll
+      for (int e = 0; e < EPL / 2; ++e) {
+        const uint16_t lo = (uint16_t)(raw[e] & 0xffffu), hi = (uint16_t)(raw[e] >> 16);
+        v[2 * e] = x_dtype == KQ_DTYPE_BF16 ? bf16_to_f32(lo) : f16_to_f32(lo);
+        v[2 * e + 1] = x_dtype == KQ_DTYPE_BF16 ? bf16_to_f32(hi) : f16_to_f32(hi);
+      }
+      bool fast = s_ok;
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) fast = fast && (__float_as_uint(v[e]) & 0x7fffffffu) < 0x7f800000u;
+      uint32_t b[EPL];
+      if (__builtin_amdgcn_read_exec() == __ballot(fast)) {
+        float t[EPL];
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) t[e] = fminf(fmaxf(div_by_recip(v[e], s, rs), -QMAX), QMAX);
+        if constexpr (FMT == kFmtFp8) {
+#pragma unroll
+          for (int e = 0; e < EPL; e += 2) {
+            const uint32_t pk = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(t[e], t[e + 1], 0, false);
+            b[e] = pk & 0xffu;
+            b[e + 1] = (pk >> 8) & 0xffu;
+          }
+        } else {
+#pragma unroll
+          for (int e = 0; e < EPL; ++e) b[e] = (uint32_t)(int32_t)__builtin_rintf(t[e]) & 0xffu;
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) {
+          const float t = clamp_keep_nan(__fdiv_rn(v[e], s), QMAX);
+          b[e] = FMT == kFmtFp8 ? f32_to_e4m3(t) : ((uint32_t)(int32_t)__builtin_rintf(t) & 0xffu);
+        }
+      }
+      // in place: this wave's reads of the raw slice precede its writes
+      if constexpr (EPL == 8) {
+        *(u32x2*)(q + qdst) = u32x2{b[0] | (b[1] << 8) | (b[2] << 16) | (b[3] << 24),
+                                    b[4] | (b[5] << 8) | (b[6] << 16) | (b[7] << 24)};
+      } else if constexpr (EPL == 4) {
+        *(uint32_t*)(q + qdst) = b[0] | (b[1] << 8) | (b[2] << 16) | (b[3] << 24);
+      } else {
+        *(uint16_t*)(q + qdst) = (uint16_t)(b[0] | (b[1] << 8));
+      }
+    }
+    const uint8_t* fx = j < MR ? q + 2048 : zero_rows;
+    const int xo_lo = j < MR ? o_lo : (o_lo & 127), xo_hi = j < MR ? o_hi : (o_hi & 127);
+    const i32x4 wl = *(const i32x4*)(q + o_lo), wh = *(const i32x4*)(q + o_hi);
+    const i32x4 xl = *(const i32x4*)(fx + xo_lo), xh = *(const i32x4*)(fx + xo_hi);
+    if constexpr (FMT == kFmtFp8) {
+      acc = mfma_fp8(i32x8{xl[0], xl[1], xl[2], xl[3], xh[0], xh[1], xh[2], xh[3]},
+                     i32x8{wl[0], wl[1], wl[2], wl[3], wh[0], wh[1], wh[2], wh[3]}, acc);
+    } else {
+      acc = mfma_i8(xl, wl, acc);
+      acc = mfma_i8(xh, wh, acc);
+    }
+  }
+
+  if (wave > 0) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) red[((wave - 1) * 4 + r) * 64 + lane] = acc_bits(acc, r);
+  }
+  __syncthreads();
+  if (wave != 0) return;
+  for (int w2 = 1; w2 < NW; ++w2)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const uint32_t bits = red[((w2 - 1) * 4 + r) * 64 + lane];
+      if constexpr (FMT == kFmtI8) acc[r] += (int)bits;
+      else acc[r] = __fadd_rn(acc[r], __uint_as_float(bits));
+    }
+  const int n = n0 + j;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int m = kg * 4 + r;
+    if (m >= M || n >= ep.N) continue;
+    float v;
+    if constexpr (FMT == kFmtI8) {
+      if (ep.acc_out) ep.acc_out[(int64_t)m * ep.N + n] = acc[r];
+      v = (float)acc[r];
+    } else {
+      v = acc[r];
+    }
+    v = __fmul_rn(v, srow[m]);
+    v = __fmul_rn(v, ep.ws_per_channel ? ep.wscale[n] : ep.wscale[0]);
+    if (ep.bias_dtype != KQ_DTYPE_NONE) v = __fadd_rn(v, load_as_f32(ep.bias, ep.bias_dtype, n));
+    ((uint16_t*)ep.out)[(int64_t)m * ep.N + n] = f32_to_out(v, ep.out_dtype);
+  }
+}
+
+template <int FMT, int MR>
+static void launch_decode_quant_mr(const uint16_t* x, int x_dtype, int ldx, int scale_mode,
+                                   const float* scale_in, const uint8_t* w, int K, const Epi& ep,
+                                   hipStream_t stream) {
+  const int nst = K / 128;
+  const dim3 grid((ep.N + kSkinnyCols - 1) / kSkinnyCols);
+  if (nst >= 64)
+    hipLaunchKernelGGL((w8a8_decode_quant_kernel<FMT, 4, 8, MR>), grid, dim3(512), 0, stream, x,
+                       x_dtype, ldx, scale_mode, scale_in, w, K, ep);
+  else if (nst >= 32)
+    hipLaunchKernelGGL((w8a8_decode_quant_kernel<FMT, 4, 4, MR>), grid, dim3(256), 0, stream, x,
+                       x_dtype, ldx, scale_mode, scale_in, w, K, ep);
+  else
+    hipLaunchKernelGGL((w8a8_decode_quant_kernel<FMT, 2, 2, MR>), grid, dim3(128), 0, stream, x,
+                       x_dtype, ldx, scale_mode, scale_in, w, K, ep);
+}
+
+// One activation row (MR = 1); the kernel also takes MR = 2 and 4.
+template <int FMT>
+static void launch_decode_quant(const uint16_t* x, int x_dtype, int ldx, int scale_mode,
+                                const float* scale_in, const uint8_t* w, int K, const Epi& ep,
+                                hipStream_t stream) {
+  launch_decode_quant_mr<FMT, 1>(x, x_dtype, ldx, scale_mode, scale_in, w, K, ep, stream);
+}
+
 // ------------------------------------------------------------------- tiled
 constexpr int kTile = 128;      // BM = BN = BK(bytes) = 128
 constexpr int kTileBytes = kTile * kTile;
@@ -590,6 +830,64 @@ static int run_w8a8(const char* what, const uint8_t* xq, const uint8_t* w, int64
 
 using namespace kq;
 
+// Rows up to which the fused decode path quantizes inside the GEMM launch.
+// Every workgroup repeats the quantization of its K slices, so the saved
+// launch pays only for one row (graph replay, C3 / C4 shapes: FP8 14.2 vs
+// 16.2 us, INT8 15.9 vs 17.1 us at M = 1; even at M = 2; slower from M = 3).
+constexpr int kFusedMaxRows = 1;
+
+// Quantize + GEMM: the fused decode launch where it applies, otherwise the
+// per-token quantizer into the workspace (bytes, then fp32 row scales) and
+// the GEMM dispatch of run_w8a8 on the rest of the workspace.
+template <int FMT>
+static int run_linear(const char* what, const void* x, int x_dtype, int64_t ldx, int scale_mode,
+                      const float* scale_in, const uint8_t* w, int64_t m, int64_t n, int64_t k,
+                      Epi ep, void* workspace, size_t ws_bytes, hipStream_t stream) {
+  if (x_dtype != KQ_DTYPE_F16 && x_dtype != KQ_DTYPE_BF16) {
+    set_error("%s: activation dtype must be fp16 or bf16 (code %d)", what, x_dtype);
+    return KQ_EUNSUPPORTED;
+  }
+  if (m < 0 || n < 1 || k < 1 || ldx < k || m > 0x7fffffff || n > 0x7fffffff || k > 65536) {
+    set_error("%s: bad shape m=%lld n=%lld k=%lld ldx=%lld", what, (long long)m, (long long)n,
+              (long long)k, (long long)ldx);
+    return KQ_EINVAL;
+  }
+  if (ep.out_dtype != KQ_DTYPE_F16 && ep.out_dtype != KQ_DTYPE_BF16) {
+    set_error("%s: output dtype must be fp16 or bf16", what);
+    return KQ_EUNSUPPORTED;
+  }
+  if (m == 0) return KQ_OK;
+  if (m > 0 && x == nullptr) {
+    set_error("%s: null activation", what);
+    return KQ_EINVAL;
+  }
+  const int K = (int)k;
+  if (m <= kFusedMaxRows && K % 128 == 0 && (n + kSkinnyCols - 1) / kSkinnyCols >= tg_device_cus() &&
+      ((uintptr_t)x % 16) == 0 && (ldx % 8) == 0 && ((uintptr_t)w % 16) == 0 &&
+      ((m - 1) * ldx + k) * 2 < ((int64_t)1 << 31) && n * k < ((int64_t)1 << 32)) {
+    ep.xscale = nullptr;
+    launch_decode_quant<FMT>((const uint16_t*)x, x_dtype, (int)ldx, scale_mode, scale_in, w, K, ep,
+                             stream);
+    return check_launch(what);
+  }
+  const size_t xq_bytes = ((size_t)m * (size_t)k + 255) / 256 * 256;
+  const size_t xs_bytes = ((size_t)m * 4 + 255) / 256 * 256;
+  if (workspace == nullptr || ws_bytes < xq_bytes + xs_bytes) {
+    set_error("%s: workspace of %zu bytes is smaller than the %zu bytes this call needs", what,
+              workspace ? ws_bytes : (size_t)0, xq_bytes + xs_bytes);
+    return KQ_EWORKSPACE;
+  }
+  uint8_t* xq = (uint8_t*)workspace;
+  float* xs = (float*)(xq + xq_bytes);
+  const int rc = FMT == kFmtI8
+                     ? kq_act_quant_i8(x, x_dtype, m, k, ldx, (int8_t*)xq, xs, stream)
+                     : kq_act_quant_fp8(x, x_dtype, m, k, ldx, scale_in, scale_mode, xq, xs, stream);
+  if (rc != KQ_OK) return rc;
+  ep.xscale = xs;
+  return run_w8a8<FMT>(what, xq, w, m, n, k, ep, xq + xq_bytes + xs_bytes,
+                       ws_bytes - xq_bytes - xs_bytes, stream);
+}
+
 extern "C" size_t kq_w8a8_workspace_size(int64_t m, int64_t n, int64_t k) {
   if (m <= 0 || n <= 0 || k <= 0 || m > 0x7fffffff || n > 0x7fffffff || k > 0x7fffffff) return 0;
   const size_t plane = (size_t)m * (size_t)n * 4;
@@ -625,4 +923,35 @@ extern "C" int kq_w8a8_fp8_gemm(const uint8_t* xq, const float* xscale, const ui
          (int)m, (int)n};
   return run_w8a8<kFmtFp8>("kq_w8a8_fp8_gemm", xq, w, m, n, k, ep, workspace, workspace_bytes,
                            (hipStream_t)stream);
+}
+
+extern "C" size_t kq_w8a8_linear_workspace_size(int64_t m, int64_t n, int64_t k) {
+  if (m <= 0 || n <= 0 || k <= 0) return 0;
+  return ((size_t)m * (size_t)k + 255) / 256 * 256 + ((size_t)m * 4 + 255) / 256 * 256 +
+         kq_w8a8_workspace_size(m, n, k);
+}
+
+extern "C" int kq_w8a8_i8_linear(const void* x, int x_dtype, int64_t ldx, const int8_t* w,
+                                 const float* wscale, const void* bias, int bias_dtype, void* out,
+                                 int out_dtype, int32_t* acc_out, int64_t m, int64_t n, int64_t k,
+                                 void* workspace, size_t workspace_bytes, void* stream) {
+  Epi ep{nullptr, wscale, 1, bias, bias_dtype, out, out_dtype, acc_out, (int)m, (int)n};
+  return run_linear<kFmtI8>("kq_w8a8_i8_linear", x, x_dtype, ldx, 0, nullptr,
+                            (const uint8_t*)w, m, n, k, ep, workspace, workspace_bytes,
+                            (hipStream_t)stream);
+}
+
+extern "C" int kq_w8a8_fp8_linear(const void* x, int x_dtype, int64_t ldx, const float* scale_in,
+                                  int scale_mode, const uint8_t* w, const float* wscale,
+                                  int wscale_per_channel, const void* bias, int bias_dtype,
+                                  void* out, int out_dtype, int64_t m, int64_t n, int64_t k,
+                                  void* workspace, size_t workspace_bytes, void* stream) {
+  if (scale_mode < 0 || scale_mode > 2 || (scale_mode != 0 && scale_in == nullptr)) {
+    set_error("kq_w8a8_fp8_linear: bad scale_mode %d", scale_mode);
+    return KQ_EINVAL;
+  }
+  Epi ep{nullptr, wscale, wscale_per_channel, bias, bias_dtype, out, out_dtype, nullptr, (int)m,
+         (int)n};
+  return run_linear<kFmtFp8>("kq_w8a8_fp8_linear", x, x_dtype, ldx, scale_mode, scale_in, w, m, n,
+                             k, ep, workspace, workspace_bytes, (hipStream_t)stream);
 }

@@ -132,11 +132,11 @@ def _workspace(device: torch.device, nbytes: int = 0) -> torch.Tensor:
     return _native.workspace(device, nbytes)
 
 
-def _w8a8_workspace(device: torch.device, m: int, n: int, k: int) -> torch.Tensor:
-    """Workspace with room for every split-K form of a W8A8 call of this shape
-    (decode split-K partials, prefill tile-engine partials)."""
+def _w8a8_linear_workspace(device: torch.device, m: int, n: int, k: int) -> torch.Tensor:
+    """Workspace for a fused W8A8 call of this shape: the quantized rows and
+    their scales (when they are staged) and every split-K form's partials."""
 
-    return _workspace(device, int(_native.library().kq_w8a8_workspace_size(m, n, k)))
+    return _workspace(device, int(_native.library().kq_w8a8_linear_workspace_size(m, n, k)))
 
 
 def _w4_workspace(device: torch.device, m: int, n: int, k: int, mode: int) -> torch.Tensor:
@@ -208,20 +208,28 @@ def fp8_linear_forward(
     *,
     add_bias: bool = True,
 ) -> torch.Tensor:
+    """FP8 W8A8: per-token (dynamic, static ``input_scale`` or given per-row
+    ``activation_scale``) e4m3 quantization of ``x`` and the GEMM in one C call
+    (small decode batches quantize inside the GEMM launch)."""
+
     flat, out = _prepare(x, module, "fp8")
     input_scale = None if module.activation_dynamic else module.input_scale
-    x_q, x_scale = _quantize_activation(
-        flat, torch.float8_e4m3fn, 448.0, static_scale=input_scale, row_scale=activation_scale
-    )
+    if input_scale is not None and activation_scale is not None:
+        raise ValueError("activation quantization accepts one scale source")
+    m, k = flat.shape
+    mode, source = 0, None
+    if activation_scale is not None:
+        mode, source = 2, _f32(activation_scale.reshape(m, 1).to(flat.device))
+    elif input_scale is not None:
+        mode, source = 1, _f32(input_scale.to(flat.device))
     weight_scale = _f32(module.weight_scale)
     bias = _bias(module, add_bias)
-    m, k = flat.shape
-    ws = _w8a8_workspace(x.device, m, module.out_features, k)
+    ws = _w8a8_linear_workspace(x.device, m, module.out_features, k)
     _native.call(
-        "kq_w8a8_fp8_gemm",
-        x_q.data_ptr(), x_scale.data_ptr(), module.weight.data_ptr(), weight_scale.data_ptr(),
-        int(weight_scale.numel() != 1), _native.ptr(bias),
-        _native.dtype_code(None if bias is None else bias.dtype), out.data_ptr(),
+        "kq_w8a8_fp8_linear",
+        flat.data_ptr(), _native.dtype_code(flat.dtype), flat.stride(0), _native.ptr(source), mode,
+        module.weight.data_ptr(), weight_scale.data_ptr(), int(weight_scale.numel() != 1),
+        _native.ptr(bias), _native.dtype_code(None if bias is None else bias.dtype), out.data_ptr(),
         _native.dtype_code(x.dtype), m, module.out_features, k, ws.data_ptr(), ws.numel(),
         _native.stream_handle(x.device),
     )
@@ -230,15 +238,14 @@ def fp8_linear_forward(
 
 def int8_linear_forward(x: torch.Tensor, module, *, add_bias: bool = True,
                         accumulators: torch.Tensor | None = None) -> torch.Tensor:
-    """INT8 W8A8.  ``accumulators`` (int32 ``[M, N]``, optional) receives the raw
-    int32 dot products for bit-exact checks."""
+    """INT8 W8A8: per-token int8 quantization of ``x`` and the GEMM in one C
+    call.  ``accumulators`` (int32 ``[M, N]``, optional) receives the raw int32
+    dot products for bit-exact checks."""
 
     flat, out = _prepare(x, module, "int8")
-    x_q, x_scale = _quantize_activation(flat, torch.int8, 127.0)
     weight_scale = _f32(module.weight_scale)
     bias = _bias(module, add_bias)
     m, k = flat.shape
-    ws = _w8a8_workspace(x.device, m, module.out_features, k)
     if accumulators is not None and (
         accumulators.dtype != torch.int32
         or tuple(accumulators.shape) != (m, module.out_features)
@@ -246,12 +253,14 @@ def int8_linear_forward(x: torch.Tensor, module, *, add_bias: bool = True,
         or accumulators.device != x.device
     ):
         raise ValueError("accumulators must be a contiguous int32 [M, N] tensor on the device")
+    ws = _w8a8_linear_workspace(x.device, m, module.out_features, k)
     _native.call(
-        "kq_w8a8_i8_gemm",
-        x_q.data_ptr(), x_scale.data_ptr(), module.weight.data_ptr(), weight_scale.data_ptr(),
-        _native.ptr(bias), _native.dtype_code(None if bias is None else bias.dtype),
-        out.data_ptr(), _native.dtype_code(x.dtype), _native.ptr(accumulators), m,
-        module.out_features, k, ws.data_ptr(), ws.numel(), _native.stream_handle(x.device),
+        "kq_w8a8_i8_linear",
+        flat.data_ptr(), _native.dtype_code(flat.dtype), flat.stride(0), module.weight.data_ptr(),
+        weight_scale.data_ptr(), _native.ptr(bias),
+        _native.dtype_code(None if bias is None else bias.dtype), out.data_ptr(),
+        _native.dtype_code(x.dtype), _native.ptr(accumulators), m, module.out_features, k,
+        ws.data_ptr(), ws.numel(), _native.stream_handle(x.device),
     )
     return out.reshape(*x.shape[:-1], module.out_features)
 

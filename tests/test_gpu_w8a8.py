@@ -125,6 +125,75 @@ def test_fp8_decode_path_matches_oracle(cuda, k, m, per_channel):
     assert_close_fp(np32(out), pre, label=f"k={k} m={m}")
 
 
+def _two_step(kind, x, module, scale_mode=0, scale_in=None):
+    """Reference for the fused entries: the quantizer, then the GEMM entry."""
+    cuda = x.device
+    m, k = x.shape
+    n = module.out_features
+    stream = hip._native.stream_handle(cuda)
+    xs = torch.empty(m, 1, device=cuda, dtype=torch.float32)
+    out = torch.empty(m, n, device=cuda, dtype=x.dtype)
+    ws = hip._workspace(cuda, int(hip._native.library().kq_w8a8_workspace_size(m, n, k)))
+    wsc = module.weight_scale.float().contiguous()
+    if kind == "int8":
+        xq = torch.empty(m, k, device=cuda, dtype=torch.int8)
+        acc = torch.empty(m, n, device=cuda, dtype=torch.int32)
+        hip._native.call("kq_act_quant_i8", x.data_ptr(), hip._native.dtype_code(x.dtype), m, k, k,
+                         xq.data_ptr(), xs.data_ptr(), stream)
+        hip._native.call("kq_w8a8_i8_gemm", xq.data_ptr(), xs.data_ptr(), module.weight.data_ptr(),
+                         wsc.data_ptr(), module.bias.data_ptr(), hip._native.dtype_code(module.bias.dtype),
+                         out.data_ptr(), hip._native.dtype_code(x.dtype), acc.data_ptr(), m, n, k,
+                         ws.data_ptr(), ws.numel(), stream)
+        return out, acc
+    xq = torch.empty(m, k, device=cuda, dtype=torch.uint8)
+    hip._native.call("kq_act_quant_fp8", x.data_ptr(), hip._native.dtype_code(x.dtype), m, k, k,
+                     hip._native.ptr(scale_in), scale_mode, xq.data_ptr(), xs.data_ptr(), stream)
+    hip._native.call("kq_w8a8_fp8_gemm", xq.data_ptr(), xs.data_ptr(), module.weight.data_ptr(),
+                     wsc.data_ptr(), int(wsc.numel() != 1), module.bias.data_ptr(),
+                     hip._native.dtype_code(module.bias.dtype), out.data_ptr(),
+                     hip._native.dtype_code(x.dtype), m, n, k, ws.data_ptr(), ws.numel(), stream)
+    return out, None
+
+
+# The fused entries: one activation row (with the decode kernel's shape
+# conditions) quantizes inside the GEMM launch, more rows go through the
+# quantizer and the GEMM; the bytes, the K split and the MFMA order are those
+# of the quantizer + decode kernel pair either way, so outputs (bit patterns,
+# NaN included) and INT8 accumulators must be identical.
+@pytest.mark.parametrize("k", [1536, 4096, 8320])
+@pytest.mark.parametrize("m", [1, 2, 4])
+def test_int8_fused_quant_decode_matches_two_step(cuda, k, m):
+    banner(f"int8 fused decode k={k} m={m}")
+    module = _int8_module(k, DECODE_N, seed=k + 7 * m).to(cuda)
+    rows = _edge_rows(k, nonfinite=True)
+    x = rows[[2, 3, 4, 7][:m]].to(cuda) if m <= 4 else None
+    acc = torch.empty(m, DECODE_N, dtype=torch.int32, device=cuda)
+    out = hip.int8_linear_forward(x, module, accumulators=acc)
+    ref, ref_acc = _two_step("int8", x, module)
+    assert torch.equal(acc, ref_acc)
+    assert torch.equal(out.view(torch.int16), ref.view(torch.int16))
+
+
+@pytest.mark.parametrize("k", [1536, 8320])
+@pytest.mark.parametrize("m", [1, 3, 4])
+@pytest.mark.parametrize("mode", ["dynamic", "static", "row"])
+def test_fp8_fused_quant_decode_matches_two_step(cuda, k, m, mode):
+    banner(f"fp8 fused decode k={k} m={m} {mode}")
+    module = _fp8_module(k, DECODE_N, seed=k + 5 * m, dynamic=(mode != "static")).to(cuda)
+    rows = _edge_rows(k, nonfinite=True)
+    x = rows[[0, 2, 6, 1][:m]].to(cuda)
+    scale_mode, scale_in, row_scale = 0, None, None
+    if mode == "static":
+        module.input_scale.fill_(0.037)
+        scale_mode, scale_in = 1, module.input_scale.float().reshape(1).contiguous()
+    elif mode == "row":
+        row_scale = torch.tensor([0.5, 3.0e-3, 7.0, 1.0e-20][:m], device=cuda).reshape(m, 1)
+        scale_mode, scale_in = 2, row_scale
+    out = hip.fp8_linear_forward(x, module, activation_scale=row_scale)
+    ref, _ = _two_step("fp8", x, module, scale_mode, scale_in)
+    assert torch.equal(out.view(torch.int16), ref.view(torch.int16))
+
+
 # Prefill with fewer 256x256 tiles than CUs: the tile engine splits each
 # tile's K range over 2..4 work units and a reduce pass sums the raw partials
 # in split order (shapes for 4 / 3 / 2 splits on 256 CUs; the second one is
