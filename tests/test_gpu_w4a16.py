@@ -296,6 +296,8 @@ _GEMV_CASES = [
     ("gptq", 16, 16384, 2048, 128, torch.float16, False, True),   # several K chunks
     ("gptq", 16, 512, 28672, 128, torch.float16, True, True),     # 7 blocks per CU, act-order
     ("gptq", 4, 4096, 4096, 128, torch.bfloat16, True, False),    # act-order, bf16
+    ("gptq", 1, 4096, 4096, 128, torch.float16, True, True),      # act-order row gathered in the GEMV
+    ("gptq", 1, 2048, 28672, 64, torch.bfloat16, True, False),    # ... bf16, two steps per group
     ("awq", 1, 4096, 4096, 128, torch.float16, False, True),
     ("awq", 16, 4096, 2048, 64, torch.bfloat16, False, True),
     ("awq", 9, 2080, 2056, 32, torch.float16, False, False),

@@ -113,6 +113,32 @@ def test_int8_decode_path_bit_exact(cuda, k, m):
     assert np.array_equal(np32(out), expected)
 
 
+# Decode kernel at N = 8200 (513 column tiles, the last half used).
+@pytest.mark.parametrize("k,m", [(1536, 16), (1536, 3), (4096, 9), (4096, 16)])
+def test_int8_decode_wide_n_bit_exact(cuda, k, m):
+    banner(f"int8 decode n=8200 k={k} m={m}")
+    n = 8200
+    module = _int8_module(k, n, seed=k + 3 * m).to(cuda)
+    x = torch.randn(m, k, generator=torch.Generator().manual_seed(k + m)).to(torch.bfloat16)
+    acc = torch.empty(m, n, dtype=torch.int32, device=cuda)
+    out = hip.int8_linear_forward(x.to(cuda), module, accumulators=acc)
+    expected, xq, xs, eacc = olinear.int8_forward(
+        np32(x), module.weight.cpu().numpy(), module.weight_scale.cpu().numpy(), np32(module.bias))
+    assert np.array_equal(acc.cpu().numpy().astype(np.int64), eacc)
+    assert np.array_equal(np32(out), expected)
+
+
+@pytest.mark.parametrize("k,m", [(1536, 16), (4096, 5)])
+def test_fp8_decode_wide_n_matches_oracle(cuda, k, m):
+    banner(f"fp8 decode n=8200 k={k} m={m}")
+    module = _fp8_module(k, 8200, seed=k + 3 * m).to(cuda)
+    x = torch.randn(m, k, generator=torch.Generator().manual_seed(k + m)).to(torch.bfloat16)
+    out = module(x.to(cuda))
+    expected, _, _, pre = olinear.fp8_forward(np32(x), bits(module.weight), np32(module.weight_scale),
+                                              np32(module.bias))
+    assert_close_fp(np32(out), pre, label=f"k={k} m={m}")
+
+
 @pytest.mark.parametrize("k,m,per_channel", [(1536, 1, True), (4096, 8, False), (4096, 9, True),
                                              (8320, 16, True), (8320, 3, False)])
 def test_fp8_decode_path_matches_oracle(cuda, k, m, per_channel):
