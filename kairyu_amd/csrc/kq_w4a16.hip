@@ -506,27 +506,46 @@ struct GvBlock {
 
 struct GvCtx {
   i32x4 rw, rs, rz;      // buffer resources: qweight, scales, qzeros
+  i32x4 rnull;           // zero-size resource (dead blocks)
   int32_t wlane;         // lane byte offset inside a step (layout dependent)
   int32_t slane, zlane;  // lane byte offsets of its scale / zero word
   int st0;               // first step of this wave
   int g0;                // group of the first step
 };
 
+// Loads of one block in the order its compute consumes them (the group's
+// scale and zero words, then the weight steps); the scheduling barrier keeps
+// the compiler from regrouping loads across blocks, so waiting for a block
+// never waits for a later block's loads (vector loads complete in order).
+// A block that is not `live` (past the workgroup's share) reads through a
+// zero-size resource instead: every lane is out of range, reads 0 and sends
+// no memory request, and the code stays branch-free.
+KQ_DEV i32x4 select_rsrc(bool live, const i32x4& r, const i32x4& dead) {
+  i32x4 o;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) o[i] = __builtin_amdgcn_readfirstlane(live ? r[i] : dead[i]);
+  return o;
+}
+
 template <int S, int SPG, int LAYOUT>
-KQ_DEV void gv_load(const W4Args& a, const GvCtx& c, int unit, GvBlock<S, SPG>& b) {
+KQ_DEV void gv_load(const W4Args& a, const GvCtx& c, int unit, bool live, GvBlock<S, SPG>& b) {
+  const i32x4 rw = select_rsrc(live, c.rw, c.rnull);
+  const i32x4 rs = select_rsrc(live, c.rs, c.rnull);
+  const i32x4 rz = select_rsrc(live, c.rz, c.rnull);
+#pragma unroll
+  for (int i = 0; i < GvShape<S, SPG>::kGroups; ++i) {
+    const int g = c.g0 + i;
+    b.sv[i] = (uint16_t)kq_rbl_i16(rs, c.slane, (g * a.N + unit * 16) * 2, 0);
+    b.zw[i] = (uint32_t)kq_rbl_i32(rz, c.zlane, (g * (a.N / 8) + unit * 2) * 4, 0);
+  }
 #pragma unroll
   for (int s = 0; s < S; ++s) {
     const int32_t so = LAYOUT == kLayoutTiles
                            ? (unit * (a.K / 8) + (c.st0 + s) * 4) * 64
                            : (c.st0 + s) * 16 * a.N + unit * 64;
-    b.w[s] = (uint32_t)kq_rbl_i32(c.rw, c.wlane, so, kAuxNT);
+    b.w[s] = (uint32_t)kq_rbl_i32(rw, c.wlane, so, kAuxNT);
   }
-#pragma unroll
-  for (int i = 0; i < GvShape<S, SPG>::kGroups; ++i) {
-    const int g = c.g0 + i;
-    b.sv[i] = (uint16_t)kq_rbl_i16(c.rs, c.slane, (g * a.N + unit * 16) * 2, 0);
-    b.zw[i] = (uint32_t)kq_rbl_i32(c.rz, c.zlane, (g * (a.N / 8) + unit * 2) * 4, 0);
-  }
+  __builtin_amdgcn_sched_barrier(0);
 }
 
 template <int S, int SPG>
@@ -553,13 +572,22 @@ KQ_DEV f32x4 gv_compute(const W4Args& a, const NibbleConsts& nc, uint32_t zsh,
   return acc;
 }
 
-// ONE: the launch guarantees ncb <= 2*D blocks per workgroup, so one round
-// with the accumulators of all of them in registers (no outer loop).
-template <int XDT, int S, int SPG, int LAYOUT, bool ONE>
+// MODE kGvOne: the launch guarantees ncb <= 2*D blocks per workgroup, so one
+// round with the accumulators of all of them in registers (no outer loop).
+// kGvShort: ncb <= D, one round of D blocks.  kGvSingle: every workgroup owns
+// exactly one block (D = U = 1).  The modes keep the slots past a share few:
+// their out-of-range loads move no data but still cost address-unit issue
+// slots.  kGvRounds: several rounds of U blocks.
+enum { kGvRounds = 0, kGvOne = 1, kGvSingle = 2, kGvShort = 3 };
+
+template <int XDT, int S, int SPG, int LAYOUT, int MODE>
 __global__ void __launch_bounds__(64 * kGvWaves)
 w4a16_gemv_kernel(W4Args a, GvPlan p) {
-  constexpr int D = GvShape<S, SPG>::kDepth;
-  constexpr int U = ONE ? GvShape<S, SPG>::kOneRound : GvShape<S, SPG>::kRound;
+  constexpr bool ONE = MODE != kGvRounds;
+  constexpr int D = MODE == kGvSingle ? 1 : GvShape<S, SPG>::kDepth;
+  constexpr int U = MODE == kGvSingle ? 1
+                    : MODE == kGvShort ? D
+                    : (MODE == kGvOne ? GvShape<S, SPG>::kOneRound : GvShape<S, SPG>::kRound);
   __shared__ float red[kGvWaves][U * 4][64];
   const int lane = lane_id();
   const int wave = __builtin_amdgcn_readfirstlane(wave_id());
@@ -582,6 +610,7 @@ w4a16_gemv_kernel(W4Args a, GvPlan p) {
   c.rw = make_rsrc(a.qw, (uint32_t)((a.K / 8) * (LAYOUT == kLayoutTiles ? npad : a.N) * 4));
   c.rs = make_rsrc(a.sc, (uint32_t)(ngroups * a.N * 2));
   c.rz = make_rsrc(a.qz, (uint32_t)(ngroups * (a.N / 8) * 4));
+  c.rnull = make_rsrc(a.qw, 0u);
   c.wlane = LAYOUT == kLayoutTiles ? (kb * 16 + j) * 4 : (kb * a.N + j) * 4;
   c.slane = j * 2;
   c.zlane = (j >> 3) * 4;
@@ -589,19 +618,31 @@ w4a16_gemv_kernel(W4Args a, GvPlan p) {
   c.g0 = __builtin_amdgcn_readfirstlane(group_of(a, c.st0 * 32));
   const uint32_t zsh = 4u * (uint32_t)(j & 7);
 
-  // rolling window: block q's weights were requested D blocks earlier
-  GvBlock<S, SPG> buf[D];
-#pragma unroll
-  for (int d = 0; d < D; ++d)
-    if (d < ncb) gv_load<S, SPG, LAYOUT>(a, c, u0 + d, buf[d]);
-
-  // x chunks of this wave's steps, loaded once and kept for every block
-  u32x4 A[S];
+  // x chunks of this wave's steps, loaded once and kept for every block.
+  // They are requested before the weights: loads complete in issue order, so
+  // the first block's compute then waits for x and that block only, not for
+  // every block in flight (which would leave HBM idle between the first
+  // window and the loads the compute issues).
+  u32x4 X[S];
   {
     const uint16_t* xr = a.x + (int64_t)min(j, a.M - 1) * a.ldx + c.st0 * 32 + 8 * kb;
 #pragma unroll
-    for (int s = 0; s < S; ++s) A[s] = gptq_order(x_to_f16<XDT>(*(const u32x4*)(xr + s * 32)));
+    for (int s = 0; s < S; ++s) X[s] = *(const u32x4*)(xr + s * 32);
   }
+
+  // rolling window: block q's weights were requested D blocks earlier.  No
+  // load sits under a branch (blocks past the share read through the
+  // zero-size resource), so the code stays straight-line and the compiler
+  // waits for exactly the block about to be computed.  (Under a branch the
+  // wait count is merged at the join, and each compute then waits for every
+  // load in flight.)
+  GvBlock<S, SPG> buf[D];
+#pragma unroll
+  for (int d = 0; d < D; ++d) gv_load<S, SPG, LAYOUT>(a, c, u0 + d, d < ncb, buf[d]);
+
+  u32x4 A[S];
+#pragma unroll
+  for (int s = 0; s < S; ++s) A[s] = gptq_order(x_to_f16<XDT>(X[s]));
 
   for (int q0 = 0; q0 < (ONE ? 1 : ncb); q0 += U) {
     // U blocks per round (U a multiple of D, so block q0+q sits in buf[q % D])
@@ -609,10 +650,9 @@ w4a16_gemv_kernel(W4Args a, GvPlan p) {
 #pragma unroll
     for (int q = 0; q < U; ++q) {
       acc[q] = f32x4{0.f, 0.f, 0.f, 0.f};
-      if (q0 + q < ncb) {
-        acc[q] = gv_compute<S, SPG>(a, nc, zsh, buf[q % D], A);
-        if (q0 + q + D < ncb) gv_load<S, SPG, LAYOUT>(a, c, u0 + q0 + q + D, buf[q % D]);
-      }
+      if (q0 + q < ncb) acc[q] = gv_compute<S, SPG>(a, nc, zsh, buf[q % D], A);
+      // (ONE: the share has at most U blocks, so slots past U are never loaded)
+      if (!ONE || q + D < U) gv_load<S, SPG, LAYOUT>(a, c, u0 + q0 + q + D, q0 + q + D < ncb, buf[q % D]);
     }
     // fixed-order reduction of the 16 waves' partial sums (the next round's
     // loads stay in flight across the barriers)
@@ -1096,25 +1136,39 @@ static void launch_prefill(const W4Args& a, hipStream_t stream) {
 
 template <int XDT, int S, int SPG>
 static void launch_gv_s(const W4Args& a, const GvPlan& p, int layout, hipStream_t st) {
-  const bool one = (p.units + p.wgs - 1) / p.wgs <= GvShape<S, SPG>::kOneRound;
+  const int per = (p.units + p.wgs - 1) / p.wgs;
+  const int mode = per <= 1                         ? kGvSingle
+                   : per <= GvShape<S, SPG>::kDepth    ? kGvShort
+                   : per <= GvShape<S, SPG>::kOneRound ? kGvOne
+                                                       : kGvRounds;
   const dim3 g(p.wgs), b(64 * kGvWaves);
+#define KQ_GV_LAUNCH(L, M) hipLaunchKernelGGL((w4a16_gemv_kernel<XDT, S, SPG, L, M>), g, b, 0, st, a, p)
   if (layout == kLayoutTiles) {
-    if (one) hipLaunchKernelGGL((w4a16_gemv_kernel<XDT, S, SPG, kLayoutTiles, true>), g, b, 0, st, a, p);
-    else hipLaunchKernelGGL((w4a16_gemv_kernel<XDT, S, SPG, kLayoutTiles, false>), g, b, 0, st, a, p);
+    if (mode == kGvSingle) KQ_GV_LAUNCH(kLayoutTiles, kGvSingle);
+    else if (mode == kGvShort) KQ_GV_LAUNCH(kLayoutTiles, kGvShort);
+    else if (mode == kGvOne) KQ_GV_LAUNCH(kLayoutTiles, kGvOne);
+    else KQ_GV_LAUNCH(kLayoutTiles, kGvRounds);
   } else {
-    if (one) hipLaunchKernelGGL((w4a16_gemv_kernel<XDT, S, SPG, kLayoutRows, true>), g, b, 0, st, a, p);
-    else hipLaunchKernelGGL((w4a16_gemv_kernel<XDT, S, SPG, kLayoutRows, false>), g, b, 0, st, a, p);
+    if (mode == kGvSingle) KQ_GV_LAUNCH(kLayoutRows, kGvSingle);
+    else if (mode == kGvShort) KQ_GV_LAUNCH(kLayoutRows, kGvShort);
+    else if (mode == kGvOne) KQ_GV_LAUNCH(kLayoutRows, kGvOne);
+    else KQ_GV_LAUNCH(kLayoutRows, kGvRounds);
   }
+#undef KQ_GV_LAUNCH
 }
 
+// Steps per group as gv_plan returns them: 8 = one group per window, else a
+// divisor of S below S.
 template <int XDT, int S>
 static void launch_gv_spg(const W4Args& a, const GvPlan& p, int spg, int layout, hipStream_t st) {
-  switch (spg) {
-    case 1: launch_gv_s<XDT, S, 1>(a, p, layout, st); break;
-    case 2: launch_gv_s<XDT, S, 2>(a, p, layout, st); break;
-    case 4: launch_gv_s<XDT, S, 4>(a, p, layout, st); break;
-    default: launch_gv_s<XDT, S, 8>(a, p, layout, st); break;
+  if constexpr (S >= 4) {
+    if (spg == 2) return launch_gv_s<XDT, S, 2>(a, p, layout, st);
   }
+  if constexpr (S >= 8) {
+    if (spg == 4) return launch_gv_s<XDT, S, 4>(a, p, layout, st);
+  }
+  if (spg == 1) return launch_gv_s<XDT, S, 1>(a, p, layout, st);
+  launch_gv_s<XDT, S, 8>(a, p, layout, st);
 }
 
 template <int XDT>
