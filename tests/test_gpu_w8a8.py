@@ -251,6 +251,36 @@ def test_fp8_tile_engine_split_k_matches_oracle(cuda, m, n, k):
     assert_close_fp(np32(out), pre, label=f"m={m} n={n} k={k}")
 
 
+# Whole-K tiles (at least one 256x256 tile per CU: no split-K); the second
+# shape is ragged in M, N (N % 8 != 0: direct stores) and K (a 16-byte last K
+# block).
+WHOLE_TILE_SHAPES = [(4096, 4096, 1024), (4100, 4108, 1040)]
+
+
+@pytest.mark.parametrize("m,n,k", WHOLE_TILE_SHAPES)
+def test_int8_whole_tiles_bit_exact(cuda, m, n, k):
+    banner(f"int8 whole tiles m={m} n={n} k={k}")
+    module = _int8_module(k, n, seed=m + n).to(cuda)
+    x = torch.randn(m, k, generator=torch.Generator().manual_seed(k)).to(torch.bfloat16)
+    acc = torch.empty(m, n, dtype=torch.int32, device=cuda)
+    out = hip.int8_linear_forward(x.to(cuda), module, accumulators=acc)
+    expected, xq, xs, eacc = olinear.int8_forward(
+        np32(x), module.weight.cpu().numpy(), module.weight_scale.cpu().numpy(), np32(module.bias))
+    assert np.array_equal(acc.cpu().numpy().astype(np.int64), eacc)
+    assert np.array_equal(np32(out), expected)
+
+
+@pytest.mark.parametrize("m,n,k", WHOLE_TILE_SHAPES)
+def test_fp8_whole_tiles_match_oracle(cuda, m, n, k):
+    banner(f"fp8 whole tiles m={m} n={n} k={k}")
+    module = _fp8_module(k, n, seed=m + n).to(cuda)
+    x = torch.randn(m, k, generator=torch.Generator().manual_seed(k)).to(torch.bfloat16)
+    out = module(x.to(cuda))
+    expected, _, _, pre = olinear.fp8_forward(np32(x), bits(module.weight), np32(module.weight_scale),
+                                              np32(module.bias))
+    assert_close_fp(np32(out), pre, label=f"m={m} n={n} k={k}")
+
+
 def test_w8a8_workspace_size_covers_split_k(cuda):
     lib = hip._native.library()
     cus = torch.cuda.get_device_properties(cuda).multi_processor_count
