@@ -157,6 +157,7 @@ def device_supported(index: int) -> bool:
 
 
 _workspaces: dict[int, torch.Tensor] = {}
+_retired_workspaces: list[torch.Tensor] = []
 
 
 def workspace(device: torch.device, nbytes: int = DEFAULT_WORKSPACE_BYTES) -> torch.Tensor:
@@ -164,7 +165,8 @@ def workspace(device: torch.device, nbytes: int = DEFAULT_WORKSPACE_BYTES) -> to
 
     Allocated once per device through torch's caching allocator, grown when a
     call needs more, and reused by every call (also inside captured graphs:
-    grow it with an eager call of the largest shape before capture).  Calls
+    grow it with an eager call of the largest shape before capture; a buffer
+    it outgrows stays allocated, so graphs captured on it remain valid).  Calls
     sharing it must be ordered on one stream, like the engine's single-stream
     decode loop.
     """
@@ -172,6 +174,10 @@ def workspace(device: torch.device, nbytes: int = DEFAULT_WORKSPACE_BYTES) -> to
     index = device.index if device.index is not None else torch.cuda.current_device()
     buffer = _workspaces.get(index)
     if buffer is None or buffer.numel() < nbytes:
+        if buffer is not None:
+            # graphs captured earlier still point at the old buffer: keep it
+            # allocated (never returned to torch's allocator for other tensors)
+            _retired_workspaces.append(buffer)
         buffer = torch.empty(max(nbytes, DEFAULT_WORKSPACE_BYTES), dtype=torch.uint8,
                              device=torch.device("cuda", index))
         _workspaces[index] = buffer
