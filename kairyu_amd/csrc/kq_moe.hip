@@ -50,15 +50,34 @@ KQ_DEV uint32_t float_key(float v) {
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
-KQ_DEV uint64_t wave_max_u64(uint64_t v) {
+
+// Wave-wide maximum of a 64-bit key, uniform result.  Within each row of 16
+// lanes: quad exchanges (xor 1, xor 2), then half-row and row mirrors through
+// DPP (register-to-register, no LDS round trip); the four row maxima are then
+// read from lanes 0, 16, 32, 48.
+template <int CTRL>
+KQ_DEV void dpp_max_step(uint32_t& lo, uint32_t& hi) {
+  const uint32_t olo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)lo, CTRL, 0xf, 0xf, false);
+  const uint32_t ohi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)hi, CTRL, 0xf, 0xf, false);
+  const bool gt = ohi > hi || (ohi == hi && olo > lo);
+  lo = gt ? olo : lo;
+  hi = gt ? ohi : hi;
+}
+
+KQ_DEV uint64_t wave_max_u64_dpp(uint64_t v) {
+  uint32_t lo = (uint32_t)v, hi = (uint32_t)(v >> 32);
+  dpp_max_step<0xB1>(lo, hi);    // quad_perm [1,0,3,2]
+  dpp_max_step<0x4E>(lo, hi);    // quad_perm [2,3,0,1]
+  dpp_max_step<0x141>(lo, hi);   // row_half_mirror
+  dpp_max_step<0x140>(lo, hi);   // row_mirror
+  uint64_t best = 0;
 #pragma unroll
-  for (int off = 32; off > 0; off >>= 1) {
-    const uint32_t lo = __shfl_xor((uint32_t)v, off, 64);
-    const uint32_t hi = __shfl_xor((uint32_t)(v >> 32), off, 64);
-    const uint64_t o = ((uint64_t)hi << 32) | lo;
-    v = o > v ? o : v;
+  for (int r = 0; r < 4; ++r) {
+    const uint64_t k = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)hi, 16 * r) << 32) |
+                       (uint32_t)__builtin_amdgcn_readlane((int)lo, 16 * r);
+    best = k > best ? k : best;
   }
-  return v;
+  return best;
 }
 
 KQ_DEV float wave_sum(float v) {
@@ -73,16 +92,17 @@ KQ_DEV float key_float(uint32_t k) {
 
 // One wave per token: k rounds of a wave-wide max over (value key, -expert);
 // every lane sees each round's winner, lane r keeps slot r's logit.
+template <int PL>   // logits per lane: E <= 64 * PL
 __global__ void __launch_bounds__(256)
 moe_route_kernel(const void* __restrict__ logits, int dtype, int T, int E, int k, int norm,
                  int32_t* __restrict__ idx, float* __restrict__ w) {
   const int lane = lane_id();
   const int t = blockIdx.x * 4 + wave_id();
   if (t >= T) return;
-  float v[kRouteMaxPerLane];
-  bool live[kRouteMaxPerLane];
+  float v[PL];
+  bool live[PL];
 #pragma unroll
-  for (int i = 0; i < kRouteMaxPerLane; ++i) {
+  for (int i = 0; i < PL; ++i) {
     const int e = lane + 64 * i;
     live[i] = e < E;
     v[i] = live[i] ? load_as_f32(logits, dtype, (int64_t)t * E + e) : 0.0f;
@@ -91,17 +111,16 @@ moe_route_kernel(const void* __restrict__ logits, int dtype, int T, int E, int k
   for (int r = 0; r < k; ++r) {
     uint64_t best = 0;
 #pragma unroll
-    for (int i = 0; i < kRouteMaxPerLane; ++i) {
-      if (!live[i]) continue;
+    for (int i = 0; i < PL; ++i) {
       const uint64_t key = ((uint64_t)float_key(v[i]) << 32) |
                            (uint32_t)(0xffffffffu - (uint32_t)(lane + 64 * i));
-      best = key > best ? key : best;
+      best = live[i] && key > best ? key : best;
     }
-    best = wave_max_u64(best);
+    best = wave_max_u64_dpp(best);
     const int e = (int)(0xffffffffu - (uint32_t)best);
     const float val = key_float((uint32_t)(best >> 32));
 #pragma unroll
-    for (int i = 0; i < kRouteMaxPerLane; ++i)
+    for (int i = 0; i < PL; ++i)
       if (lane + 64 * i == e) live[i] = false;
     if (lane == 0) idx[(int64_t)t * k + r] = e;
     if (lane == r) my_sel = val;
@@ -113,12 +132,12 @@ moe_route_kernel(const void* __restrict__ logits, int dtype, int T, int E, int k
   if (!norm) {
     float m = -__builtin_inff();
 #pragma unroll
-    for (int i = 0; i < kRouteMaxPerLane; ++i)
+    for (int i = 0; i < PL; ++i)
       if (lane + 64 * i < E) m = fmaxf(m, v[i]);
     mx = wave_max(m);
     float sum = 0.0f;
 #pragma unroll
-    for (int i = 0; i < kRouteMaxPerLane; ++i)
+    for (int i = 0; i < PL; ++i)
       if (lane + 64 * i < E) sum += expf(v[i] - mx);
     denom = wave_sum(sum);
   }
@@ -144,21 +163,35 @@ moe_count_kernel(const int32_t* __restrict__ idx, int R, int E, int32_t* __restr
   for (int i = threadIdx.x; i < E; i += kSortChunk) counts[(int64_t)blockIdx.x * E + i] = hist[i];
 }
 
-// Exclusive prefix sum of v[0..n) in LDS (n <= 1024, 1024 threads); returns the total.
+// Exclusive prefix sum of v[0..n) in LDS (n <= 1024); returns the total.
+// Wave 0 scans (each lane a run of consecutive entries, lane totals through a
+// shuffle scan) while the other waves wait at the barrier: two barriers
+// instead of a workgroup-wide Hillis-Steele scan's twenty.  tmp[0] carries
+// the total.
 KQ_DEV int block_exclusive_scan(int* v, int* tmp, int n) {
-  const int t = threadIdx.x;
-  int x = t < n ? v[t] : 0;
-  tmp[t] = x;
-  __syncthreads();
-  for (int off = 1; off < 1024; off <<= 1) {
-    const int y = t >= off ? tmp[t - off] : 0;
-    __syncthreads();
-    tmp[t] += y;
-    __syncthreads();
+  if (wave_id() == 0) {
+    const int lane = lane_id();
+    const int per = (n + 63) / 64;
+    const int b = min(n, lane * per), e = min(n, b + per);
+    int sum = 0;
+    for (int i = b; i < e; ++i) sum += v[i];
+    int inc = sum;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const int y = __shfl_up(inc, off, 64);
+      if (lane >= off) inc += y;
+    }
+    int run = inc - sum;
+    for (int i = b; i < e; ++i) {
+      const int x = v[i];
+      v[i] = run;
+      run += x;
+    }
+    if (lane == 63) tmp[0] = inc;
   }
-  const int total = tmp[1023];
-  if (t < n) v[t] = tmp[t] - x;
   __syncthreads();
+  const int total = tmp[0];
+  __syncthreads();  // tmp and v are reused by the caller
   return total;
 }
 
@@ -404,9 +437,18 @@ extern "C" int kq_moe_route_topk(const void* logits, int dtype, int64_t tokens, 
     return KQ_EINVAL;
   }
   if (tokens == 0) return KQ_OK;
-  hipLaunchKernelGGL(moe_route_kernel, dim3((unsigned)((tokens + 3) / 4)), dim3(256), 0,
-                     (hipStream_t)stream, logits, dtype, (int)tokens, (int)experts, top_k,
-                     norm_topk_prob ? 1 : 0, topk_idx, topk_w);
+  const dim3 grid((unsigned)((tokens + 3) / 4)), block(256);
+  hipStream_t st = (hipStream_t)stream;
+  const int T = (int)tokens, E = (int)experts, norm = norm_topk_prob ? 1 : 0;
+  if (E <= 64)
+    hipLaunchKernelGGL(moe_route_kernel<1>, grid, block, 0, st, logits, dtype, T, E, top_k, norm, topk_idx, topk_w);
+  else if (E <= 128)
+    hipLaunchKernelGGL(moe_route_kernel<2>, grid, block, 0, st, logits, dtype, T, E, top_k, norm, topk_idx, topk_w);
+  else if (E <= 256)
+    hipLaunchKernelGGL(moe_route_kernel<4>, grid, block, 0, st, logits, dtype, T, E, top_k, norm, topk_idx, topk_w);
+  else
+    hipLaunchKernelGGL(moe_route_kernel<kRouteMaxPerLane>, grid, block, 0, st, logits, dtype, T, E, top_k, norm,
+                       topk_idx, topk_w);
   return check_launch("kq_moe_route_topk");
 }
 
