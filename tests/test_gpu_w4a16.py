@@ -301,6 +301,13 @@ _GEMV_CASES = [
     ("awq", 1, 4096, 4096, 128, torch.float16, False, True),
     ("awq", 16, 4096, 2048, 64, torch.bfloat16, False, True),
     ("awq", 9, 2080, 2056, 32, torch.float16, False, False),
+    # GEMV share modes on 256 CUs: 513 column blocks (3 per workgroup, the
+    # one-window form with dead slots), 1280 (5: one round with dead slots),
+    # 2560 (10: several rounds) and 2305 (ragged rounds)
+    ("gptq", 4, 1024, 8208, 128, torch.float16, False, True),
+    ("gptq", 3, 1024, 20480, 64, torch.bfloat16, True, False),
+    ("gptq", 2, 1024, 40960, 128, torch.float16, False, True),
+    ("awq", 16, 2048, 36880, 128, torch.float16, False, False),
 ]
 
 
