@@ -229,9 +229,14 @@ tile_gemm_kernel(TileGemmArgs a) {
       const int r = tl.row0 + (((wave * 4 + i) * 64 + lane) >> 3);
       pf_src[i] = r < tl.row_end ? (a.gather ? a.gather[r] : r) : -1;
     }
-    if (BLOCK && wave < 4) {  // LDS scale float p holds tile row (p % 16) * 16 + p / 16
+    if (BLOCK && wave < 4) {
+      // LDS scale float p = 16 * lr + 4 * c + i (lr = p / 16) holds tile row
+      // 64 * wm + 16 * i + lr of slab wm = c ^ ((lr >> 1) & 3): a lane's four
+      // row scales are one 16-byte chunk, and the chunk XOR spreads the 16
+      // lanes of a read over eight bank groups (2-way instead of 8-way)
       const int p = wave * 64 + lane;
-      const int r = tl.row0 + (p & 15) * 16 + (p >> 4);
+      const int lr_ = p >> 4, c_ = (p >> 2) & 3, i_ = p & 3;
+      const int r = tl.row0 + 64 * (c_ ^ ((lr_ >> 1) & 3)) + 16 * i_ + lr_;
       pf_xsrc = r < tl.row_end ? (a.gather ? a.gather[r] : r) : -1;
     }
     if (BLOCK && (int)threadIdx.x < 2 * KB) {
@@ -355,7 +360,8 @@ tile_gemm_kernel(TileGemmArgs a) {
       const uint8_t* sX = smem + kTgLdsX + st * (kTgBM * kTgBK) + (64 * wm) * kTgBK;
       float prod[2][4];
       if constexpr (BLOCK) {
-        const f32x4 sx = *(const f32x4*)(smem + kTgLdsXs + st * (kTgBM * 4) + (lr * 16 + 4 * wm) * 4);
+        const f32x4 sx =
+            *(const f32x4*)(smem + kTgLdsXs + st * (kTgBM * 4) + (lr * 16 + 4 * (wm ^ ((lr >> 1) & 3))) * 4);
         if constexpr (EPI == kTgEpiSwiGluQuant) {
           const float s0 = sWs[kb], s1 = sWs[KB + kb];
 #pragma unroll
