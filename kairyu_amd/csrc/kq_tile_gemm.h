@@ -44,6 +44,8 @@
 
 #include "kq_common.h"
 
+#include <type_traits>
+
 namespace kq {
 
 constexpr int kTgBM = 256;        // activation rows per tile
@@ -426,153 +428,160 @@ tile_gemm_kernel(TileGemmArgs a) {
     }
 
     // ------------------------------------------------------------ epilogue
-    // lane holds rows m = 64*wm + 16*mb + lr, columns 128*wn + 16*j + 4*lg + q
-    const int row0 = cur.row0, row_end = cur.row_end, ntile = cur.ntile;
-    if constexpr (EPI == kTgEpiSwiGluQuant) {
-      // SwiGLU rounded to the activation dtype at each step (as torch does for
-      // bf16 / fp16 tensors), then 1x128 e4m3 quantization of the tile's 128
-      // activation columns: s = max(amax, 1e-12) / 448, q = e4m3(clamp(v / s)).
-      float amax[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-#pragma unroll
-        for (int mb = 0; mb < 4; ++mb)
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            const float g = tg_round_act(acc[j][mb][q], a.out_dtype);
-            const float u = tg_round_act(acc[j + 4][mb][q], a.out_dtype);
-            const float sl = tg_round_act(g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)), a.out_dtype);
-            const float v = tg_round_act(sl * u, a.out_dtype);
-            acc[j][mb][q] = v;
-            amax[mb] = fmaxf(amax[mb], fabsf(v));
-          }
-#pragma unroll
-      for (int mb = 0; mb < 4; ++mb) {
-        amax[mb] = fmaxf(amax[mb], __shfl_xor(amax[mb], 16, 64));
-        amax[mb] = fmaxf(amax[mb], __shfl_xor(amax[mb], 32, 64));
-        if (lg == 0) sRed[wn * kTgBM + 64 * wm + 16 * mb + lr] = amax[mb];
-      }
-      __syncthreads();
-      const int IB = a.I / 128;
-      // the tile's 256 x 128 e4m3 block goes through the idle pipeline stage
-      // (row r at r*128, 16-byte chunk c at c ^ (r & 7)) so that the global
-      // stores below write whole 128-byte rows
-      uint8_t* stg = smem + kTgLdsX + (st ^ 1) * (kTgBM * kTgBK);
-#pragma unroll
-      for (int mb = 0; mb < 4; ++mb) {
-        const int lrow = 64 * wm + 16 * mb + lr;
-        const float am = fmaxf(sRed[lrow], sRed[kTgBM + lrow]);
-        const float s = __fdiv_rn(fmaxf(am, 1e-12f), 448.0f);
-        const float rs = __fdiv_rn(1.0f, s);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          float v[4];
-#pragma unroll
-          for (int q = 0; q < 4; ++q) v[q] = fminf(fmaxf(div_by_recip(acc[j][mb][q], s, rs), -448.0f), 448.0f);
-          const int col = 64 * wn + 16 * j + 4 * lg;
-          *(uint32_t*)(stg + lrow * 128 + (((col >> 4) ^ (lrow & 7)) << 4) + (col & 15)) =
-              pack4_e4m3(v[0], v[1], v[2], v[3]);
-        }
-        if (wn == 0 && lg == 0 && row0 + lrow < row_end) a.acts[(int64_t)(row0 + lrow) * IB + ntile] = s;
-      }
-      __syncthreads();
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int r = 64 * i + ((int)threadIdx.x >> 3), c = (int)threadIdx.x & 7;
-        if (row0 + r < row_end)
-          *(i32x4*)(a.actq + (int64_t)(row0 + r) * a.I + ntile * 128 + c * 16) =
-              *(const i32x4*)(stg + r * 128 + ((c ^ (r & 7)) << 4));
-      }
-    } else if (ksplit > 1) {
-      // raw 32-bit accumulators of this work unit's K range; a reduce pass
-      // sums the splits in order and applies the scales
-      uint32_t* pb = a.partials + (int64_t)cur.split * a.M * a.N;
-      const bool vec = (a.N & 3) == 0;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int n = ntile * kTgBN + 128 * wn + 16 * j + 4 * lg;
-#pragma unroll
-        for (int mb = 0; mb < 4; ++mb) {
-          const int grow = row0 + 64 * wm + 16 * mb + lr;
-          if (grow >= row_end) continue;
-          uint32_t v[4];
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            if constexpr (FMT == kTgI8) v[q] = (uint32_t)(int)acc[j][mb][q];
-            else v[q] = __float_as_uint((float)acc[j][mb][q]);
-          }
-          uint32_t* dst = pb + (int64_t)grow * a.N + n;
-          if (vec && n + 3 < a.N) {
-            *(u32x4*)dst = u32x4{v[0], v[1], v[2], v[3]};
-          } else {
-#pragma unroll
-            for (int q = 0; q < 4; ++q)
-              if (n + q < a.N) dst[q] = v[q];
-          }
-        }
-      }
-    } else {
-      const float* eX = (const float*)(smem + kTgLdsEpi) + buf * 3 * 256;
-      // each wave's 128 x 64 output block goes through its 8 KB of the idle
-      // pipeline stage in two column halves ([m][64 columns], 16-byte chunk c of
-      // row m at c ^ (m & 7)), so every global store writes whole 128-byte
-      // row segments; rows of 8-aligned N only (others store directly)
-      uint8_t* stg = smem + (wave < 4 ? kTgLdsW : kTgLdsX) + (st ^ 1) * (kTgBN * kTgBK) + (wave & 3) * 8192;
-      const bool staged = (a.N & 7) == 0;
-#pragma unroll
-      for (int half = 0; half < 2; ++half) {
-#pragma unroll
-        for (int jj = 0; jj < 4; ++jj) {
-          const int j = 4 * half + jj;
-          const int nl = 128 * wn + 16 * j + 4 * lg;  // tile column of q = 0
-          const int n = ntile * kTgBN + nl;
-          const f32x4 wsc = *(const f32x4*)(eX + 256 + nl);
-          const f32x4 bv = *(const f32x4*)(eX + 512 + nl);
-#pragma unroll
-          for (int mb = 0; mb < 4; ++mb) {
-            const int ml = 16 * mb + lr;  // row within the wave's block
-            const int grow = row0 + 64 * wm + ml;
-            const float xsc = BLOCK ? 1.0f : eX[64 * wm + ml];
-            uint16_t o[4];
-#pragma unroll
+    // One copy per output dtype (a uniform branch picks it), so every
+    // rounding and conversion below is a single fixed instruction sequence.
+    auto epilogue = [&](auto odt) {
+      constexpr int ODT = decltype(odt)::value;
+      // lane holds rows m = 64*wm + 16*mb + lr, columns 128*wn + 16*j + 4*lg + q
+      const int row0 = cur.row0, row_end = cur.row_end, ntile = cur.ntile;
+      if constexpr (EPI == kTgEpiSwiGluQuant) {
+        // SwiGLU rounded to the activation dtype at each step (as torch does for
+        // bf16 / fp16 tensors), then 1x128 e4m3 quantization of the tile's 128
+        // activation columns: s = max(amax, 1e-12) / 448, q = e4m3(clamp(v / s)).
+        float amax[4] = {0.f, 0.f, 0.f, 0.f};
+  #pragma unroll
+        for (int j = 0; j < 4; ++j)
+  #pragma unroll
+          for (int mb = 0; mb < 4; ++mb)
+  #pragma unroll
             for (int q = 0; q < 4; ++q) {
-              float v = (float)acc[j][mb][q];
-              if (!BLOCK) v = __fmul_rn(__fmul_rn(v, xsc), wsc[q]);
-              if (a.bias_dtype != KQ_DTYPE_NONE) v = __fadd_rn(v, bv[q]);
-              o[q] = tg_to_out(v, a.out_dtype);
+              const float g = tg_round_act(acc[j][mb][q], ODT);
+              const float u = tg_round_act(acc[j + 4][mb][q], ODT);
+              const float sl = tg_round_act(g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)), ODT);
+              const float v = tg_round_act(sl * u, ODT);
+              acc[j][mb][q] = v;
+              amax[mb] = fmaxf(amax[mb], fabsf(v));
             }
-            const u32x2 word = u32x2{(uint32_t)o[0] | ((uint32_t)o[1] << 16), (uint32_t)o[2] | ((uint32_t)o[3] << 16)};
-            if (staged) {
-              const int cb = 32 * jj + 8 * lg;  // byte column within the 128-byte row
-              *(u32x2*)(stg + ml * 128 + (((cb >> 4) ^ (ml & 7)) << 4) + (cb & 15)) = word;
-            } else if (grow < row_end) {
-              uint16_t* dst = (uint16_t*)a.out + (int64_t)grow * a.N + n;
-#pragma unroll
+  #pragma unroll
+        for (int mb = 0; mb < 4; ++mb) {
+          amax[mb] = fmaxf(amax[mb], __shfl_xor(amax[mb], 16, 64));
+          amax[mb] = fmaxf(amax[mb], __shfl_xor(amax[mb], 32, 64));
+          if (lg == 0) sRed[wn * kTgBM + 64 * wm + 16 * mb + lr] = amax[mb];
+        }
+        __syncthreads();
+        const int IB = a.I / 128;
+        // the tile's 256 x 128 e4m3 block goes through the idle pipeline stage
+        // (row r at r*128, 16-byte chunk c at c ^ (r & 7)) so that the global
+        // stores below write whole 128-byte rows
+        uint8_t* stg = smem + kTgLdsX + (st ^ 1) * (kTgBM * kTgBK);
+  #pragma unroll
+        for (int mb = 0; mb < 4; ++mb) {
+          const int lrow = 64 * wm + 16 * mb + lr;
+          const float am = fmaxf(sRed[lrow], sRed[kTgBM + lrow]);
+          const float s = __fdiv_rn(fmaxf(am, 1e-12f), 448.0f);
+          const float rs = __fdiv_rn(1.0f, s);
+  #pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            float v[4];
+  #pragma unroll
+            for (int q = 0; q < 4; ++q) v[q] = fminf(fmaxf(div_by_recip(acc[j][mb][q], s, rs), -448.0f), 448.0f);
+            const int col = 64 * wn + 16 * j + 4 * lg;
+            *(uint32_t*)(stg + lrow * 128 + (((col >> 4) ^ (lrow & 7)) << 4) + (col & 15)) =
+                pack4_e4m3(v[0], v[1], v[2], v[3]);
+          }
+          if (wn == 0 && lg == 0 && row0 + lrow < row_end) a.acts[(int64_t)(row0 + lrow) * IB + ntile] = s;
+        }
+        __syncthreads();
+  #pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int r = 64 * i + ((int)threadIdx.x >> 3), c = (int)threadIdx.x & 7;
+          if (row0 + r < row_end)
+            *(i32x4*)(a.actq + (int64_t)(row0 + r) * a.I + ntile * 128 + c * 16) =
+                *(const i32x4*)(stg + r * 128 + ((c ^ (r & 7)) << 4));
+        }
+      } else if (ksplit > 1) {
+        // raw 32-bit accumulators of this work unit's K range; a reduce pass
+        // sums the splits in order and applies the scales
+        uint32_t* pb = a.partials + (int64_t)cur.split * a.M * a.N;
+        const bool vec = (a.N & 3) == 0;
+  #pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const int n = ntile * kTgBN + 128 * wn + 16 * j + 4 * lg;
+  #pragma unroll
+          for (int mb = 0; mb < 4; ++mb) {
+            const int grow = row0 + 64 * wm + 16 * mb + lr;
+            if (grow >= row_end) continue;
+            uint32_t v[4];
+  #pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              if constexpr (FMT == kTgI8) v[q] = (uint32_t)(int)acc[j][mb][q];
+              else v[q] = __float_as_uint((float)acc[j][mb][q]);
+            }
+            uint32_t* dst = pb + (int64_t)grow * a.N + n;
+            if (vec && n + 3 < a.N) {
+              *(u32x4*)dst = u32x4{v[0], v[1], v[2], v[3]};
+            } else {
+  #pragma unroll
               for (int q = 0; q < 4; ++q)
-                if (n + q < a.N) dst[q] = o[q];
+                if (n + q < a.N) dst[q] = v[q];
             }
-            if constexpr (FMT == kTgI8) {
-              if (a.acc_out && grow < row_end) {
-                int32_t* ad = a.acc_out + (int64_t)grow * a.N + n;
-#pragma unroll
+          }
+        }
+      } else {
+        const float* eX = (const float*)(smem + kTgLdsEpi) + buf * 3 * 256;
+        // each wave's 128 x 64 output block goes through its 8 KB of the idle
+        // pipeline stage in two column halves ([m][64 columns], 16-byte chunk c of
+        // row m at c ^ (m & 7)), so every global store writes whole 128-byte
+        // row segments; rows of 8-aligned N only (others store directly)
+        uint8_t* stg = smem + (wave < 4 ? kTgLdsW : kTgLdsX) + (st ^ 1) * (kTgBN * kTgBK) + (wave & 3) * 8192;
+        const bool staged = (a.N & 7) == 0;
+  #pragma unroll
+        for (int half = 0; half < 2; ++half) {
+  #pragma unroll
+          for (int jj = 0; jj < 4; ++jj) {
+            const int j = 4 * half + jj;
+            const int nl = 128 * wn + 16 * j + 4 * lg;  // tile column of q = 0
+            const int n = ntile * kTgBN + nl;
+            const f32x4 wsc = *(const f32x4*)(eX + 256 + nl);
+            const f32x4 bv = *(const f32x4*)(eX + 512 + nl);
+  #pragma unroll
+            for (int mb = 0; mb < 4; ++mb) {
+              const int ml = 16 * mb + lr;  // row within the wave's block
+              const int grow = row0 + 64 * wm + ml;
+              const float xsc = BLOCK ? 1.0f : eX[64 * wm + ml];
+              uint16_t o[4];
+  #pragma unroll
+              for (int q = 0; q < 4; ++q) {
+                float v = (float)acc[j][mb][q];
+                if (!BLOCK) v = __fmul_rn(__fmul_rn(v, xsc), wsc[q]);
+                if (a.bias_dtype != KQ_DTYPE_NONE) v = __fadd_rn(v, bv[q]);
+                o[q] = tg_to_out(v, ODT);
+              }
+              const u32x2 word = u32x2{(uint32_t)o[0] | ((uint32_t)o[1] << 16), (uint32_t)o[2] | ((uint32_t)o[3] << 16)};
+              if (staged) {
+                const int cb = 32 * jj + 8 * lg;  // byte column within the 128-byte row
+                *(u32x2*)(stg + ml * 128 + (((cb >> 4) ^ (ml & 7)) << 4) + (cb & 15)) = word;
+              } else if (grow < row_end) {
+                uint16_t* dst = (uint16_t*)a.out + (int64_t)grow * a.N + n;
+  #pragma unroll
                 for (int q = 0; q < 4; ++q)
-                  if (n + q < a.N) ad[q] = acc[j][mb][q];
+                  if (n + q < a.N) dst[q] = o[q];
+              }
+              if constexpr (FMT == kTgI8) {
+                if (a.acc_out && grow < row_end) {
+                  int32_t* ad = a.acc_out + (int64_t)grow * a.N + n;
+  #pragma unroll
+                  for (int q = 0; q < 4; ++q)
+                    if (n + q < a.N) ad[q] = acc[j][mb][q];
+                }
               }
             }
           }
-        }
-        if (staged) {
-#pragma unroll
-          for (int i = 0; i < 8; ++i) {
-            const int ml = 8 * i + (lane >> 3), c = lane & 7;
-            const int grow = row0 + 64 * wm + ml;
-            const int n = ntile * kTgBN + 128 * wn + 64 * half + 8 * c;
-            const i32x4 v = *(const i32x4*)(stg + ml * 128 + ((c ^ (ml & 7)) << 4));
-            if (grow < row_end && n < a.N) *(i32x4*)((uint16_t*)a.out + (int64_t)grow * a.N + n) = v;
+          if (staged) {
+  #pragma unroll
+            for (int i = 0; i < 8; ++i) {
+              const int ml = 8 * i + (lane >> 3), c = lane & 7;
+              const int grow = row0 + 64 * wm + ml;
+              const int n = ntile * kTgBN + 128 * wn + 64 * half + 8 * c;
+              const i32x4 v = *(const i32x4*)(stg + ml * 128 + ((c ^ (ml & 7)) << 4));
+              if (grow < row_end && n < a.N) *(i32x4*)((uint16_t*)a.out + (int64_t)grow * a.N + n) = v;
+            }
           }
         }
       }
-    }
+    };
+    if (a.out_dtype == KQ_DTYPE_BF16) epilogue(std::integral_constant<int, KQ_DTYPE_BF16>{});
+    else epilogue(std::integral_constant<int, KQ_DTYPE_F16>{});
     if (!has_next) break;
     __builtin_amdgcn_s_waitcnt(0);  // the next tile's first block has landed
     __syncthreads();
