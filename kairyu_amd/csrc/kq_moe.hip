@@ -195,25 +195,49 @@ KQ_DEV int block_exclusive_scan(int* v, int* tmp, int n) {
   return total;
 }
 
+// Chunk slices of the scan: the largest power of two with 2 * slices * E <=
+// 1024 (at least 1), so slices * E threads each scan one run of chunks.
+__host__ __device__ inline int moe_scan_slices(int E) {
+  int slices = 1;
+  while (slices * 2 * E <= 1024) slices *= 2;
+  return slices;
+}
+
 // One 1024-thread workgroup: column-wise exclusive scan of counts[C][E] into
 // base[c][e] (sorted position of chunk c's first row of expert e), expert
 // offsets, the row-tile table (tile i -> (expert, first row, end row, 0);
 // unused entries get expert -1) and the count of tiles in use.  Thread
-// (slice, e) scans a contiguous run of chunks.
+// (slice, e) scans a contiguous run of chunks.  PER > 0: the run has at most
+// PER chunks, and the thread issues all its count loads at once into
+// registers (unconditional loads from clamped, in-range addresses, so no load
+// sits under a branch and they overlap) and keeps them for the second pass;
+// PER = 0: any run length, one load at a time.
+template <int PER>
 __global__ void __launch_bounds__(1024)
 moe_scan_kernel(const int32_t* __restrict__ counts, int C, int E, int BM, int max_tiles,
                 int32_t* __restrict__ offsets, int32_t* __restrict__ base, int32_t* __restrict__ tiles,
                 int32_t* __restrict__ tile_count) {
   __shared__ int part[1024], tot[1024], ntile[1024], tmp[1024];
   const int t = threadIdx.x;
-  int slices = 1;
-  while (slices * 2 * E <= 1024) slices *= 2;
+  const int slices = moe_scan_slices(E);
   const int per = (C + slices - 1) / slices;
   const int e = t % E, sl = t / E;
   const bool active = sl < slices;
   const int c0 = active ? sl * per : 0, c1 = active ? min(C, c0 + per) : 0;
+  int cnt[PER > 0 ? PER : 1];
   int sum = 0;
-  for (int c = c0; c < c1; ++c) sum += counts[(int64_t)c * E + e];
+  if constexpr (PER > 0) {
+    const int last = max(c1 - 1, 0);   // C >= 1, so chunk 0 always exists
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int v = counts[(int64_t)min(c0 + i, last) * E + e];
+      cnt[i] = c0 + i < c1 ? v : 0;
+    }
+#pragma unroll
+    for (int i = 0; i < PER; ++i) sum += cnt[i];
+  } else {
+    for (int c = c0; c < c1; ++c) sum += counts[(int64_t)c * E + e];
+  }
   part[t] = sum;
   __syncthreads();
   if (t < E) {
@@ -232,9 +256,17 @@ moe_scan_kernel(const int32_t* __restrict__ counts, int C, int E, int BM, int ma
   (void)total_rows;
   if (active) {
     int run = tot[e] + part[t];
-    for (int c = c0; c < c1; ++c) {
-      base[(int64_t)c * E + e] = run;
-      run += counts[(int64_t)c * E + e];
+    if constexpr (PER > 0) {
+#pragma unroll
+      for (int i = 0; i < PER; ++i) {
+        if (c0 + i < c1) base[(int64_t)(c0 + i) * E + e] = run;
+        run += cnt[i];
+      }
+    } else {
+      for (int c = c0; c < c1; ++c) {
+        base[(int64_t)c * E + e] = run;
+        run += counts[(int64_t)c * E + e];
+      }
     }
   }
   if (t < E) {
@@ -546,8 +578,16 @@ extern "C" int kq_moe_block_fp8_experts(const void* hidden, int dtype, int64_t t
 
   hipLaunchKernelGGL(moe_count_kernel, dim3(C), dim3(kSortChunk), E * sizeof(int), st, topk_idx, R, E,
                      counts);
-  hipLaunchKernelGGL(moe_scan_kernel, dim3(1), dim3(1024), 0, st, counts, C, E, kBM, max_tiles, offsets,
-                     base, tiles, tile_count);
+  const int scan_per = (C + moe_scan_slices(E) - 1) / moe_scan_slices(E);
+  if (scan_per <= 16)
+    hipLaunchKernelGGL(moe_scan_kernel<16>, dim3(1), dim3(1024), 0, st, counts, C, E, kBM, max_tiles,
+                       offsets, base, tiles, tile_count);
+  else if (scan_per <= 64)
+    hipLaunchKernelGGL(moe_scan_kernel<64>, dim3(1), dim3(1024), 0, st, counts, C, E, kBM, max_tiles,
+                       offsets, base, tiles, tile_count);
+  else
+    hipLaunchKernelGGL(moe_scan_kernel<0>, dim3(1), dim3(1024), 0, st, counts, C, E, kBM, max_tiles,
+                       offsets, base, tiles, tile_count);
   hipLaunchKernelGGL(moe_scatter_kernel, dim3(C), dim3(kSortChunk), 0, st, topk_idx, R, E, base, sorted,
                      inv);
   launch_act_quant_blocks(hidden, dtype, tokens, hidden_size, hidden_size, xq, xs, st);

@@ -134,6 +134,36 @@ def test_routed_block_fp8_experts_match_oracle(cuda, cfg):
     assert_close_fp(np32(out), expected, label=str(cfg))
 
 
+@pytest.mark.parametrize("tokens,top_k,experts", [
+    (600, 8, 512),     # 19 sort chunks over 2 slices: runs of <= 16 chunks
+    (1000, 8, 1024),   # 32 chunks, one slice: runs of <= 64 chunks
+    (3000, 8, 1024),   # 94 chunks, one slice: the any-length scan
+])
+def test_sort_scan_forms_match_oracle(cuda, tokens, top_k, experts):
+    """Every form of the expert-offset scan (by chunks per thread), with
+    many experts and given top-k indices (each token's experts distinct).
+
+    A token's result does not depend on the other tokens of the call (fixed
+    K order per output, per-token quantization, slot-order combine), so the
+    whole call must equal, bit for bit, the same tokens run 256 at a time
+    (8 sort chunks: the short-run form); a token sample is checked against
+    the oracle."""
+    banner(f"moe sort tokens={tokens} top_k={top_k} experts={experts}")
+    pack = _pack(experts, 128, 128, seed=tokens, device=cuda)
+    g = torch.Generator().manual_seed(tokens + 1)
+    x = torch.randn(tokens, 128, generator=g).to(torch.bfloat16)
+    idx = torch.argsort(torch.rand(tokens, experts, generator=g), dim=1)[:, :top_k].to(torch.int32)
+    w = torch.softmax(torch.randn(tokens, top_k, generator=g), dim=1)
+    xd, idxd, wd = x.to(cuda), idx.to(cuda), w.to(cuda)
+    out = pack.forward(xd, idxd, wd)
+    parts = torch.cat([pack.forward(xd[i:i + 256], idxd[i:i + 256], wd[i:i + 256])
+                       for i in range(0, tokens, 256)])
+    assert torch.equal(out, parts)
+    sample = np.random.default_rng(tokens).choice(tokens, size=24, replace=False)
+    expected = _oracle_moe(pack, x, idx.numpy(), w.numpy(), tokens=sample)
+    assert_close_fp(np32(out)[sample], expected, label=f"sort {tokens}x{top_k} E={experts}")
+
+
 def test_block_module_uses_grouped_path_and_matches_cpu(cuda):
     torch.manual_seed(2)
     block = hmoe.Qwen3BlockFp8MoeBlock(256, 128, 8, 2)
