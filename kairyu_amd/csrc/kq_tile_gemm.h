@@ -356,6 +356,14 @@ tile_gemm_kernel(TileGemmArgs a) {
     // for all vector-memory operations (the next block's copies included) in
     // every K step; one wait per tile here lets it drop that.
     if constexpr (EPI == kTgEpiStore) __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    // Block scaling (MoE experts, block-FP8 linear): a ragged row tile (an
+    // expert's last one holds a few rows at C5-like routing, about a third of
+    // the row tiles) can leave this wave's 64-row slab without rows; the wave
+    // then skips its fragment reads and MFMAs (its accumulators stay 0 and are
+    // never stored) and only takes part in the copies and barriers.  (The
+    // W8A8 prefill instantiations keep the unbranched loop: same speed
+    // without the branch, measured.)
+    const bool slab_live = !BLOCK || __builtin_amdgcn_readfirstlane(cur.row_end - cur.row0 - 64 * wm) > 0;
     for (int kb = cur.kb0; kb < cur.kb1; ++kb) {
       if (kb + 1 < cur.kb1) issue(kb + 1, st ^ 1);
       const uint8_t* sW = smem + kTgLdsW + st * (kTgBN * kTgBK) + (128 * wn) * kTgBK;
@@ -377,43 +385,52 @@ tile_gemm_kernel(TileGemmArgs a) {
           for (int mb = 0; mb < 4; ++mb) prod[0][mb] = prod[1][mb] = sx[mb] * s0;
         }
       }
-      TgFrag xf[4];
-      f32x4 blk[2];
+      // fragment reads and MFMAs of row blocks mb < NRB
+      auto kstep = [&](auto nrb_c) {
+        constexpr int NRB = decltype(nrb_c)::value;
+        TgFrag xf[NRB];
+        f32x4 blk[2];
 #pragma unroll
-      for (int mb = 0; mb < 4; ++mb) xf[mb] = tg_load(sX + mb * 16 * kTgBK, o_lo, o_hi);
+        for (int mb = 0; mb < NRB; ++mb) xf[mb] = tg_load(sX + mb * 16 * kTgBK, o_lo, o_hi);
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const TgFrag wf = tg_load(sW + j * 16 * kTgBK, o_lo, o_hi);
+        for (int j = 0; j < 8; ++j) {
+          const TgFrag wf = tg_load(sW + j * 16 * kTgBK, o_lo, o_hi);
 #pragma unroll
-        for (int mb = 0; mb < 4; ++mb) {
-          if constexpr (FMT == kTgI8) {
-            acc[j][mb] = mfma_i8(wf.lo, xf[mb].lo, acc[j][mb]);
-            acc[j][mb] = mfma_i8(wf.hi, xf[mb].hi, acc[j][mb]);
-          } else {
-            const i32x8 A = i32x8{wf.lo[0], wf.lo[1], wf.lo[2], wf.lo[3], wf.hi[0], wf.hi[1], wf.hi[2], wf.hi[3]};
-            const i32x8 B = i32x8{xf[mb].lo[0], xf[mb].lo[1], xf[mb].lo[2], xf[mb].lo[3],
-                                  xf[mb].hi[0], xf[mb].hi[1], xf[mb].hi[2], xf[mb].hi[3]};
-            if constexpr (BLOCK) {
-              // scale-accumulate one MFMA behind, from alternating temporaries,
-              // so no MFMA waits on its own result before the next is issued
-              const int idx = j * 4 + mb;
-              blk[idx & 1] = mfma_fp8(A, B, f32x4{0.f, 0.f, 0.f, 0.f});
-              if (idx > 0) {
-                const int pj = (idx - 1) >> 2, pm = (idx - 1) & 3;
-                const float sc = prod[pj >> 2][pm];
-#pragma unroll
-                for (int q = 0; q < 4; ++q) acc[pj][pm][q] = fmaf(blk[(idx - 1) & 1][q], sc, acc[pj][pm][q]);
-              }
-              if (idx == 31) {
-                const float sc = prod[1][3];
-#pragma unroll
-                for (int q = 0; q < 4; ++q) acc[7][3][q] = fmaf(blk[1][q], sc, acc[7][3][q]);
-              }
+          for (int mb = 0; mb < NRB; ++mb) {
+            if constexpr (FMT == kTgI8) {
+              acc[j][mb] = mfma_i8(wf.lo, xf[mb].lo, acc[j][mb]);
+              acc[j][mb] = mfma_i8(wf.hi, xf[mb].hi, acc[j][mb]);
             } else {
-              acc[j][mb] = mfma_fp8(A, B, acc[j][mb]);
+              const i32x8 A = i32x8{wf.lo[0], wf.lo[1], wf.lo[2], wf.lo[3], wf.hi[0], wf.hi[1], wf.hi[2], wf.hi[3]};
+              const i32x8 B = i32x8{xf[mb].lo[0], xf[mb].lo[1], xf[mb].lo[2], xf[mb].lo[3],
+                                    xf[mb].hi[0], xf[mb].hi[1], xf[mb].hi[2], xf[mb].hi[3]};
+              if constexpr (BLOCK) {
+                // scale-accumulate one MFMA behind, from alternating temporaries,
+                // so no MFMA waits on its own result before the next is issued
+                const int idx = j * NRB + mb;
+                blk[idx & 1] = mfma_fp8(A, B, f32x4{0.f, 0.f, 0.f, 0.f});
+                if (idx > 0) {
+                  const int pj = (idx - 1) / NRB, pm = (idx - 1) % NRB;
+                  const float sc = prod[pj >> 2][pm];
+#pragma unroll
+                  for (int q = 0; q < 4; ++q) acc[pj][pm][q] = fmaf(blk[(idx - 1) & 1][q], sc, acc[pj][pm][q]);
+                }
+                if (idx == 8 * NRB - 1) {
+                  const float sc = prod[1][NRB - 1];
+#pragma unroll
+                  for (int q = 0; q < 4; ++q) acc[7][NRB - 1][q] = fmaf(blk[idx & 1][q], sc, acc[7][NRB - 1][q]);
+                }
+              } else {
+                acc[j][mb] = mfma_fp8(A, B, acc[j][mb]);
+              }
             }
           }
         }
+      };
+      if constexpr (BLOCK) {
+        if (slab_live) kstep(std::integral_constant<int, 4>{});
+      } else {
+        kstep(std::integral_constant<int, 4>{});
       }
       __builtin_amdgcn_s_waitcnt(0);  // this wave's copies of the next block have landed
       __syncthreads();                 // ... and everyone's; stage st is free again
