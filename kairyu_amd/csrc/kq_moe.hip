@@ -148,19 +148,18 @@ moe_route_kernel(const void* __restrict__ logits, int dtype, int T, int E, int k
 constexpr int kSortChunk = 256;   // rows per chunk = threads per sort workgroup
 constexpr int kBM = kTgBM;        // rows per GEMM row tile
 
-// Per-chunk expert histogram: counts[c][e].
-__global__ void __launch_bounds__(kSortChunk)
-moe_count_kernel(const int32_t* __restrict__ idx, int R, int E, int32_t* __restrict__ counts) {
-  extern __shared__ int hist[];
+// Per-chunk expert histogram: counts[c][e] for chunk c (hist: E ints of LDS).
+KQ_DEV void moe_count_chunk(const int32_t* __restrict__ idx, int R, int E, int32_t* __restrict__ counts,
+                            int c, int* hist) {
   for (int i = threadIdx.x; i < E; i += kSortChunk) hist[i] = 0;
   __syncthreads();
-  const int r = blockIdx.x * kSortChunk + threadIdx.x;
+  const int r = c * kSortChunk + threadIdx.x;
   if (r < R) {
     const int e = idx[r];
     if (e >= 0 && e < E) atomicAdd(&hist[e], 1);
   }
   __syncthreads();
-  for (int i = threadIdx.x; i < E; i += kSortChunk) counts[(int64_t)blockIdx.x * E + i] = hist[i];
+  for (int i = threadIdx.x; i < E; i += kSortChunk) counts[(int64_t)c * E + i] = hist[i];
 }
 
 // Exclusive prefix sum of v[0..n) in LDS (n <= 1024); returns the total.
@@ -315,12 +314,11 @@ moe_scatter_kernel(const int32_t* __restrict__ idx, int R, int E, const int32_t*
 }
 
 // --------------------------------------------------- 1x128 activation quant
-// Grid (rows, ceil(K / 2048)); 256 threads x 8 elements; 16 threads per block.
-__global__ void __launch_bounds__(256)
-act_quant_fp8_blocks_kernel(const uint16_t* __restrict__ x, int dtype, int K, int64_t ldx, bool vec,
-                            uint8_t* __restrict__ xq, float* __restrict__ xs) {
-  const int64_t row = blockIdx.x;
-  const int k0 = blockIdx.y * 2048 + threadIdx.x * 8;
+// One 2048-element span (256 threads x 8) of row `row`: 16 threads per 1x128
+// block, e4m3 values and the block's scale.
+KQ_DEV void act_quant_fp8_blocks_span(const uint16_t* __restrict__ x, int dtype, int K, int64_t ldx, bool vec,
+                                      uint8_t* __restrict__ xq, float* __restrict__ xs, int64_t row, int y) {
+  const int k0 = y * 2048 + threadIdx.x * 8;
   const uint16_t* xr = x + row * ldx;
   float v[8];
   if (vec && k0 + 8 <= K) {
@@ -373,6 +371,31 @@ act_quant_fp8_blocks_kernel(const uint16_t* __restrict__ x, int dtype, int K, in
   }
   if ((threadIdx.x & 15) == 0) xs[row * ((K + 127) / 128) + k0 / 128] = s;
 }
+
+// Grid (rows, ceil(K / 2048)); 256 threads x 8 elements; 16 threads per block.
+__global__ void __launch_bounds__(256)
+act_quant_fp8_blocks_kernel(const uint16_t* __restrict__ x, int dtype, int K, int64_t ldx, bool vec,
+                            uint8_t* __restrict__ xq, float* __restrict__ xs) {
+  act_quant_fp8_blocks_span(x, dtype, K, ldx, vec, xq, xs, blockIdx.x, blockIdx.y);
+}
+
+// MoE: the chunk histograms (blocks [0, C)) and the token quantization
+// (blocks C + row * KY + y) in one launch; neither reads the other's output.
+static_assert(kSortChunk == 256, "a sort chunk and a quantization span both take 256 threads");
+__global__ void __launch_bounds__(256)
+moe_count_quant_kernel(const int32_t* __restrict__ idx, int R, int E, int32_t* __restrict__ counts, int C,
+                       const uint16_t* __restrict__ x, int dtype, int K, int64_t ldx, bool vec, int KY,
+                       uint8_t* __restrict__ xq, float* __restrict__ xs) {
+  extern __shared__ int hist[];
+  const int b = blockIdx.x;
+  if (b < C) {
+    moe_count_chunk(idx, R, E, counts, b, hist);
+  } else {
+    const int q = b - C;
+    act_quant_fp8_blocks_span(x, dtype, K, ldx, vec, xq, xs, q / KY, q % KY);
+  }
+}
+
 
 // ------------------------------------------------------------------ combine
 // out[t] = sum over slots s (in order) of fp32(y[inv[t*k+s]]) * w[t*k+s].
@@ -576,8 +599,15 @@ extern "C" int kq_moe_block_fp8_experts(const void* hidden, int dtype, int64_t t
   const int E = (int)experts;
   const int max_tiles = (R + kBM - 1) / kBM + E;
 
-  hipLaunchKernelGGL(moe_count_kernel, dim3(C), dim3(kSortChunk), E * sizeof(int), st, topk_idx, R, E,
-                     counts);
+  // chunk histograms and the token quantization share one launch
+  {
+    const int KY = (int)((hidden_size + 2047) / 2048);
+    const bool vec = ((uintptr_t)hidden % 16) == 0 && (hidden_size % 8) == 0;
+    const int64_t blocks = (int64_t)C + tokens * KY;
+    hipLaunchKernelGGL(moe_count_quant_kernel, dim3((unsigned)blocks), dim3(kSortChunk), E * sizeof(int), st,
+                       topk_idx, R, E, counts, C, (const uint16_t*)hidden, dtype, (int)hidden_size,
+                       (int64_t)hidden_size, vec, KY, xq, xs);
+  }
   const int scan_per = (C + moe_scan_slices(E) - 1) / moe_scan_slices(E);
   if (scan_per <= 16)
     hipLaunchKernelGGL(moe_scan_kernel<16>, dim3(1), dim3(1024), 0, st, counts, C, E, kBM, max_tiles,
@@ -590,7 +620,6 @@ extern "C" int kq_moe_block_fp8_experts(const void* hidden, int dtype, int64_t t
                        offsets, base, tiles, tile_count);
   hipLaunchKernelGGL(moe_scatter_kernel, dim3(C), dim3(kSortChunk), 0, st, topk_idx, R, E, base, sorted,
                      inv);
-  launch_act_quant_blocks(hidden, dtype, tokens, hidden_size, hidden_size, xq, xs, st);
 
   TileGemmArgs g{};
   g.x = xq; g.xs = xs; g.x_rows = (int)tokens; g.gather = sorted; g.topk = top_k;
