@@ -51,32 +51,23 @@ KQ_DEV uint32_t float_key(float v) {
 }
 
 
-// Wave-wide maximum of a 64-bit key, uniform result.  Within each row of 16
+// Wave-wide maximum of a 32-bit key, uniform result.  Within each row of 16
 // lanes: quad exchanges (xor 1, xor 2), then half-row and row mirrors through
 // DPP (register-to-register, no LDS round trip); the four row maxima are then
 // read from lanes 0, 16, 32, 48.
 template <int CTRL>
-KQ_DEV void dpp_max_step(uint32_t& lo, uint32_t& hi) {
-  const uint32_t olo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)lo, CTRL, 0xf, 0xf, false);
-  const uint32_t ohi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)hi, CTRL, 0xf, 0xf, false);
-  const bool gt = ohi > hi || (ohi == hi && olo > lo);
-  lo = gt ? olo : lo;
-  hi = gt ? ohi : hi;
+KQ_DEV uint32_t dpp_max_u32(uint32_t v) {
+  return max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xf, 0xf, false));
 }
 
-KQ_DEV uint64_t wave_max_u64_dpp(uint64_t v) {
-  uint32_t lo = (uint32_t)v, hi = (uint32_t)(v >> 32);
-  dpp_max_step<0xB1>(lo, hi);    // quad_perm [1,0,3,2]
-  dpp_max_step<0x4E>(lo, hi);    // quad_perm [2,3,0,1]
-  dpp_max_step<0x141>(lo, hi);   // row_half_mirror
-  dpp_max_step<0x140>(lo, hi);   // row_mirror
-  uint64_t best = 0;
+KQ_DEV uint32_t wave_max_u32_dpp(uint32_t v) {
+  v = dpp_max_u32<0xB1>(v);    // quad_perm [1,0,3,2]
+  v = dpp_max_u32<0x4E>(v);    // quad_perm [2,3,0,1]
+  v = dpp_max_u32<0x141>(v);   // row_half_mirror
+  v = dpp_max_u32<0x140>(v);   // row_mirror
+  uint32_t best = (uint32_t)__builtin_amdgcn_readlane((int)v, 0);
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const uint64_t k = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)hi, 16 * r) << 32) |
-                       (uint32_t)__builtin_amdgcn_readlane((int)lo, 16 * r);
-    best = k > best ? k : best;
-  }
+  for (int r = 1; r < 4; ++r) best = max(best, (uint32_t)__builtin_amdgcn_readlane((int)v, 16 * r));
   return best;
 }
 
@@ -90,8 +81,9 @@ KQ_DEV float key_float(uint32_t k) {
   return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
 }
 
-// One wave per token: k rounds of a wave-wide max over (value key, -expert);
-// every lane sees each round's winner, lane r keeps slot r's logit.
+// One wave per token: k rounds of a wave-wide max of the value keys, ties
+// to the smallest expert (a ballot of the lanes holding the maximum); every
+// lane sees each round's winner, lane r keeps slot r's logit.
 template <int PL>   // logits per lane: E <= 64 * PL
 __global__ void __launch_bounds__(256)
 moe_route_kernel(const void* __restrict__ logits, int dtype, int T, int E, int k, int norm,
@@ -107,21 +99,28 @@ moe_route_kernel(const void* __restrict__ logits, int dtype, int T, int E, int k
     live[i] = e < E;
     v[i] = live[i] ? load_as_f32(logits, dtype, (int64_t)t * E + e) : 0.0f;
   }
+  // value keys of the live experts; 0 marks a dead slot (no float maps to 0)
+  uint32_t key[PL];
+#pragma unroll
+  for (int i = 0; i < PL; ++i) key[i] = live[i] ? float_key(v[i]) : 0u;
   float my_sel = 0.0f, first = 0.0f, denom = 0.0f;
   for (int r = 0; r < k; ++r) {
-    uint64_t best = 0;
+    // the largest key, then the smallest expert holding it: slot i covers
+    // experts 64i..64i+63, so the first slot with a match holds the smallest
+    uint32_t m = key[0];
 #pragma unroll
-    for (int i = 0; i < PL; ++i) {
-      const uint64_t key = ((uint64_t)float_key(v[i]) << 32) |
-                           (uint32_t)(0xffffffffu - (uint32_t)(lane + 64 * i));
-      best = live[i] && key > best ? key : best;
+    for (int i = 1; i < PL; ++i) m = max(m, key[i]);
+    m = wave_max_u32_dpp(m);
+    int e = -1;
+#pragma unroll
+    for (int i = PL - 1; i >= 0; --i) {
+      const uint64_t hit = __ballot(key[i] == m);
+      if (hit) e = 64 * i + (int)__builtin_ctzll(hit);
     }
-    best = wave_max_u64_dpp(best);
-    const int e = (int)(0xffffffffu - (uint32_t)best);
-    const float val = key_float((uint32_t)(best >> 32));
+    const float val = key_float(m);
 #pragma unroll
     for (int i = 0; i < PL; ++i)
-      if (lane + 64 * i == e) live[i] = false;
+      if (lane + 64 * i == e) key[i] = 0u;
     if (lane == 0) idx[(int64_t)t * k + r] = e;
     if (lane == r) my_sel = val;
     if (r == 0) first = val;
