@@ -290,26 +290,43 @@ moe_scan_kernel(const int32_t* __restrict__ counts, int C, int E, int BM, int ma
 }
 
 // Sorted position of row r = base[chunk][e] + its rank among the chunk's
-// earlier rows routed to the same expert (stable).
+// earlier rows routed to the same expert (stable).  The rank is the rows of
+// expert e in the chunk's earlier waves (per-wave counts in LDS, whist[w][e])
+// plus the earlier lanes of this wave with expert e: one ballot per bit of
+// the expert id leaves the mask of lanes whose id equals this lane's.
 __global__ void __launch_bounds__(kSortChunk)
 moe_scatter_kernel(const int32_t* __restrict__ idx, int R, int E, const int32_t* __restrict__ base,
                    int32_t* __restrict__ sorted_rows, int32_t* __restrict__ inv) {
-  __shared__ int ids[kSortChunk];
+  extern __shared__ int whist[];   // [kSortChunk / 64][E]
   const int c = blockIdx.x, t = threadIdx.x;
+  const int w = t >> 6, lane = t & 63;
   const int r = c * kSortChunk + t;
   const int e = r < R ? idx[r] : -1;
-  ids[t] = e;
+  const bool ok = e >= 0 && e < E;
+  for (int i = t; i < (kSortChunk / 64) * E; i += kSortChunk) whist[i] = 0;
+  const int nbits = E > 1 ? 32 - __builtin_clz((unsigned)(E - 1)) : 0;
+  uint64_t same = __ballot(ok);
+  for (int b = 0; b < nbits; ++b) {
+    const bool bit = (e >> b) & 1;
+    const uint64_t m = __ballot(bit);
+    same &= bit ? m : ~m;
+  }
+  const int rank_in = __popcll(same & ((1ull << lane) - 1ull));
+  __syncthreads();   // whist cleared
+  if (ok && rank_in == 0) whist[w * E + e] = __popcll(same);
   __syncthreads();
   if (r >= R) return;
-  if (e < 0 || e >= E) {
+  if (!ok) {
     inv[r] = -1;
     return;
   }
-  int rank = 0;
-  for (int j = 0; j < t; ++j) rank += ids[j] == e ? 1 : 0;
+  int rank = rank_in;
+  for (int w2 = 0; w2 < w; ++w2) rank += whist[w2 * E + e];
   const int pos = base[(int64_t)c * E + e] + rank;
-  sorted_rows[pos] = r;
-  inv[r] = pos;
+  // (pos < R always holds for a consistent base table; the check keeps a
+  // position outside the buffer from ever being written or combined)
+  if (pos < R) sorted_rows[pos] = r;
+  inv[r] = pos < R ? pos : -1;
 }
 
 // --------------------------------------------------- 1x128 activation quant
@@ -617,8 +634,8 @@ extern "C" int kq_moe_block_fp8_experts(const void* hidden, int dtype, int64_t t
   else
     hipLaunchKernelGGL(moe_scan_kernel<0>, dim3(1), dim3(1024), 0, st, counts, C, E, kBM, max_tiles,
                        offsets, base, tiles, tile_count);
-  hipLaunchKernelGGL(moe_scatter_kernel, dim3(C), dim3(kSortChunk), 0, st, topk_idx, R, E, base, sorted,
-                     inv);
+  hipLaunchKernelGGL(moe_scatter_kernel, dim3(C), dim3(kSortChunk), (kSortChunk / 64) * E * sizeof(int), st,
+                     topk_idx, R, E, base, sorted, inv);
 
   TileGemmArgs g{};
   g.x = xq; g.xs = xs; g.x_rows = (int)tokens; g.gather = sorted; g.topk = top_k;
