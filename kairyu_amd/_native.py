@@ -156,29 +156,71 @@ def device_supported(index: int) -> bool:
     return _supported[index]
 
 
-_workspaces: dict[int, torch.Tensor] = {}
-_retired_workspaces: list[torch.Tensor] = []
+class WorkspacePool:
+    """Per-device scratch buffers (split-K partials, act-order activation
+    gather, MoE intermediates), one per device, reused by every call.
+
+    Growth is geometric: a call needing more than the current buffer gets
+    ``max(need, 2 * current)`` bytes, so a sequence of ever larger calls
+    allocates O(log(need)) times.  A buffer handed out while the stream was
+    capturing a graph may be referenced by that graph, so once outgrown it is
+    retained until the process ends; the retained buffers of one device sum to
+    less than its current buffer (each is at most half the next).  Any other
+    outgrown buffer is released after a device synchronization (kernels still
+    queued on it must finish before torch's allocator can hand it out again).
+    Calls sharing the buffer must be ordered on one stream, like the engine's
+    single-stream decode loop; grow it with an eager call of the largest shape
+    before capturing.
+    """
+
+    def __init__(self, allocate, capturing, synchronize, minimum: int = DEFAULT_WORKSPACE_BYTES):
+        self._allocate = allocate
+        self._capturing = capturing
+        self._synchronize = synchronize
+        self._minimum = minimum
+        self._buffers: dict[int, torch.Tensor] = {}
+        self._captured: dict[int, bool] = {}
+        self.retained: list[torch.Tensor] = []
+
+    @staticmethod
+    def grown_size(current: int, need: int, minimum: int) -> int:
+        return max(need, 2 * current, minimum)
+
+    def get(self, index: int, nbytes: int) -> torch.Tensor:
+        buffer = self._buffers.get(index)
+        capturing = bool(self._capturing(index))
+        if buffer is None or buffer.numel() < nbytes:
+            current = 0 if buffer is None else buffer.numel()
+            if buffer is not None:
+                if self._captured.get(index, False) or capturing:
+                    self.retained.append(buffer)
+                else:
+                    self._synchronize(index)
+            buffer = self._allocate(index, self.grown_size(current, nbytes, self._minimum))
+            self._buffers[index] = buffer
+            self._captured[index] = False
+        if capturing:
+            self._captured[index] = True
+        return buffer
+
+
+def _allocate_device(index: int, nbytes: int) -> torch.Tensor:
+    return torch.empty(nbytes, dtype=torch.uint8, device=torch.device("cuda", index))
+
+
+def _capturing(index: int) -> bool:
+    return torch.cuda.is_current_stream_capturing()
+
+
+def _synchronize(index: int) -> None:
+    torch.cuda.synchronize(index)
+
+
+_pool = WorkspacePool(_allocate_device, _capturing, _synchronize)
 
 
 def workspace(device: torch.device, nbytes: int = DEFAULT_WORKSPACE_BYTES) -> torch.Tensor:
-    """Per-device scratch buffer (split-K partials, act-order activation gather).
-
-    Allocated once per device through torch's caching allocator, grown when a
-    call needs more, and reused by every call (also inside captured graphs:
-    grow it with an eager call of the largest shape before capture; a buffer
-    it outgrows stays allocated, so graphs captured on it remain valid).  Calls
-    sharing it must be ordered on one stream, like the engine's single-stream
-    decode loop.
-    """
+    """The device's scratch buffer, at least ``nbytes`` long (``WorkspacePool``)."""
 
     index = device.index if device.index is not None else torch.cuda.current_device()
-    buffer = _workspaces.get(index)
-    if buffer is None or buffer.numel() < nbytes:
-        if buffer is not None:
-            # graphs captured earlier still point at the old buffer: keep it
-            # allocated (never returned to torch's allocator for other tensors)
-            _retired_workspaces.append(buffer)
-        buffer = torch.empty(max(nbytes, DEFAULT_WORKSPACE_BYTES), dtype=torch.uint8,
-                             device=torch.device("cuda", index))
-        _workspaces[index] = buffer
-    return buffer
+    return _pool.get(index, nbytes)

@@ -1,0 +1,16 @@
+"""AWQ W4A16 device forward under its per-format module name.
+
+Counterpart of the reference's legacy per-format entry
+(kairyu/kernels/awq_gemm_gpu.py:8-11): callers that import the format's own
+module get the same gfx950 kernel as quant_gemm_hip.awq_linear_forward.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from kairyu_amd.kernels.quant_gemm_hip import awq_linear_forward as _forward
+
+
+def linear_forward(x: torch.Tensor, module) -> torch.Tensor:
+    return _forward(x, module)

@@ -280,6 +280,17 @@ def _tile(qweight: torch.Tensor, src_format: int, perm: torch.Tensor | None, n: 
     return tiles
 
 
+def _refuse_under_capture(scheme: str) -> None:
+    """Building derived W4A16 operands allocates and (GPTQ) compares g_idx on
+    the host; neither may happen while a stream is capturing a graph."""
+
+    if torch.cuda.is_available() and torch.cuda.is_current_stream_capturing():
+        raise RuntimeError(
+            f"{scheme} derived operands are missing or stale during graph capture; run the "
+            "module once eagerly (after any weight update) before capturing"
+        )
+
+
 def _awq_operands(module, device: torch.device):
     """(tiles, natural-order qzeros) of an AWQ module, or None.
 
@@ -300,6 +311,7 @@ def _awq_operands(module, device: torch.device):
     cached = module.__dict__.get("_kq_awq_operands")
     if cached is not None and cached[0] == key:
         return cached[1]
+    _refuse_under_capture("AWQ")
     tiles = _tile(qweight, 0, None, n, k, device)
     qzeros_n = torch.empty_like(qzeros)
     _native.call(
@@ -353,6 +365,7 @@ def _gptq_operands(module, device: torch.device):
     cached = module.__dict__.get("_kq_gptq_operands")
     if cached is not None and cached[0] == key:
         return cached[1]
+    _refuse_under_capture("GPTQ")
     k, n, group = module.in_features, module.out_features, module.group_size
     natural = torch.arange(k, device=device, dtype=torch.int64) // group
     gi = g_idx.to(torch.int64)

@@ -24,7 +24,13 @@ from torch import nn
 
 from kairyu_amd import _native
 from kairyu_amd.quant import block_fp8
-from kairyu_amd.quant.linear import BlockFp8Linear
+from kairyu_amd.quant.linear import (
+    BlockFp8Linear,
+    ExpertScope,
+    LinearRole,
+    ModelScope,
+    make_linear,
+)
 
 __all__ = [
     "BlockFp8ExpertMlp",
@@ -82,16 +88,46 @@ def route_experts(block: nn.Module, hidden: torch.Tensor) -> tuple[torch.Tensor,
 
 # ------------------------------------------------------------------ experts
 class BlockFp8ExpertMlp(nn.Module):
-    """One SwiGLU expert with block-FP8 projections at the checkpoint's
-    (Hugging Face) names: ``down(silu(gate(x)) * up(x))`` (moe.py:27-83)."""
+    """One SwiGLU expert at the checkpoint's (Hugging Face) names:
+    ``down(silu(gate(x)) * up(x))`` (``_ExpertMlp``, moe.py:27-83).
+
+    With a ``linear_factory`` the three projections are built through
+    :func:`make_linear` with the reference's roles (``MLP_GATE`` / ``MLP_UP``
+    column-parallel, ``MLP_DOWN`` row-parallel) and expert identity, so the
+    checkpoint's quantization (block FP8 here) and the device kernel binding
+    come from the factory; without one they are :class:`BlockFp8Linear`."""
 
     _kairyu_grouped_swiglu = True
 
-    def __init__(self, hidden_size: int, intermediate_size: int) -> None:
+    def __init__(
+        self,
+        hidden_size: int,
+        intermediate_size: int,
+        linear_factory=None,
+        *,
+        prefix: str = "expert",
+        layer_index: int | None = None,
+        expert_index: int | None = None,
+        expert_scope: ExpertScope = ExpertScope.NONE,
+        model_scope: ModelScope = ModelScope.TARGET,
+    ) -> None:
         super().__init__()
-        self.gate_proj = BlockFp8Linear(hidden_size, intermediate_size, False)
-        self.up_proj = BlockFp8Linear(hidden_size, intermediate_size, False)
-        self.down_proj = BlockFp8Linear(intermediate_size, hidden_size, False)
+        if linear_factory is None:
+            self.gate_proj = BlockFp8Linear(hidden_size, intermediate_size, False)
+            self.up_proj = BlockFp8Linear(hidden_size, intermediate_size, False)
+            self.down_proj = BlockFp8Linear(intermediate_size, hidden_size, False)
+            return
+        common = {"layer_index": layer_index, "expert_index": expert_index,
+                  "expert_scope": expert_scope, "model_scope": model_scope}
+        self.gate_proj = make_linear(linear_factory, hidden_size, intermediate_size, False,
+                                     qualified_name=f"{prefix}.gate_proj", role=LinearRole.MLP_GATE,
+                                     shard_dim=0, **common)
+        self.up_proj = make_linear(linear_factory, hidden_size, intermediate_size, False,
+                                   qualified_name=f"{prefix}.up_proj", role=LinearRole.MLP_UP,
+                                   shard_dim=0, **common)
+        self.down_proj = make_linear(linear_factory, intermediate_size, hidden_size, False,
+                                     qualified_name=f"{prefix}.down_proj", role=LinearRole.MLP_DOWN,
+                                     shard_dim=1, **common)
 
     def forward(self, hidden: torch.Tensor) -> torch.Tensor:
         return self.down_proj(nn.functional.silu(self.gate_proj(hidden)) * self.up_proj(hidden))
@@ -257,16 +293,33 @@ def _refresh_grouped(module: nn.Module, _incompatible_keys=None) -> None:
 
 class Qwen3BlockFp8MoeBlock(nn.Module):
     """Qwen3 sparse MoE block (moe.py:276-332) with block-FP8 routed experts:
-    ``gate`` (router linear), ``experts.{i}.{gate,up,down}_proj``."""
+    ``gate`` (router linear), ``experts.{i}.{gate,up,down}_proj``.
+
+    With a ``linear_factory`` the router (``MOE_ROUTER``: dense by the default
+    selection policy) and every routed expert projection (``ROUTED`` scope,
+    global expert index) are built through it, as the reference's block does."""
 
     def __init__(self, hidden_size: int, intermediate_size: int, num_experts: int, top_k: int,
-                 norm_topk_prob: bool = True) -> None:
+                 norm_topk_prob: bool = True, linear_factory=None, *, prefix: str = "mlp",
+                 layer_index: int = 0, model_scope: ModelScope = ModelScope.TARGET) -> None:
         super().__init__()
         self.top_k = top_k
         self.norm_topk_prob = norm_topk_prob
-        self.gate = nn.Linear(hidden_size, num_experts, bias=False)
+        if linear_factory is None:
+            self.gate = nn.Linear(hidden_size, num_experts, bias=False)
+        else:
+            self.gate = make_linear(linear_factory, hidden_size, num_experts, False,
+                                    qualified_name=f"{prefix}.gate", model_scope=model_scope,
+                                    role=LinearRole.MOE_ROUTER, layer_index=layer_index)
         self.experts = nn.ModuleList(
-            BlockFp8ExpertMlp(hidden_size, intermediate_size) for _ in range(num_experts)
+            BlockFp8ExpertMlp(
+                hidden_size, intermediate_size, linear_factory,
+                prefix=f"{prefix}.experts.{index}", layer_index=layer_index,
+                expert_index=index if linear_factory is not None else None,
+                expert_scope=ExpertScope.ROUTED if linear_factory is not None else ExpertScope.NONE,
+                model_scope=model_scope,
+            )
+            for index in range(num_experts)
         )
         _refresh_grouped(self)
         self.register_load_state_dict_post_hook(_refresh_grouped)

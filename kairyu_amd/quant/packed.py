@@ -216,9 +216,15 @@ class QuantLinearPack:
                 for m in mods:  # the pack holds the only tiled copy
                     m.__dict__.pop("_kq_awq_operands", None)
             else:
+                first = mods[0]
+                if any(not torch.equal(m.g_idx, first.g_idx) for m in mods[1:]):
+                    # one activation gather serves every projection
+                    raise RuntimeError("packed GPTQ projections need one g_idx")
                 ops = [hip._gptq_operands(m, device) for m in mods]
                 if any(mode == hip.GIDX_PER_K for mode, _, _ in ops):
                     raise RuntimeError("GPTQ pack requires uniform or act-order groups")
+                if any(mode != ops[0][0] for mode, _, _ in ops):
+                    raise RuntimeError("packed GPTQ projections need one group mode")
                 d["tiles"] = torch.cat([t for _, t, _ in ops], dim=0)
                 d["zeros"] = torch.cat([m.qzeros for m in mods], dim=1).contiguous()
                 d["scales"] = torch.cat([m.scales for m in mods], dim=1).contiguous()

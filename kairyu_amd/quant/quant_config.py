@@ -1,8 +1,8 @@
 """HF ``quantization_config`` -> :class:`QuantConfig` detection.
 
-Interface of kairyu/engine/core/quant_config.py:27-321 (``QuantMethod``,
+Interface of kairyu/engine/core/quant_config.py:27-295 (``QuantMethod``,
 ``QuantConfig``, ``CheckpointQuantization``, ``detect_quantization``,
-``load_checkpoint_quantization``, ``validate_*``), limited to the formats this
+``load_checkpoint_quantization``), limited to the formats this
 package executes on gfx950: FP8 (per-tensor / per-channel), INT8 W8A8, AWQ and
 GPTQ W4A16, plus 128x128 block-scaled FP8 (``weight_block_size``), which the
 reference rejects (quant_config.py:156-163) and this package adds as its own
@@ -124,6 +124,11 @@ def _modelopt(quant: dict) -> QuantConfig:
             activation_bits=8,
             activation_dynamic=_activation_scheme(quant, "modelopt FP8"),
             ignored_layers=_ignored_layers(quant),
+        )
+    if algo == "NVFP4":
+        raise ValueError(
+            "modelopt NVFP4 checkpoints are not supported: NVFP4 is an NVIDIA FP4 ABI with no "
+            "gfx950 kernel in this package; supported modelopt quant_algo: FP8"
         )
     raise ValueError(f"unsupported modelopt quant_algo {algo!r}; supported: FP8")
 
@@ -252,19 +257,3 @@ def load_checkpoint_quantization(model_dir: str | Path, hf_config: dict) -> Chec
         producer_name=name,
         producer_version=version,
     )
-
-
-def validate_tensor_parallel_quantization(quant: QuantConfig) -> None:
-    if quant.method not in (QuantMethod.NONE, QuantMethod.FP8):
-        raise ValueError(
-            "tensor parallelism currently supports dense and FP8 checkpoints; "
-            f"got {quant.method.value}"
-        )
-
-
-def validate_model_quantization(quant: QuantConfig, *, is_mla: bool, architecture: str) -> None:
-    if is_mla and quant.method is not QuantMethod.NONE:
-        raise ValueError(
-            f"{architecture} MLA does not support {quant.method.value} checkpoints: its absorbed "
-            "KV projection requires an unquantized kv_b_proj weight"
-        )

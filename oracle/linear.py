@@ -117,3 +117,37 @@ def gptq_forward_fast(x, qweight, qzeros, scales, g_idx, x_dtype, bias=None) -> 
     a = w4a16_activation(x, x_dtype)
     out = a @ w.T
     return to_dtype(_bias_add(out.astype(np.float32), bias), x_dtype)
+
+
+def w4a16_reference(x, w_dequant_fp32, x_dtype: str, bias=None) -> tuple[np.ndarray, np.ndarray]:
+    """(pre, abs_terms) of the W4A16 contract: ``pre`` is the fp64 dot of the
+    fp16 activation operand and the fp16 weights ``fp16((q - z) * s)`` plus
+    the bias, before the cast to ``x_dtype``; ``abs_terms`` is
+    ``sum_k |a_k * w_k|`` per output, the scale of any fp32 accumulation error."""
+
+    a = w4a16_activation(x, x_dtype).astype(np.float64)
+    w = formats.w4a16_weight_fp16(w_dequant_fp32).astype(np.float64)
+    pre = a @ w.T
+    if bias is not None:
+        pre = pre + np.asarray(bias, np.float32).astype(np.float64)
+    return pre, np.abs(a) @ np.abs(w).T
+
+
+def awq_reference(x, qweight, qzeros, scales, group_size, x_dtype, bias=None):
+    return w4a16_reference(x, formats.awq_dequantize(qweight, qzeros, scales, group_size),
+                           x_dtype, bias)
+
+
+def gptq_reference(x, qweight, qzeros, scales, g_idx, x_dtype, bias=None):
+    return w4a16_reference(x, formats.gptq_dequantize(qweight, qzeros, scales, g_idx),
+                           x_dtype, bias)
+
+
+def fp8_abs_terms(x_bits, w_bits, x_scale, w_scale) -> np.ndarray:
+    """``sum_k |x_k * w_k| * xs * ws`` per output of an FP8 W8A8 product, in
+    the output's units (the scale of the fp32 accumulation error)."""
+
+    acc = np.abs(e4m3_decode(x_bits)).astype(np.float64) @ np.abs(e4m3_decode(w_bits)).astype(np.float64).T
+    ws = np.asarray(w_scale, np.float64).reshape(-1)
+    ws = ws.reshape(1, -1) if ws.size > 1 else ws.reshape(1, 1)
+    return acc * np.asarray(x_scale, np.float64).reshape(-1, 1) * ws

@@ -126,3 +126,19 @@ def moe_forward(hidden, topk_idx, topk_w, w13q, s13, w2q, s2, dtype: str = "bflo
         t, s = np.nonzero(idx == e)
         y[t, s] = expert_forward(x[t], w13q[e], s13[e], w2q[e], s2[e], dtype)
     return to_dtype(combine(y, topk_w), dtype)
+
+
+def block_fp8_linear_reference(x, wq, ws, bias=None) -> tuple[np.ndarray, np.ndarray]:
+    """(pre, abs_terms) of one block-FP8 linear: ``pre`` is the fp64 value
+    ``sum_b (qx . qw)_b * xs[r, b] * ws[n // 128, b] (+ bias)`` before any cast;
+    ``abs_terms`` the same sum over |qx| and |qw| (the scale of fp32
+    accumulation error)."""
+
+    xq, xs = block_fp8_quantize_rows(np.asarray(x, np.float32))
+    pre = block_gemm(xq, xs, wq, ws)
+    if bias is not None:
+        pre = pre + np.asarray(bias, np.float32).astype(np.float64)
+    # e4m3 magnitudes: the bits with the sign bit cleared
+    abs_terms = block_gemm(np.asarray(xq, np.uint8) & 0x7F, np.abs(xs),
+                           np.asarray(wq, np.uint8) & 0x7F, np.abs(ws))
+    return pre, abs_terms

@@ -9,11 +9,10 @@ from __future__ import annotations
 import pytest
 import torch
 
-from gpu_helpers import assert_close_fp, banner, bits, np32
+from gpu_helpers import banner, check_fp8, check_w4a16
 from kairyu_amd.graphs import BucketedGraphs
-from oracle import linear as olinear
 from test_gpu_packed import _fp8
-from test_gpu_w4a16 import _gptq_module, _oracle as _w4_oracle
+from test_gpu_w4a16 import _gptq_module
 
 pytestmark = pytest.mark.gpu
 
@@ -46,10 +45,8 @@ def test_bucketed_decode_graphs(cuda):
         padded[:rows] = x
         assert torch.equal(got, step(padded)[:rows])   # eager work between replays too
         hidden = up(x)
-        assert_close_fp(np32(hidden), _w4_oracle(up, x.cpu()), label=f"up rows={rows}")
-        _, _, _, pre = olinear.fp8_forward(np32(hidden), bits(down.weight), np32(down.weight_scale),
-                                           np32(down.bias))
-        assert_close_fp(np32(got), pre, label=f"step rows={rows}")
+        check_w4a16(hidden, up, x.cpu(), label=f"up rows={rows}")
+        check_fp8(got, hidden, down, label=f"step rows={rows}")
     big = torch.randn(20, K, generator=gen).to(torch.float16).to(cuda)
     assert torch.equal(graphs.run(big), step(big))     # beyond the largest bucket: eager
 

@@ -3,9 +3,11 @@
 Routing: expert indices exact (stable, ties to the smaller id), weights within
 2e-6 relative (fp32 softmax; exp may differ from numpy's by an ulp).
 Activation quantization (1x128 blocks): bytes and scales bit-exact.
-Dense block-FP8 linear and the routed experts: within 1e-2 normwise and
-rel-RMSE of the fp64-accumulated oracle.  Parity of the block-FP8 expert
-arithmetic is unpinned at the reference boundary (its hub kernel is not
+Dense block-FP8 linear: every output within one ulp (plus an fp32
+accumulation slack) of the fp64-accumulated oracle.  Routed experts: at least
+99% of the outputs within two ulps and relative RMSE <= 3e-3 of the oracle
+(``gpu_helpers.assert_moe_close`` says why no per-element bound holds there).
+Parity of the block-FP8 expert arithmetic is unpinned at the reference boundary (its hub kernel is not
 vendored); every piece is pinned by the oracle's own tests.
 """
 
@@ -15,7 +17,7 @@ import numpy as np
 import pytest
 import torch
 
-from gpu_helpers import assert_close_fp, banner, np32
+from gpu_helpers import assert_moe_close, banner, check_block_fp8, np32
 from kairyu_amd import _native
 from kairyu_amd import moe as hmoe
 from kairyu_amd import workloads
@@ -27,12 +29,15 @@ from oracle import formats, moe
 pytestmark = pytest.mark.gpu
 
 
+_DT = {torch.bfloat16: "bfloat16", torch.float16: "float16"}
+
+
 def _bits(t: torch.Tensor) -> np.ndarray:
     return t.detach().contiguous().view(torch.uint8).cpu().numpy()
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
-@pytest.mark.parametrize("experts,top_k", [(4, 1), (60, 2), (128, 8), (512, 8)])
+@pytest.mark.parametrize("experts,top_k", [(4, 1), (60, 2), (128, 8), (200, 8), (256, 8), (512, 8)])
 @pytest.mark.parametrize("norm", [True, False])
 def test_route_matches_oracle(cuda, dtype, experts, top_k, norm):
     g = torch.Generator().manual_seed(experts * 7 + top_k)
@@ -93,9 +98,7 @@ def test_dense_block_fp8_linear_matches_oracle(cuda, m, n, dtype):
     x = torch.randn(m, k, generator=g).to(dtype)
     out = module.to(cuda)(x.to(cuda))
     assert out.dtype == dtype
-    expected = moe.block_fp8_linear(x.float().numpy(), _bits(module.weight), module.weight_scale_inv.cpu().numpy(),
-                                    module.bias.detach().cpu().numpy())
-    assert_close_fp(np32(out), expected, label=f"dense m={m} n={n}")
+    check_block_fp8(out, x, module, label=f"dense m={m} n={n}")
 
 
 def _pack(experts, hidden, inter, seed, device):
@@ -131,7 +134,7 @@ def test_routed_block_fp8_experts_match_oracle(cuda, cfg):
     out = pack.forward(x.to(cuda), idx, w)
     assert out.dtype == dtype
     expected = _oracle_moe(pack, x, idx.cpu().numpy(), w.cpu().numpy())
-    assert_close_fp(np32(out), expected, label=str(cfg))
+    assert_moe_close(np32(out), expected, _DT[dtype], label=str(cfg))
 
 
 @pytest.mark.parametrize("tokens,top_k,experts", [
@@ -161,7 +164,7 @@ def test_sort_scan_forms_match_oracle(cuda, tokens, top_k, experts):
     assert torch.equal(out, parts)
     sample = np.random.default_rng(tokens).choice(tokens, size=24, replace=False)
     expected = _oracle_moe(pack, x, idx.numpy(), w.numpy(), tokens=sample)
-    assert_close_fp(np32(out)[sample], expected, label=f"sort {tokens}x{top_k} E={experts}")
+    assert_moe_close(np32(out)[sample], expected, "bfloat16", label=f"sort {tokens}x{top_k} E={experts}")
 
 
 def test_block_module_uses_grouped_path_and_matches_cpu(cuda):
@@ -196,7 +199,7 @@ def test_c5_shape_sampled_tokens_and_determinism(cuda):
     sample = np.random.default_rng(0).choice(4096, size=24, replace=False)
     pack = hmoe.GroupedBlockFp8Experts.from_tensors(mod.w13, mod.s13, mod.w2, mod.s2)
     expected = _oracle_moe(pack, wl.x.cpu(), idx.cpu().numpy(), w.cpu().numpy(), tokens=sample)
-    assert_close_fp(np32(out1)[sample], expected, label="C5 sample")
+    assert_moe_close(np32(out1)[sample], expected, "bfloat16", label="C5 sample")
 
 
 def test_graph_replays_match_eager(cuda):
@@ -238,3 +241,94 @@ def test_rejects_bad_shapes(cuda):
     module = BlockFp8Linear(200, 256, bias=False).to(cuda)
     with pytest.raises(ValueError, match="in_features % 128"):
         module(torch.randn(2, 200, device=cuda, dtype=torch.bfloat16))
+
+
+def test_factory_built_block_packs_its_experts_and_matches_oracle(cuda):
+    """The reference's construction (moe.py:276-332): every routed expert
+    projection through ``make_linear`` under the checkpoint's block-FP8
+    quantization; the experts become BlockFp8Linear modules bound to the HIP
+    forward, the block packs them (GroupedBlockFp8Experts.create) and the
+    grouped call matches the oracle."""
+    from kairyu_amd.quant.linear import LinearRole, linear_factory
+    from kairyu_amd.quant.quant_config import detect_quantization
+
+    banner("moe block through the factory")
+    quant = detect_quantization({"quantization_config": {"quant_method": "fp8",
+                                                         "weight_block_size": [128, 128]}})
+    factory = linear_factory(quant, device=cuda, dtype=torch.bfloat16)
+    block = hmoe.Qwen3BlockFp8MoeBlock(256, 128, 8, 2, linear_factory=factory, prefix="model.layers.1.mlp",
+                                       layer_index=1)
+    assert type(block.gate) is torch.nn.Linear                       # router stays dense
+    assert block.gate.linear_selection.reason == "default-dense-role:moe_router"
+    proj = block.experts[5].down_proj
+    assert isinstance(proj, BlockFp8Linear) and proj._fused_forward is hip.block_fp8_linear_forward
+    assert proj.linear_context.qualified_name == "model.layers.1.mlp.experts.5.down_proj"
+    assert proj.linear_context.role is LinearRole.MLP_DOWN and proj.linear_context.expert_index == 5
+    g = torch.Generator().manual_seed(17)
+    hmoe.quantize_experts(block, torch.randn(8, 256, 256, generator=g) * 0.05,
+                          torch.randn(8, 256, 128, generator=g) * 0.05)
+    with torch.no_grad():
+        block.gate.weight.normal_(0, 0.1, generator=g)
+    block = block.to(cuda)
+    block.gate.to(torch.bfloat16)
+    pack = block._grouped_experts
+    assert pack is not None and pack.w13.is_cuda and pack.is_current()
+    x = torch.randn(37, 256, generator=g).to(torch.bfloat16).to(cuda)
+    with torch.no_grad():
+        out = block(x)
+        idx, w = hmoe.route_logits(block.gate(x), 2)
+    expected = _oracle_moe(pack, x.cpu(), idx.cpu().numpy(), w.cpu().numpy())
+    assert_moe_close(np32(out), expected, "bfloat16", label="factory block")
+    # an expert projection on its own runs the bound dense block-FP8 kernel
+    single = block.experts[3].up_proj(x)
+    check_block_fp8(single, x, block.experts[3].up_proj, label="factory expert up_proj")
+
+
+def test_single_route_with_empty_trailing_experts(cuda):
+    """One token routed to expert 0 of 4 with weight 1 (reference
+    tests/gpu/test_grouped_moe_gpu.py:133-146): experts 1..3 get no rows."""
+    pack = _pack(4, 256, 128, seed=13, device=cuda)
+    x = torch.randn(1, 256, generator=torch.Generator().manual_seed(13)).to(torch.bfloat16).to(cuda)
+    idx = torch.zeros(1, 1, dtype=torch.int64, device=cuda)
+    w = torch.ones(1, 1, dtype=torch.float32, device=cuda)
+    out = pack.forward(x, idx, w)
+    expected = _oracle_moe(pack, x.cpu(), idx.cpu().numpy(), w.cpu().numpy())
+    assert_moe_close(np32(out), expected, "bfloat16", label="single route")
+    # weight 1 on one slot: the combine is the expert's own output
+    alone = moe.expert_forward(np32(x), _bits(pack.w13)[0], pack.s13[0].cpu().numpy(),
+                               _bits(pack.w2)[0], pack.s2[0].cpu().numpy())
+    assert np.array_equal(expected, alone)
+
+
+def test_empty_input_preserves_shape(cuda):
+    """No tokens (reference tests/gpu/test_grouped_moe_gpu.py:148-158): the
+    output keeps the [0, H] shape and nothing is launched."""
+    pack = _pack(4, 256, 128, seed=14, device=cuda)
+    x = torch.empty(0, 256, device=cuda, dtype=torch.bfloat16)
+    out = pack.forward(x, torch.empty(0, 2, dtype=torch.int64, device=cuda),
+                       torch.empty(0, 2, dtype=torch.float32, device=cuda))
+    assert out.shape == x.shape and out.dtype == x.dtype
+    block = hmoe.Qwen3BlockFp8MoeBlock(256, 128, 4, 2).to(cuda)
+    block.gate.to(torch.bfloat16)
+    with torch.no_grad():
+        assert block(torch.empty(3, 0, 256, device=cuda, dtype=torch.bfloat16)).shape == (3, 0, 256)
+
+
+def test_grouped_path_has_no_host_synchronization(cuda):
+    """The routed-expert call issues no host-synchronizing ops (reference
+    tests/gpu/test_grouped_moe_gpu.py:87-130 asserts the same of its
+    grouped path): no nonzero / unique / item."""
+    pack = _pack(8, 256, 128, seed=15, device=cuda)
+    g = torch.Generator().manual_seed(15)
+    x = torch.randn(64, 256, generator=g).to(torch.bfloat16).to(cuda)
+    logits = torch.randn(64, 8, generator=g).to(cuda)
+    idx, w = hmoe._route(logits, 2, True)
+    pack.forward(x, idx, w)
+    torch.cuda.synchronize()
+    with torch.profiler.profile(activities=[torch.profiler.ProfilerActivity.CPU]) as prof:
+        idx, w = hmoe._route(logits, 2, True)
+        pack.forward(x, idx, w)
+    keys = {event.key for event in prof.key_averages()}
+    assert "aten::_local_scalar_dense" not in keys and "aten::nonzero" not in keys
+    assert not any("unique" in key for key in keys)
+    assert not any("synchronize" in key.lower() for key in keys)

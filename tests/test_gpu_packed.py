@@ -12,13 +12,13 @@ import numpy as np
 import pytest
 import torch
 
-from gpu_helpers import assert_close_fp, banner, bits, np32
+from gpu_helpers import banner, check_fp8, check_w4a16, np32
 from kairyu_amd.quant.fp8 import quantize_fp8
 from kairyu_amd.quant.int8 import quantize_int8_weight
 from kairyu_amd.quant.packed import QuantLinearPack
 from kairyu_amd.quant.linear import Fp8Linear, Int8Linear
 from oracle import linear as olinear
-from test_gpu_w4a16 import _awq_module, _gptq_module, _oracle as _w4_oracle
+from test_gpu_w4a16 import _awq_module, _gptq_module
 
 pytestmark = pytest.mark.gpu
 
@@ -77,9 +77,7 @@ def test_fp8_pack_matches_oracle(cuda, m, dynamic, per_channel):
     x = torch.randn(m, K, generator=torch.Generator().manual_seed(7 * m)).to(torch.bfloat16).to(cuda)
     for mod, o in zip(mods, pack(x)):
         static = None if dynamic else np32(mod.input_scale)
-        _, _, _, pre = olinear.fp8_forward(np32(x), bits(mod.weight), np32(mod.weight_scale),
-                                           np32(mod.bias), static_scale=static)
-        assert_close_fp(np32(o), pre, label=f"m={m}")
+        check_fp8(o, x, mod, label=f"m={m}", static_scale=static)
 
 
 @pytest.mark.parametrize("fmt,act_order", [("awq", False), ("gptq", False), ("gptq", True)])
@@ -102,7 +100,7 @@ def test_w4a16_pack_matches_oracle(cuda, fmt, act_order, m):
     x = torch.randn(m, K, generator=torch.Generator().manual_seed(11 * m)).to(torch.float16)
     outs = pack(x.to(cuda))
     for mod, o in zip(mods, outs):
-        assert_close_fp(np32(o), _w4_oracle(mod, x), label=f"{fmt} m={m}")
+        check_w4a16(o, mod, x, label=f"{fmt} m={m}")
 
 
 def test_pack_graph_replays_match_eager(cuda):

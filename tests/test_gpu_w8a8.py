@@ -1,8 +1,9 @@
 """INT8 / FP8 W8A8 on gfx950 against the CPU oracle.
 
 INT8 is bit-exact end to end (activation bytes and scales, int32 accumulators,
-bf16 output).  FP8 activation bytes and scales are bit-exact; outputs match
-the exact-accumulation oracle within 1e-2 normwise and rel-RMSE.  Cases follow
+bf16 output).  FP8 activation bytes and scales are bit-exact; every output is
+within one ulp of its dtype (plus an fp32 accumulation slack,
+``gpu_helpers.assert_ulp_close``) of the exact-accumulation oracle.  Cases follow
 the reference's tests/gpu/test_quant_kernels.py plus every kernel path of this
 package (skinny MT=1/2/4, split-K, tiled, generic K).
 """
@@ -13,7 +14,7 @@ import numpy as np
 import pytest
 import torch
 
-from gpu_helpers import DTYPE_NAME, assert_close_fp, banner, bits, np32
+from gpu_helpers import DTYPE_NAME, banner, bits, check_fp8, np32
 from kairyu_amd.kernels import quant_gemm_hip as hip
 from kairyu_amd.quant.fp8 import quantize_fp8
 from kairyu_amd.quant.int8 import quantize_int8_weight
@@ -134,9 +135,7 @@ def test_fp8_decode_wide_n_matches_oracle(cuda, k, m):
     module = _fp8_module(k, 8200, seed=k + 3 * m).to(cuda)
     x = torch.randn(m, k, generator=torch.Generator().manual_seed(k + m)).to(torch.bfloat16)
     out = module(x.to(cuda))
-    expected, _, _, pre = olinear.fp8_forward(np32(x), bits(module.weight), np32(module.weight_scale),
-                                              np32(module.bias))
-    assert_close_fp(np32(out), pre, label=f"k={k} m={m}")
+    check_fp8(out, x, module, label=f"k={k} m={m}")
 
 
 @pytest.mark.parametrize("k,m,per_channel", [(1536, 1, True), (4096, 8, False), (4096, 9, True),
@@ -146,9 +145,7 @@ def test_fp8_decode_path_matches_oracle(cuda, k, m, per_channel):
     module = _fp8_module(k, DECODE_N, seed=k + m, per_channel=per_channel).to(cuda)
     x = torch.randn(m, k, generator=torch.Generator().manual_seed(k * m)).to(torch.bfloat16)
     out = module(x.to(cuda))
-    expected, _, _, pre = olinear.fp8_forward(np32(x), bits(module.weight), np32(module.weight_scale),
-                                              np32(module.bias))
-    assert_close_fp(np32(out), pre, label=f"k={k} m={m}")
+    check_fp8(out, x, module, label=f"k={k} m={m}")
 
 
 def _two_step(kind, x, module, scale_mode=0, scale_in=None):
@@ -246,9 +243,7 @@ def test_fp8_tile_engine_split_k_matches_oracle(cuda, m, n, k):
     module = _fp8_module(k, n, seed=m + n).to(cuda)
     x = torch.randn(m, k, generator=torch.Generator().manual_seed(k)).to(torch.bfloat16)
     out = module(x.to(cuda))
-    expected, _, _, pre = olinear.fp8_forward(np32(x), bits(module.weight), np32(module.weight_scale),
-                                              np32(module.bias))
-    assert_close_fp(np32(out), pre, label=f"m={m} n={n} k={k}")
+    check_fp8(out, x, module, label=f"m={m} n={n} k={k}")
 
 
 # Whole-K tiles (at least one 256x256 tile per CU: no split-K); the second
@@ -276,9 +271,7 @@ def test_fp8_whole_tiles_match_oracle(cuda, m, n, k):
     module = _fp8_module(k, n, seed=m + n).to(cuda)
     x = torch.randn(m, k, generator=torch.Generator().manual_seed(k)).to(torch.bfloat16)
     out = module(x.to(cuda))
-    expected, _, _, pre = olinear.fp8_forward(np32(x), bits(module.weight), np32(module.weight_scale),
-                                              np32(module.bias))
-    assert_close_fp(np32(out), pre, label=f"m={m} n={n} k={k}")
+    check_fp8(out, x, module, label=f"m={m} n={n} k={k}")
 
 
 def test_w8a8_workspace_size_covers_split_k(cuda):
@@ -376,9 +369,7 @@ def test_fp8_output_matches_oracle_all_paths(cuda, m):
     module = _fp8_module(k, n, seed=m).to(cuda)
     x = torch.randn(m, k, generator=torch.Generator().manual_seed(m)).to(torch.bfloat16)
     out = module(x.to(cuda))
-    expected, _, _, pre = olinear.fp8_forward(np32(x), bits(module.weight), np32(module.weight_scale),
-                                              np32(module.bias))
-    assert_close_fp(np32(out), pre, label=f"m={m}")
+    check_fp8(out, x, module, label=f"m={m}")
 
 
 def test_fp8_per_tensor_weight_scale_and_static_input(cuda):
@@ -387,9 +378,7 @@ def test_fp8_per_tensor_weight_scale_and_static_input(cuda):
     module.input_scale.copy_(torch.tensor(0.01))
     x = torch.randn(7, 64, generator=torch.Generator().manual_seed(2)).to(torch.bfloat16)
     out = module.to(cuda)(x.to(cuda))
-    _, _, _, pre = olinear.fp8_forward(np32(x), bits(module.weight), np32(module.weight_scale),
-                                       static_scale=0.01)
-    assert_close_fp(np32(out), pre)
+    check_fp8(out, x, module, static_scale=0.01, add_bias=False)
 
 
 def test_fp8_global_per_token_scale_and_exact_amax(cuda):
@@ -402,9 +391,7 @@ def test_fp8_global_per_token_scale_and_exact_amax(cuda):
     xc = x.to(cuda)
     assert np.array_equal(np32(module.activation_amax(xc)), amax)
     out = module.forward_with_activation_scale(xc, torch.from_numpy(scale).to(cuda))
-    _, _, _, pre = olinear.fp8_forward(np32(x), bits(module.weight), np32(module.weight_scale),
-                                       np32(module.bias), row_scale=scale)
-    assert_close_fp(np32(out), pre)
+    check_fp8(out, x, module, row_scale=scale)
 
 
 # ------------------------------------------------ reference ragged cases

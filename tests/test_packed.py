@@ -94,3 +94,18 @@ def test_cpu_call_equals_separate_projections():
     assert [tuple(o.shape) for o in outs] == [(3, 5, 32), (3, 5, 16)]
     for o, m in zip(outs, mods):
         assert torch.equal(o, m(x))
+
+
+def test_gptq_pack_rebuild_rejects_a_diverged_g_idx():
+    """The pack gathers x once through the first projection's permutation, so
+    a g_idx updated in place on one projection must stop the pack at its next
+    operand rebuild instead of producing silently wrong rows."""
+    perm = (torch.randperm(128, generator=torch.Generator().manual_seed(3)) // 32).to(torch.int32)
+    g1, g2 = GptqLinear(128, 32, bias=False, group_size=32), GptqLinear(128, 32, bias=False, group_size=32)
+    g1.g_idx.copy_(perm)
+    g2.g_idx.copy_(perm)
+    pack = QuantLinearPack.create([g1, g2])
+    assert pack is not None
+    g2.g_idx.copy_(torch.flip(perm, [0]))
+    with pytest.raises(RuntimeError, match="one g_idx"):
+        pack._operands(torch.device("cpu"))
