@@ -25,7 +25,7 @@ import numpy as np
 import pytest
 import torch
 
-from gpu_helpers import assert_ulp_close, banner, bits, check_fp8, check_w4a16, np32
+from gpu_helpers import assert_ulp_close, banner, bits, check_fp8, check_w4a16, fp16_mfma_slack, np32
 from kairyu_amd import workloads
 from kairyu_amd.kernels import quant_gemm_hip as hip
 from oracle import linear as olinear
@@ -63,7 +63,7 @@ def test_c2_gptq_act_order(cuda, m):
         cols = slice(c0, c0 + 1024)
         pre, terms = olinear.gptq_reference(x, qweight[:, cols], qzeros[:, c0 // 8:(c0 + 1024) // 8],
                                             scales[:, cols], g_idx, "float16")
-        assert_ulp_close(out[:, cols], pre, "float16", terms, module.in_features,
+        assert_ulp_close(out[:, cols], pre, "float16", fp16_mfma_slack(terms, module.in_features),
                          label=f"C2 M={m} cols {c0}:{c0 + 1024}")
 
 

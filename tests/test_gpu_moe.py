@@ -5,7 +5,7 @@ Routing: expert indices exact (stable, ties to the smaller id), weights within
 Activation quantization (1x128 blocks): bytes and scales bit-exact.
 Dense block-FP8 linear: every output within one ulp (plus an fp32
 accumulation slack) of the fp64-accumulated oracle.  Routed experts: at least
-99% of the outputs within two ulps and relative RMSE <= 3e-3 of the oracle
+95% of the outputs within eight ulps and relative RMSE <= 5e-3 of the oracle
 (``gpu_helpers.assert_moe_close`` says why no per-element bound holds there).
 Parity of the block-FP8 expert arithmetic is unpinned at the reference boundary (its hub kernel is not
 vendored); every piece is pinned by the oracle's own tests.
