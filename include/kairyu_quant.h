@@ -184,6 +184,24 @@ int kq_w4a16_tiled_gemm(const void* x, int x_dtype, const int32_t* tiles, const 
                         int bias_dtype, void* out, int64_t m, int64_t n, int64_t k, int group_size,
                         void* workspace, size_t workspace_bytes, void* stream);
 
+/* Allocation-free form of kq_w4a16_tiled_gemm, same arguments and results
+ * except `workspace`: the call's scratch (act-order activation gather, the
+ * prefill GEMM's staged activations, split-K partial sums) lives in a fixed
+ * device array of KQ_W4A16_NOALLOC_SCRATCH_BYTES that the library holds on
+ * every GPU it runs on until the process ends.  A shape whose
+ * kq_w4a16_workspace_size() exceeds that size fails with KQ_EWORKSPACE before
+ * anything is launched.  The call allocates nothing (no hipMalloc, no
+ * allocating library routine), for callers that cannot allocate: code under
+ * HIP graph capture, tight serving loops, harnesses that forbid allocation.
+ * Calls on one GPU share its array: calls that overlap on one GPU (two
+ * streams, or two threads) race; order them on one stream.  No counterpart in
+ * the reference. */
+#define KQ_W4A16_NOALLOC_SCRATCH_BYTES (16u << 20)
+int kq_w4a16_tiled_gemm_noalloc(const void* x, int x_dtype, const int32_t* tiles,
+                                const int32_t* qzeros, int zero_offset, const void* scales,
+                                const int32_t* perm, const void* bias, int bias_dtype, void* out,
+                                int64_t m, int64_t n, int64_t k, int group_size, void* stream);
+
 /* Bytes of `workspace` a W4A16 call of this shape needs (gidx_mode as for
  * kq_w4a16_gptq_gemm; AWQ uses 0).  No reference counterpart: sizing helper
  * for the caller-owned scratch buffer. */

@@ -63,6 +63,9 @@ _SIGNATURES: dict[str, list] = {
     "kq_w4a16_tiled_gemm": [
         _P, _I, _P, _P, _I, _P, _P, _P, _I, _P, _I64, _I64, _I64, _I, _P, _SZ, _P,
     ],
+    "kq_w4a16_tiled_gemm_noalloc": [
+        _P, _I, _P, _P, _I, _P, _P, _P, _I, _P, _I64, _I64, _I64, _I, _P,
+    ],
     "kq_w4a16_workspace_size": [_I64, _I64, _I64, _I],
     "kq_moe_route_topk": [_P, _I, _I64, _I64, _I, _I, _P, _P, _P],
     "kq_act_quant_fp8_blocks": [_P, _I, _I64, _I64, _I64, _P, _P, _P],

@@ -38,6 +38,7 @@
 #include "kq_tile_gemm.h"  // LDS-DMA helpers (tg_dma16 / tg_dma4), kTgOob
 
 #include <algorithm>
+#include <mutex>
 
 namespace kq {
 
@@ -1350,21 +1351,21 @@ extern "C" int kq_w4a16_gptq_gemm(const void* x, int x_dtype, const int32_t* qwe
                 (hipStream_t)stream);
 }
 
-extern "C" int kq_w4a16_tiled_gemm(const void* x, int x_dtype, const int32_t* tiles,
-                                   const int32_t* qzeros, int zero_offset, const void* scales,
-                                   const int32_t* perm, const void* bias, int bias_dtype, void* out,
-                                   int64_t m, int64_t n, int64_t k, int group_size, void* workspace,
-                                   size_t workspace_bytes, void* stream) {
+// Arguments of the tiled entry points (validated; a.layout = tiles).
+static int tiled_args(const char* what, const void* x, int x_dtype, const int32_t* tiles,
+                      const int32_t* qzeros, int zero_offset, const void* scales,
+                      const int32_t* perm, const void* bias, int bias_dtype, void* out, int64_t m,
+                      int64_t n, int64_t k, int group_size, W4Args* args) {
   if (m > 0x7fffffff || n > 0x7fffffff || k > 0x7fffffff) {
-    set_error("kq_w4a16_tiled_gemm: dimensions exceed int32");
+    set_error("%s: dimensions exceed int32", what);
     return KQ_EINVAL;
   }
   if (k % 8 != 0 || group_size % 8 != 0 || (zero_offset != 0 && zero_offset != 1)) {
-    set_error("kq_w4a16_tiled_gemm: needs k %% 8 == 0, group_size %% 8 == 0, zero_offset 0 or 1");
+    set_error("%s: needs k %% 8 == 0, group_size %% 8 == 0, zero_offset 0 or 1", what);
     return KQ_EINVAL;
   }
   if ((uint64_t)(k / 8) * (uint64_t)((n + 15) / 16 * 16) * 4u >= ((uint64_t)1 << 32)) {
-    set_error("kq_w4a16_tiled_gemm: tiled weight exceeds 4 GiB");
+    set_error("%s: tiled weight exceeds 4 GiB", what);
     return KQ_EINVAL;
   }
   W4Args a{};
@@ -1374,8 +1375,84 @@ extern "C" int kq_w4a16_tiled_gemm(const void* x, int x_dtype, const int32_t* ti
   a.bias = bias; a.bias_dtype = bias_dtype; a.out = (uint16_t*)out; a.out_dtype = x_dtype;
   a.M = (int)m; a.N = (int)n; a.K = (int)k; a.G = group_size; a.zoff = (uint32_t)zero_offset;
   a.layout = kLayoutTiles;
+  *args = a;
+  return KQ_OK;
+}
+
+extern "C" int kq_w4a16_tiled_gemm(const void* x, int x_dtype, const int32_t* tiles,
+                                   const int32_t* qzeros, int zero_offset, const void* scales,
+                                   const int32_t* perm, const void* bias, int bias_dtype, void* out,
+                                   int64_t m, int64_t n, int64_t k, int group_size, void* workspace,
+                                   size_t workspace_bytes, void* stream) {
+  W4Args a{};
+  const int status = tiled_args("kq_w4a16_tiled_gemm", x, x_dtype, tiles, qzeros, zero_offset,
+                                scales, perm, bias, bias_dtype, out, m, n, k, group_size, &a);
+  if (status != KQ_OK) return status;
   return run_w4("kq_w4a16_tiled_gemm", kGptq, a, perm ? kGroupsPermuted : kGroupsUniform,
                 workspace, workspace_bytes, (hipStream_t)stream);
+}
+
+// ---------------------------------------------------------------------------
+// Allocation-free form of kq_w4a16_tiled_gemm.  Its scratch (the act-order
+// activation gather, the prefill GEMM's staged activations, split-K partial
+// sums) lives in this fixed array, which the runtime places once on every
+// device the library is loaded on.  Every scratch byte a call reads is written
+// earlier in the same call (gathers and partial planes are written in full),
+// so nothing needs clearing between calls; calls that overlap on one device
+// share the array and race.
+static __device__ __align__(256) uint8_t scratch[KQ_W4A16_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+constexpr int kScratchDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kScratchDevices] = {};
+}  // namespace
+
+// Device address of `scratch` on the current device, resolved once per device
+// (the symbol's host-side name is not a device address).
+static int current_scratch(const char* what, void** ptr) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kScratchDevices) {
+    set_error("%s: no current device (or device index %d beyond %d)", what, dev, kScratchDevices);
+    return KQ_EUNSUPPORTED;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* address = nullptr;
+    const hipError_t err = hipGetSymbolAddress(&address, HIP_SYMBOL(scratch));
+    if (err != hipSuccess || address == nullptr) {
+      set_error("%s: hipGetSymbolAddress(scratch) failed on device %d: %s", what, dev,
+                hipGetErrorString(err));
+      return KQ_ELAUNCH;
+    }
+    g_scratch_ptr[dev] = address;
+  }
+  *ptr = g_scratch_ptr[dev];
+  return KQ_OK;
+}
+
+extern "C" int kq_w4a16_tiled_gemm_noalloc(const void* x, int x_dtype, const int32_t* tiles,
+                                           const int32_t* qzeros, int zero_offset,
+                                           const void* scales, const int32_t* perm,
+                                           const void* bias, int bias_dtype, void* out, int64_t m,
+                                           int64_t n, int64_t k, int group_size, void* stream) {
+  const char* what = "kq_w4a16_tiled_gemm_noalloc";
+  W4Args a{};
+  int status = tiled_args(what, x, x_dtype, tiles, qzeros, zero_offset, scales, perm, bias,
+                          bias_dtype, out, m, n, k, group_size, &a);
+  if (status != KQ_OK) return status;
+  const size_t need = kq_w4a16_workspace_size(m, n, k, perm ? kGroupsPermuted : kGroupsUniform);
+  if (need > (size_t)KQ_W4A16_NOALLOC_SCRATCH_BYTES) {
+    set_error("%s: m=%lld n=%lld k=%lld needs %zu bytes of scratch, more than the fixed %zu "
+              "(use kq_w4a16_tiled_gemm with a workspace)", what, (long long)m, (long long)n,
+              (long long)k, need, (size_t)KQ_W4A16_NOALLOC_SCRATCH_BYTES);
+    return KQ_EWORKSPACE;
+  }
+  void* buffer = nullptr;
+  status = current_scratch(what, &buffer);
+  if (status != KQ_OK) return status;
+  return run_w4(what, kGptq, a, perm ? kGroupsPermuted : kGroupsUniform, buffer,
+                (size_t)KQ_W4A16_NOALLOC_SCRATCH_BYTES, (hipStream_t)stream);
 }
 
 extern "C" int kq_w4a16_tile_weights(const int32_t* qweight, int src_format, const int32_t* perm,
