@@ -7,16 +7,27 @@ batch; weights rotate over enough distinct HBM copies (> 256 MB MALL) that no
 step is served from the Infinity Cache.  Steps are captured in a HIP graph and
 timed with HIP events on the stream they run on.
 
-``roofline`` describes the dominant kernel alone: the decode GEMV's
-algorithmic bytes per launch over its per-launch time, timed live with HIP
-events on its own captured launches (x gathered once up front).
+``roofline`` describes the headline's dominant kernel alone: the decode
+GEMV's algorithmic bytes per launch over its per-launch time, timed live with
+HIP events on its own captured launches (x gathered once up front).
 
-``sweep`` reports every BASELINE configuration (C1-C4 over their M values, C5
-when built) with GB/s or TFLOPS and roofline fractions.  ``cpu_baseline``
-times the repo's CPU oracle (a numpy port of the reference's dequantize-then-
-matmul path) on a bounded sample of the headline workload on this host.
+``sweep`` reports every BASELINE configuration (C1-C4 over their M values,
+C5), each row with
+  * ``op``: the whole module call (activation quantization / act-order gather
+    included) -- GB/s, TFLOPS and both roofline fractions;
+  * ``gemm``: the dominant GEMM entry alone on pre-processed activations
+    (gathered fp16 x, quantized int8 / e4m3 rows), its algorithmic bytes or
+    FLOPs per launch over the per-launch time (none for C5, whose kernels are
+    split in ``profiles/``);
+  * ``cpu_baseline`` and ``parity`` (unless ``--no-cpu``): the repo's CPU
+    restatement of the reference path timed on a bounded sample of the row's
+    workload on this host's cores, and the device output on the same sample
+    judged against the oracle with the test suite's criteria
+    (``oracle.parity``).
+The top-level ``cpu_baseline`` is the headline row's.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-sweep] [--no-cpu]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-sweep]
+                       [--no-cpu] [--no-headline] [--only SUBSTRING]
 """
 
 from __future__ import annotations
@@ -39,6 +50,10 @@ MALL_BYTES = 256 * 1024 * 1024
 
 def _weight_bytes(module) -> int:
     return sum(t.numel() * t.element_size() for t in module.buffers(recurse=False))
+
+
+def _copies(module) -> int:
+    return min(64, max(1, math.ceil(1.25 * MALL_BYTES / max(1, _weight_bytes(module)))))
 
 
 def clock_warmup(seconds: float = 1.0) -> None:
@@ -82,41 +97,13 @@ def _timed_replays(graph, steps: int, repeats: int = 3, settle_s: float = 0.3) -
     return sorted(times)[len(times) // 2]
 
 
-def measure_headline_kernel(workload, steps: int) -> dict:
-    """Live per-launch time of the headline's dominant kernel (the W4A16
-    decode GEMV) alone: the act-order gather is done once up front and each
-    captured step is one kq_w4a16_tiled_gemm launch on the gathered fp16 x,
-    rotating over the same weight copies as the whole-op measurement."""
+def _graph_ms(launch, copies: int, steps: int, warmup: int = 0) -> float:
+    """ms per launch of `launch(i)` (i = step index, rotating over `copies`
+    operand sets), captured `steps` times in one graph."""
 
     import torch
 
-    from kairyu_amd import _native, workloads
-    from kairyu_amd.kernels import quant_gemm_hip as hip
-
-    module = workload.module
-    copies = max(1, math.ceil(1.25 * MALL_BYTES / max(1, _weight_bytes(module))))
-    copies = min(copies, 64)
-    mods = workloads.replicas(workload, copies)
-    device = workload.x.device
-    m, k = workload.x.shape
-    n, group = module.out_features, module.group_size
-    operands = [hip._gptq_operands(mod, device) for mod in mods]
-    mode, _, perm = operands[0]
-    x16 = workload.x[:, perm.long()].contiguous() if mode == hip.GIDX_PERMUTED else workload.x
-    out = torch.empty((m, n), device=device, dtype=torch.float16)
-    ws = _native.workspace(device)
-
-    def launch(i):
-        _, tiles, _ = operands[i % copies]
-        mod = mods[i % copies]
-        _native.call(
-            "kq_w4a16_tiled_gemm", x16.data_ptr(), _native.DTYPE_F16, tiles.data_ptr(),
-            mod.qzeros.data_ptr(), 1, mod.scales.data_ptr(), None, None, _native.DTYPE_NONE,
-            out.data_ptr(), m, n, k, group, ws.data_ptr(), ws.numel(),
-            _native.stream_handle(device),
-        )
-
-    for i in range(copies):
+    for i in range(max(warmup, copies)):
         launch(i)
     torch.cuda.synchronize()
     side = torch.cuda.Stream()
@@ -132,43 +119,300 @@ def measure_headline_kernel(workload, steps: int) -> dict:
             launch(i)
     ms = _timed_replays(graph, steps)
     del graph
-    # bytes one launch reads and writes: packed weights, zeros, scales, x16, out
-    groups = -(-k // group)
-    nbytes = k * n // 2 + groups * (n // 8) * 4 + groups * n * 2 + m * k * 2 + m * n * 2
-    return {"ms": ms, "bytes": nbytes, "gbps": nbytes / (ms * 1e-3) / 1e9}
+    return ms
 
 
 def measure(workload, steps: int, warmup: int) -> dict:
-    import torch
+    """Whole module call, weights rotating over distinct copies."""
 
     from kairyu_amd import workloads
 
-    copies = max(1, math.ceil(1.25 * MALL_BYTES / max(1, _weight_bytes(workload.module))))
-    copies = min(copies, 64)
+    copies = _copies(workload.module)
     mods = workloads.replicas(workload, copies)
     x = workload.x
-    for i in range(max(warmup, copies)):
-        mods[i % copies](x)
-    torch.cuda.synchronize()
-    side = torch.cuda.Stream()
-    side.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(side):
-        for i in range(copies):
-            mods[i](x)
-    torch.cuda.current_stream().wait_stream(side)
-    torch.cuda.synchronize()
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
-        for i in range(steps):
-            mods[i % copies](x)
-    ms = _timed_replays(graph, steps)
-    del graph
-    gbps = workload.bytes / (ms * 1e-3) / 1e9
-    tflops = workload.flops / (ms * 1e-3) / 1e12
-    return {"ms": ms, "gbps": gbps, "tflops": tflops, "copies": copies}
+    ms = _graph_ms(lambda i: mods[i % copies](x), copies, steps, warmup)
+    return {"ms": ms, "gbps": workload.bytes / (ms * 1e-3) / 1e9,
+            "tflops": workload.flops / (ms * 1e-3) / 1e12, "copies": copies}
 
 
-def sweep_entries(include_moe: bool = True):
+def gemm_launcher(workload, copies: int):
+    """(launch(i), algorithmic bytes, flops, kernel description) of the
+    workload's dominant GEMM entry alone, on pre-processed activations, or
+    None for workloads without a single dominant GEMM entry (MoE)."""
+
+    import torch
+
+    from kairyu_amd import _native, workloads
+    from kairyu_amd.kernels import quant_gemm_hip as hip
+    from kairyu_amd.quant.linear import AwqLinear, Fp8Linear, GptqLinear, Int8Linear
+
+    module, x = workload.module, workload.x
+    if not isinstance(module, (AwqLinear, GptqLinear, Fp8Linear, Int8Linear)):
+        return None
+    device = x.device
+    m, k = x.shape
+    n = module.out_features
+    mods = workloads.replicas(workload, copies)
+    if isinstance(module, (AwqLinear, GptqLinear)):
+        group = module.group_size
+        groups = -(-k // group)
+        if isinstance(module, GptqLinear):
+            ops = [hip._gptq_operands(mod, device) for mod in mods]
+            mode, _, perm = ops[0]
+            x16 = x[:, perm.long()].contiguous() if mode == hip.GIDX_PERMUTED else x
+            operands = [(t, mod.qzeros, 1, mod.scales) for mod, (_, t, _) in zip(mods, ops)]
+        else:
+            ops = [hip._awq_operands(mod, device) for mod in mods]
+            x16 = x
+            operands = [(t, z, 0, mod.scales) for mod, (t, z) in zip(mods, ops)]
+        out = torch.empty((m, n), device=device, dtype=x.dtype)
+        ws = _native.workspace(device, int(_native.library().kq_w4a16_workspace_size(m, n, k, 0)))
+
+        def launch(i):
+            tiles, zeros, zoff, scales = operands[i % copies]
+            _native.call("kq_w4a16_tiled_gemm", x16.data_ptr(), _native.dtype_code(x16.dtype),
+                         tiles.data_ptr(), zeros.data_ptr(), zoff, scales.data_ptr(), None, None,
+                         _native.DTYPE_NONE, out.data_ptr(), m, n, k, group, ws.data_ptr(), ws.numel(),
+                         _native.stream_handle(device))
+
+        nbytes = k * n // 2 + groups * (n // 8) * 4 + groups * n * 2 + m * k * 2 + m * n * 2
+        kernel = ("w4a16_gemv_kernel (M <= 16 decode GEMV)" if m <= 16
+                  else "w4a16_prefill_kernel (+ its fp16 staging pass)")
+        return launch, nbytes, 2 * m * n * k, kernel
+    fp8 = isinstance(module, Fp8Linear)
+    xq, xs = hip._quantize_activation(x, torch.float8_e4m3fn if fp8 else torch.int8,
+                                      448.0 if fp8 else 127.0)
+    wscales = [hip._f32(mod.weight_scale) for mod in mods]
+    out = torch.empty((m, n), device=device, dtype=x.dtype)
+    ws = _native.workspace(device, int(_native.library().kq_w8a8_workspace_size(m, n, k)))
+
+    def launch(i):
+        mod, wsc = mods[i % copies], wscales[i % copies]
+        if fp8:
+            _native.call("kq_w8a8_fp8_gemm", xq.data_ptr(), xs.data_ptr(), mod.weight.data_ptr(),
+                         wsc.data_ptr(), int(wsc.numel() != 1), None, _native.DTYPE_NONE,
+                         out.data_ptr(), _native.dtype_code(x.dtype), m, n, k, ws.data_ptr(),
+                         ws.numel(), _native.stream_handle(device))
+        else:
+            _native.call("kq_w8a8_i8_gemm", xq.data_ptr(), xs.data_ptr(), mod.weight.data_ptr(),
+                         wsc.data_ptr(), None, _native.DTYPE_NONE, out.data_ptr(),
+                         _native.dtype_code(x.dtype), None, m, n, k, ws.data_ptr(), ws.numel(),
+                         _native.stream_handle(device))
+
+    nbytes = n * k + 4 * n + m * k + 4 * m + 2 * m * n
+    kernel = ("w8a8_decode_kernel" if m <= 16 else "tile_gemm_kernel (+ split-K reduce when used)")
+    return launch, nbytes, 2 * m * n * k, kernel
+
+
+def measure_gemm(workload, steps: int, dtype: str) -> dict | None:
+    copies = _copies(workload.module)
+    spec = gemm_launcher(workload, copies)
+    if spec is None:
+        return None
+    launch, nbytes, flops, kernel = spec
+    ms = _graph_ms(launch, copies, steps)
+    gbps = nbytes / (ms * 1e-3) / 1e9
+    tflops = flops / (ms * 1e-3) / 1e12
+    hbm = workload.bound == "hbm"
+    achieved = gbps if hbm else tflops
+    peak = HBM_PEAK_GBS if hbm else MFMA_PEAK_TFLOPS[dtype]
+    return {"kernel": kernel, "us": round(ms * 1e3, 3), "bytes_per_launch": nbytes,
+            "flops_per_launch": flops, "bound": workload.bound, "achieved": round(achieved, 1),
+            "unit": "GB/s" if hbm else "TFLOP/s", "peak": peak, "frac": round(achieved / peak, 4)}
+
+
+# ------------------------------------------------------------ CPU baselines
+def _blas_threads() -> int:
+    from threadpoolctl import threadpool_info
+
+    return int(max((p.get("num_threads", 1) for p in threadpool_info()), default=1))
+
+
+def _median_time(fn, target_s: float, max_runs: int = 20) -> tuple[float, int]:
+    fn()  # warm up
+    times = []
+    deadline = time.perf_counter() + target_s
+    while len(times) < 3 or (time.perf_counter() < deadline and len(times) < max_runs):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return float(sorted(times)[len(times) // 2]), len(times)
+
+
+def _np(t):
+    import torch
+
+    return t.detach().to("cpu", torch.float32).numpy()
+
+
+def _bits_np(t):
+    import torch
+
+    return t.detach().cpu().contiguous().view(torch.uint8).numpy()
+
+
+def cpu_row(name: str, workload, gpu_out, target_s: float = 2.0) -> tuple[dict, dict]:
+    """(cpu_baseline, parity) of one sweep row: the oracle's port of the
+    reference CPU path timed on a bounded sample of the row's workload, and
+    the device output judged on a sample against the oracle's exact path."""
+
+    import numpy as np
+
+    from kairyu_amd.quant.linear import AwqLinear, Fp8Linear, GptqLinear, Int8Linear
+    from oracle import linear as olinear
+    from oracle import moe as omoe
+    from oracle import parity
+    from oracle.numerics import e4m3_decode
+
+    module, x = workload.module, workload.x
+    m, k = x.shape
+    out_np = _np(gpu_out)
+    cores = _blas_threads()
+    dt = {"torch.float16": "float16", "torch.bfloat16": "bfloat16"}[str(x.dtype)]
+    if isinstance(module, (AwqLinear, GptqLinear)):
+        n = module.out_features
+        cols = min(n, 7168)
+        xs = _np(x)
+        qw, qz, sc = module.qweight.cpu().numpy(), module.qzeros.cpu().numpy(), _np(module.scales)
+        groups = sc.shape[0]
+        if isinstance(module, GptqLinear):
+            gi = module.g_idx.cpu().numpy()
+            run = (lambda: olinear.gptq_forward_fast(xs, qw[:, :cols], qz[:, :cols // 8], sc[:, :cols], gi, dt))
+            ref = (lambda c0, c1: olinear.gptq_reference(xs, qw[:, c0:c1], qz[:, c0 // 8:c1 // 8],
+                                                         sc[:, c0:c1], gi, dt))
+        else:
+            g = module.group_size
+            run = (lambda: olinear.awq_forward_fast(xs, qw[:, :cols // 8], qz[:, :cols // 8], sc[:, :cols], g, dt))
+            ref = (lambda c0, c1: olinear.awq_reference(xs, qw[:, c0 // 8:c1 // 8], qz[:, c0 // 8:c1 // 8],
+                                                        sc[:, c0:c1], g, dt))
+        med, runs = _median_time(run, target_s)
+        scale = n / cols
+        nbytes = workload.bytes
+        value = nbytes / (med * scale) / 1e9
+        cpu = {"value": round(value, 3), "unit": "GB/s", "cores": cores, "kind": "port",
+               "sample": (f"oracle.linear.{'gptq' if isinstance(module, GptqLinear) else 'awq'}_forward_fast "
+                          f"(numpy dequantize -> fp16 weight -> fp32 BLAS) on M={m} K={k} N={cols} of {n}, "
+                          f"median of {runs} runs = {med * 1e3:.1f} ms, scaled by N; {groups} groups")}
+        checks = []
+        for c0 in sorted({0, (n // 2 - 256) // 8 * 8, n - 512}):
+            pre, terms = ref(c0, c0 + 512)
+            checks.append(parity.ulp_check(out_np[:, c0:c0 + 512], pre, dt,
+                                           parity.fp16_mfma_slack(terms, k)))
+        par = _summarize(checks, f"columns 0:512, middle 512, last 512 of all {m} rows")
+        return cpu, par
+    if isinstance(module, (Fp8Linear, Int8Linear)):
+        n = module.out_features
+        rows = np.arange(m) if m <= 32 else np.unique(np.r_[0:16, m - 16:m])
+        xs = _np(x)[rows]
+        w_np = module.weight.cpu()
+        wscale = _np(module.weight_scale)
+        if isinstance(module, Fp8Linear):
+            from oracle import formats
+
+            wb = _bits_np(w_np)
+            t0 = time.perf_counter()
+            wdec = e4m3_decode(wb)
+            decode_s = time.perf_counter() - t0
+            xb, xsc = formats.fp8_quantize_rows(xs)
+            med, runs = _median_time(lambda: olinear.fp8_forward_fast(xb, xsc, wdec, wscale), target_s)
+            total = decode_s + med * (m / len(rows))
+            cpu = {"value": round(workload.flops / total / 1e12, 4) if m > 64 else
+                   round(workload.bytes / total / 1e9, 3),
+                   "unit": "TFLOP/s" if m > 64 else "GB/s", "cores": cores, "kind": "port",
+                   "sample": (f"oracle.linear.fp8_forward_fast (fp32 BLAS of decoded e4m3) on {len(rows)} of "
+                              f"{m} rows ({med * 1e3:.1f} ms, median of {runs}) + the weight decode "
+                              f"({decode_s * 1e3:.0f} ms), extrapolated linearly in rows")}
+            _, x_bits, x_scale, pre = olinear.fp8_forward(xs, wb, wscale)
+            terms = olinear.fp8_abs_terms(x_bits, wb, x_scale, wscale)
+            wsv = np.abs(wscale.astype(np.float64)).reshape(-1, 1)
+            slack = parity.e4m3_mfma_slack(terms, k, np.abs(e4m3_decode(x_bits)) * x_scale,
+                                           np.abs(wdec) * wsv)
+            par = _summarize([parity.ulp_check(out_np[rows], pre, dt, slack)],
+                             f"{len(rows)} rows (first and last 16) x all {n} columns")
+            return cpu, par
+        wq = w_np.numpy()
+        run = lambda: olinear.int8_forward(xs, wq, wscale, None, out_dtype=dt)  # noqa: E731
+        med, runs = _median_time(run, target_s, max_runs=5)
+        total = med * (m / len(rows))
+        cpu = {"value": round(workload.flops / total / 1e12, 4) if m > 64 else
+               round(workload.bytes / total / 1e9, 3),
+               "unit": "TOP/s" if m > 64 else "GB/s", "cores": cores, "kind": "port",
+               "sample": (f"oracle.linear.int8_forward (exact int32 accumulation through fp64 BLAS) "
+                          f"on {len(rows)} of {m} rows, median of {runs} = {med * 1e3:.1f} ms, "
+                          f"extrapolated linearly in rows")}
+        expected, *_ = run()
+        same = bool(np.array_equal(out_np[rows].view(np.uint32), expected.astype(np.float32).view(np.uint32)))
+        par = {"verdict": "pass" if same else "FAIL", "criterion": "bf16 output bit-exact",
+               "sample": f"{len(rows)} rows x all {n} columns"}
+        return cpu, par
+    # MoE: the per-expert loop on a token sample (one timed run: the loop's
+    # per-expert weight decode dominates and the result is deterministic)
+    tokens = 16
+    sel = np.random.default_rng(0).choice(m, size=tokens, replace=False)
+    from kairyu_amd import moe as hmoe
+
+    idx, w = hmoe.route_logits(module.logits, module.top_k, module.norm_topk_prob)
+    args = (_np(x)[sel], idx.cpu().numpy()[sel], w.cpu().numpy()[sel], _bits_np(module.w13),
+            module.s13.cpu().numpy(), _bits_np(module.w2), module.s2.cpu().numpy(), dt)
+    t0 = time.perf_counter()
+    expected = omoe.moe_forward(*args)
+    elapsed = time.perf_counter() - t0
+    total = elapsed * m / tokens
+    cpu = {"value": round(workload.bytes / total / 1e9, 4), "unit": "GB/s", "cores": cores, "kind": "port",
+           "sample": (f"oracle.moe.moe_forward (per-expert loop, fp64 block sums) on {tokens} of {m} tokens "
+                      f"({elapsed:.1f} s, one run), extrapolated linearly in tokens")}
+    check = parity.moe_check(out_np[sel], expected, dt)
+    par = _summarize([check], f"{tokens} tokens x all {x.shape[1]} outputs", moe=True)
+    return cpu, par
+
+
+def _summarize(checks, sample: str, moe: bool = False) -> dict:
+    ok = all(c["ok"] for c in checks)
+    out = {"verdict": "pass" if ok else "FAIL",
+           "criterion": ("statistical (oracle.parity.moe_check)" if moe else
+                         "per-element ulp + MFMA slack, rel-RMSE (oracle.parity.ulp_check)"),
+           "sample": sample,
+           "normwise_max": max(c.get("normwise_max", 0.0) for c in checks),
+           "rel_rmse": max(c.get("rel_rmse", 0.0) for c in checks)}
+    if not moe:
+        out["max_ulp"] = round(max(c.get("max_ulp", 0.0) for c in checks), 3)
+    if not ok:
+        out["why"] = "; ".join(c.get("why", "") for c in checks if not c["ok"])
+    return out
+
+
+def cpu_baseline(target_seconds: float = 12.0) -> dict:
+    """Time the oracle's GPTQ act-order forward on a column slice of the
+    headline workload (M=16, K=4096, N=7168 of 28672) on this host."""
+
+    import numpy as np
+
+    from oracle import formats
+    from oracle import linear as olinear
+
+    rng = np.random.default_rng(0)
+    m, k, n, group = 16, 4096, 7168, 128
+    q = rng.integers(0, 16, size=(k, n))
+    qweight = formats.gptq_pack_rows(q)
+    qzeros = formats.gptq_pack_cols(np.full((k // group, n), 7))
+    scales = rng.uniform(0.001, 0.01, size=(k // group, n)).astype(np.float16)
+    g_idx = (rng.permutation(k) // group).astype(np.int32)
+    x = rng.standard_normal((m, k)).astype(np.float16)
+    nbytes = k * n // 2 + (k // group) * (n // 8) * 4 + (k // group) * n * 2 + 4 * k + m * k * 2 + m * n * 2
+    med, runs = _median_time(lambda: olinear.gptq_forward_fast(x, qweight, qzeros, scales, g_idx, "float16"),
+                             target_seconds, max_runs=50)
+    return {
+        "value": round(nbytes / med / 1e9, 3),
+        "unit": "GB/s",
+        "cores": _blas_threads(),
+        "kind": "port",
+        "sample": (f"oracle.linear.gptq_forward_fast (numpy dequantize -> fp16 weight -> fp32 BLAS "
+                   f"matmul) on M=16 K=4096 N=7168 (1/4 of C2's columns), median of {runs} "
+                   f"runs = {med * 1e3:.1f} ms; host os.cpu_count()={os.cpu_count()}"),
+    }
+
+
+def sweep_entries():
     from kairyu_amd import workloads as W
 
     entries = [("C1 AWQ W4A16 N=K=4096 g128", "fp16", lambda: W.awq_layer(m=16))]
@@ -179,15 +423,7 @@ def sweep_entries(include_moe: bool = True):
         entries.append((f"C3 FP8 W8A8 N=4096 K=14336 M={m}", "fp8", lambda m=m: W.fp8_layer(m=m)))
     for m in (16, 4096):
         entries.append((f"C4 INT8 W8A8 N=18944 K=3584 M={m}", "int8", lambda m=m: W.int8_layer(m=m)))
-    if include_moe:
-        try:
-            from kairyu_amd import moe  # noqa: F401
-
-            if hasattr(W, "moe_layer"):
-                entries.append(("C5 block-FP8 MoE E=128 H=2048 I=768 T=4096 top8", "fp8",
-                                lambda: W.moe_layer()))
-        except ImportError:
-            pass
+    entries.append(("C5 block-FP8 MoE E=128 H=2048 I=768 T=4096 top8", "fp8", lambda: W.moe_layer()))
     return entries
 
 
@@ -210,47 +446,6 @@ def summarize(name: str, dtype: str, workload, result: dict) -> dict:
     }
 
 
-def cpu_baseline(target_seconds: float = 12.0) -> dict:
-    """Time the oracle's GPTQ act-order forward on a column slice of the
-    headline workload (M=16, K=4096, N=7168 of 28672) on this host."""
-
-    import numpy as np
-    from threadpoolctl import threadpool_info
-
-    from oracle import formats
-    from oracle import linear as olinear
-
-    rng = np.random.default_rng(0)
-    m, k, n, group = 16, 4096, 7168, 128
-    q = rng.integers(0, 16, size=(k, n))
-    qweight = formats.gptq_pack_rows(q)
-    qzeros = formats.gptq_pack_cols(np.full((k // group, n), 7))
-    scales = rng.uniform(0.001, 0.01, size=(k // group, n)).astype(np.float16)
-    g_idx = (rng.permutation(k) // group).astype(np.int32)
-    x = rng.standard_normal((m, k)).astype(np.float16)
-    nbytes = k * n // 2 + (k // group) * (n // 8) * 4 + (k // group) * n * 2 + 4 * k + m * k * 2 + m * n * 2
-    olinear.gptq_forward_fast(x, qweight, qzeros, scales, g_idx, "float16")  # warm up
-    times = []
-    deadline = time.perf_counter() + target_seconds
-    while time.perf_counter() < deadline or len(times) < 3:
-        t0 = time.perf_counter()
-        olinear.gptq_forward_fast(x, qweight, qzeros, scales, g_idx, "float16")
-        times.append(time.perf_counter() - t0)
-        if len(times) >= 50:
-            break
-    med = float(np.median(times))
-    blas_threads = max((p.get("num_threads", 1) for p in threadpool_info()), default=1)
-    return {
-        "value": round(nbytes / med / 1e9, 3),
-        "unit": "GB/s",
-        "cores": int(blas_threads),
-        "kind": "port",
-        "sample": (f"oracle.linear.gptq_forward_fast (numpy dequantize -> fp16 weight -> fp32 BLAS "
-                   f"matmul) on M=16 K=4096 N=7168 (1/4 of C2's columns), median of {len(times)} "
-                   f"runs = {med * 1e3:.1f} ms; host os.cpu_count()={os.cpu_count()}"),
-    }
-
-
 def main() -> int:
     parser = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     parser.add_argument("--gpus", type=int, default=1)
@@ -258,6 +453,8 @@ def main() -> int:
     parser.add_argument("--warmup", type=int, default=20)
     parser.add_argument("--no-sweep", action="store_true")
     parser.add_argument("--no-cpu", action="store_true")
+    parser.add_argument("--no-headline", action="store_true",
+                        help="skip the headline measurement (profiling one sweep row)")
     parser.add_argument("--only", default=None, help="substring filter for sweep entries")
     parser.add_argument("--copy-calibration", action="store_true",
                         help="only run 256 MiB device-to-device copies (HBM counter calibration)")
@@ -285,16 +482,18 @@ def main() -> int:
         return 0
 
     clock_warmup()
-    headline_wl = W.gptq_layer(m=16)
-    print(f"[bench] headline {headline_wl.name}", file=sys.stderr, flush=True)
-    head = measure(headline_wl, args.steps, args.warmup)
-    head_summary = summarize("C2 GPTQ act-order W4A16 N=28672 K=4096 g128 M=16", "fp16",
-                             headline_wl, head)
-    kernel = measure_headline_kernel(headline_wl, args.steps)
-    print(f"[bench] headline {head['ms'] * 1e3:.2f} us per op, decode GEMV "
-          f"{kernel['ms'] * 1e3:.2f} us per launch", file=sys.stderr, flush=True)
-    del headline_wl
-    torch.cuda.empty_cache()
+    head = kernel = head_summary = None
+    if not args.no_headline:
+        headline_wl = W.gptq_layer(m=16)
+        print(f"[bench] headline {headline_wl.name}", file=sys.stderr, flush=True)
+        head = measure(headline_wl, args.steps, args.warmup)
+        head_summary = summarize("C2 GPTQ act-order W4A16 N=28672 K=4096 g128 M=16", "fp16",
+                                 headline_wl, head)
+        kernel = measure_gemm(headline_wl, args.steps, "fp16")
+        print(f"[bench] headline {head['ms'] * 1e3:.2f} us per op, decode GEMV "
+              f"{kernel['us']:.2f} us per launch", file=sys.stderr, flush=True)
+        del headline_wl
+        torch.cuda.empty_cache()
 
     sweep = []
     if not args.no_sweep:
@@ -303,12 +502,25 @@ def main() -> int:
                 continue
             wl = builder()
             print(f"[bench] sweep {name}", file=sys.stderr, flush=True)
-            res = measure(wl, max(20, min(args.steps, 100)), min(args.warmup, 10))
-            sweep.append(summarize(name, dtype, wl, res))
-            print(f"[bench]   {sweep[-1]['us']} us  {sweep[-1]['gb_per_s']} GB/s  "
-                  f"{sweep[-1]['tflops']} TFLOPS", file=sys.stderr, flush=True)
+            row = summarize(name, dtype, wl, measure(wl, max(20, min(args.steps, 100)),
+                                                     min(args.warmup, 10)))
+            row["gemm"] = measure_gemm(wl, max(20, min(args.steps, 100)), dtype)
+            print(f"[bench]   op {row['us']} us  {row['gb_per_s']} GB/s  {row['tflops']} TFLOPS"
+                  + (f"; gemm {row['gemm']['us']} us {row['gemm']['achieved']} {row['gemm']['unit']}"
+                     if row["gemm"] else ""), file=sys.stderr, flush=True)
+            if not args.no_cpu:
+                out = wl.module(wl.x)
+                torch.cuda.synchronize()
+                row["cpu_baseline"], row["parity"] = cpu_row(name, wl, out)
+                print(f"[bench]   cpu {row['cpu_baseline']['value']} {row['cpu_baseline']['unit']}; "
+                      f"parity {row['parity']['verdict']}", file=sys.stderr, flush=True)
+            sweep.append(row)
             del wl
             torch.cuda.empty_cache()
+
+    if head is None:
+        print(json.dumps({"sweep": sweep}), flush=True)
+        return 0
 
     traffic = None
     traffic_file = ROOT / "profiles" / "traffic.json"
@@ -337,13 +549,13 @@ def main() -> int:
         "roofline": {
             "bound": "hbm",
             "kernel": "w4a16_gemv_kernel (kq_w4a16_tiled_gemm, M=16 decode GEMV)",
-            "achieved": round(kernel["gbps"], 1),
+            "achieved": kernel["achieved"],
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
-            "frac": round(kernel["gbps"] / HBM_PEAK_GBS, 4),
+            "frac": kernel["frac"],
             "traffic": traffic,
-            "bytes_per_launch": kernel["bytes"],
-            "us_per_launch": round(kernel["ms"] * 1e3, 3),
+            "bytes_per_launch": kernel["bytes_per_launch"],
+            "us_per_launch": kernel["us"],
         },
         "cpu_baseline": cpu,
         "sweep": sweep,

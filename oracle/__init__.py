@@ -21,6 +21,10 @@ Pinning (how each function is known to be right, see tests/test_oracle_*.py):
   linear.fp8_*                 e4m3 products exact in fp64 (closed form)
   moe.route_*                  reference fixtures (test_moe_precision.py:97-154)
   moe.combine_*                reference fixtures (test_moe_precision.py:138-154,194-226)
+  parity                       the device-output criteria (ulp bound with the
+                               measured MFMA accumulation slack, relative RMSE,
+                               the routed-expert statistics); pinned by planted
+                               mistakes in tests/test_parity_bounds.py
   moe block-FP8 expert math    parity unpinned at the reference boundary (no
                                reference implementation or test exists); the
                                pieces are pinned individually as above

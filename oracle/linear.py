@@ -151,3 +151,24 @@ def fp8_abs_terms(x_bits, w_bits, x_scale, w_scale) -> np.ndarray:
     ws = np.asarray(w_scale, np.float64).reshape(-1)
     ws = ws.reshape(1, -1) if ws.size > 1 else ws.reshape(1, 1)
     return acc * np.asarray(x_scale, np.float64).reshape(-1, 1) * ws
+
+
+def awq_forward_fast(x, qweight, qzeros, scales, group_size, x_dtype, bias=None) -> np.ndarray:
+    """AWQ counterpart of ``gptq_forward_fast`` (linear.py:401-404 order, fp32
+    BLAS matmul); the timed CPU baseline only."""
+
+    w = formats.w4a16_weight_fp16(formats.awq_dequantize(qweight, qzeros, scales, group_size))
+    a = w4a16_activation(x, x_dtype)
+    return to_dtype(_bias_add((a @ w.T).astype(np.float32), bias), x_dtype)
+
+
+def fp8_forward_fast(x_bits, x_scale, w_decoded, w_scale, out_dtype="bfloat16") -> np.ndarray:
+    """``fp8_w8a8_matmul`` (kairyu/quant/fp8.py:48-56) in the reference's op
+    order -- ``(x_q.f32 @ w_q.f32^T) * x_scale * w_scale`` with an fp32 BLAS
+    matmul -- on already quantized rows and an already decoded weight
+    (``e4m3_decode``); the timed CPU baseline only (parity uses the exact
+    ``fp8_forward``)."""
+
+    acc = e4m3_decode(x_bits) @ np.asarray(w_decoded, np.float32).T
+    ws = np.asarray(w_scale, np.float32).reshape(1, -1)
+    return to_dtype(((acc * x_scale).astype(np.float32) * ws).astype(np.float32), out_dtype)

@@ -1,0 +1,158 @@
+"""Parity criteria of the device outputs -- TEST INFRASTRUCTURE ONLY.
+
+Used by ``tests/`` and by ``bench.py``'s ``cpu_baseline`` leg to judge a
+device output against the oracle's value; nothing in the ``kairyu_amd``
+package imports it.
+
+Floating-point outputs are checked per element against the oracle's value
+before its final cast (``pre``, accumulated exactly or in fp64):
+
+    |out - pre| <= ulps * ulp_dtype(max(|out|, |pre|)) + slack + 4 * 2^-24 * |pre|
+
+where the final ulp covers the device's last rounding (half an ulp) plus the
+part of its accumulation error that moves the value across a rounding
+boundary, ``4 * 2^-24 * |pre|`` the epilogue's fp32 roundings, and ``slack``
+the accumulation error of the device's matrix instructions:
+
+* fp16 MFMA (W4A16): ``sqrt(K) * 2^-24 * sum_k |a_k w_k|``, fp32 round-off on
+  the sum of absolute terms (the f16 MFMA keeps products down to about 2^-24 of
+  the largest product of its group of 8, measured on gfx950);
+* e4m3 MFMA (FP8, block FP8): ``2 * (sqrt(K) * 2^-24 * sum_k |a_k w_k| +
+  2^-13 * sqrt(7 * sum_g (max_g |a| * max_g |w|)^2))`` in output units.  The
+  gfx950 e4m3 MFMA sums each group of 8 products in a window of 13 bits below
+  the group's largest product (measured: a product 2^14 below it is dropped);
+  the second term is that window's error at a few standard deviations over
+  the K/8 groups, with the group maximum bounded by max|a| * max|w|.
+
+A dropped or doubled K term (on average ``sum|terms| / K``) exceeds the slack
+on most outputs at the test shapes (tests/test_parity_bounds.py plants such
+mistakes in the oracle); at the largest K the relative RMSE check catches it
+as well: every check also requires the relative RMSE of ``out - pre`` to stay
+within 1.5x of the RMSE of rounding ``pre`` to the output dtype (a dropped
+term adds about ``1/sqrt(K)``).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+from .linear import error_metrics
+
+U32 = 2.0 ** -24
+_MANTISSA = {"float16": 10, "bfloat16": 7, "float32": 23}
+_EMIN = {"float16": -14, "bfloat16": -126, "float32": -126}
+
+
+def ulp(values, dtype: str) -> np.ndarray:
+    """Spacing of ``dtype`` numbers at |values| (subnormal spacing below the
+    smallest normal)."""
+
+    a = np.abs(np.asarray(values, np.float64))
+    with np.errstate(divide="ignore"):
+        e = np.floor(np.log2(np.where(a > 0, a, 1.0)))
+    e = np.maximum(np.where(a > 0, e, _EMIN[dtype]), _EMIN[dtype])
+    return np.ldexp(1.0, (e - _MANTISSA[dtype]).astype(np.int64))
+
+
+def rounding_rel_rmse(pre, dtype: str) -> float:
+    """Relative RMSE that rounding ``pre`` to ``dtype`` alone produces
+    (uniform error in half an ulp either side: ulp / sqrt(12))."""
+
+    ref = np.asarray(pre, np.float64)
+    rms = float(np.sqrt(np.mean(ref * ref))) if ref.size else 0.0
+    if rms == 0.0:
+        return 0.0
+    return float(np.sqrt(np.mean(ulp(ref, dtype) ** 2) / 12.0)) / rms
+
+
+def fp16_mfma_slack(abs_terms, k: int):
+    """Accumulation slack of the fp16 MFMA path (module docstring)."""
+
+    return np.sqrt(max(k, 1)) * U32 * np.asarray(abs_terms, np.float64)
+
+
+def e4m3_mfma_slack(abs_terms, k: int, x_mag, w_mag):
+    """Accumulation slack of the e4m3 MFMA path (module docstring).
+    ``abs_terms``: sum_k |a_k w_k| in output units; ``x_mag`` [M, K] and
+    ``w_mag`` [N, K]: |a| and |w| with their scales applied, so that
+    ``x_mag @ w_mag.T`` is in output units too."""
+
+    xm = np.asarray(x_mag, np.float64)
+    wm = np.asarray(w_mag, np.float64)
+    kk = xm.shape[1]
+    pad = (-kk) % 8
+    if pad:
+        xm = np.pad(xm, ((0, 0), (0, pad)))
+        wm = np.pad(wm, ((0, 0), (0, pad)))
+    gx = xm.reshape(xm.shape[0], -1, 8).max(axis=2)
+    gw = wm.reshape(wm.shape[0], -1, 8).max(axis=2)
+    window = 2.0 ** -13 * np.sqrt(7.0 * ((gx * gx) @ (gw * gw).T))
+    return 2.0 * (np.sqrt(max(k, 1)) * U32 * np.asarray(abs_terms, np.float64) + window)
+
+
+def ulp_check(actual, pre, dtype: str, slack, ulps: float = 1.0, rmse_factor: float = 1.5) -> dict:
+    """Per-element bound of the module docstring plus the relative-RMSE check.
+    Returns metrics with ``ok`` and, when not ok, ``why``."""
+
+    out = np.asarray(actual, np.float64)
+    ref = np.asarray(pre, np.float64)
+    if out.shape != ref.shape:
+        return {"ok": False, "why": f"shape {out.shape} != {ref.shape}"}
+    finite = np.isfinite(ref)
+    if not np.array_equal(np.isfinite(out), finite):
+        return {"ok": False, "why": "non-finite pattern differs"}
+    out, ref = out[finite], ref[finite]
+    slack = np.broadcast_to(np.asarray(slack, np.float64), finite.shape)[finite]
+    diff = np.abs(out - ref)
+    unit = ulp(np.maximum(np.abs(out), np.abs(ref)), dtype)
+    bound = ulps * unit + slack + 4 * U32 * np.abs(ref)
+    ratio = diff / ulp(ref, dtype)
+    edges = [0.0, 0.25, 0.5, 0.75, 1.0, 1.5, 2.0, np.inf]
+    metrics = error_metrics(out, ref) if out.size else {"rel_rmse": 0.0}
+    rounding = rounding_rel_rmse(ref, dtype)
+    metrics.update({
+        "ulp_bins": edges[1:-1],
+        "ulp_hist": np.histogram(ratio, bins=edges)[0].tolist() if ratio.size else [],
+        "max_ulp": float(ratio.max()) if ratio.size else 0.0,
+        "rounding_rel_rmse": rounding,
+        "outside": int((diff > bound).sum()),
+        "count": int(diff.size),
+        "ok": True,
+    })
+    if metrics["outside"]:
+        i = int(np.argmax(diff - bound))
+        metrics["ok"] = False
+        metrics["why"] = (f"{metrics['outside']} of {diff.size} outputs outside {ulps} ulp + "
+                          f"accumulation slack; worst out={out[i]!r} pre={ref[i]!r} bound={bound[i]!r}")
+    elif metrics["rel_rmse"] > rmse_factor * rounding + 1e-7:
+        metrics["ok"] = False
+        metrics["why"] = (f"relative RMSE {metrics['rel_rmse']:.3e} above {rmse_factor} x the "
+                          f"rounding RMSE {rounding:.3e}")
+    return metrics
+
+
+def moe_check(actual, expected, dtype: str, ulps: float = 8.0, frac: float = 0.95,
+              rel_rmse: float = 5e-3) -> dict:
+    """Routed-expert outputs against the oracle's rounded result.
+
+    The expert path rounds inside (gate/up to the activation dtype, the
+    SwiGLU product re-quantized to e4m3 per 128-wide block), and its e4m3
+    MFMAs sum in a 13-bit window, so an accumulation difference can move an
+    intermediate across a rounding boundary and shift a whole token row by a
+    few output ulps; no per-element bound holds for every element.  Required
+    instead: at least ``frac`` of the outputs within ``ulps`` ulp, and the
+    relative RMSE within ``rel_rmse`` (a dropped K term of a 2048-wide
+    gate/up or 768-wide down reduction moves it to 2-4e-2; measured on
+    gfx950 at the test shapes: 0.975-0.997 within 8 ulp, 0.6-2.2e-3)."""
+
+    out = np.asarray(actual, np.float64)
+    ref = np.asarray(expected, np.float64)
+    ratio = np.abs(out - ref) / ulp(ref, dtype)
+    edges = [0.0, 0.5, 1.0, 2.0, 4.0, 8.0, np.inf]
+    metrics = error_metrics(out, ref)
+    within = float(np.mean(ratio <= ulps))
+    metrics.update({"ulp_bins": edges[1:-1], "ulp_hist": np.histogram(ratio, bins=edges)[0].tolist(),
+                    "within": within, "ok": within >= frac and metrics["rel_rmse"] <= rel_rmse})
+    if not metrics["ok"]:
+        metrics["why"] = f"{within:.4f} within {ulps} ulp (need {frac}), rel_rmse {metrics['rel_rmse']:.3e}"
+    return metrics
