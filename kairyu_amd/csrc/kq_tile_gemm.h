@@ -105,13 +105,15 @@ KQ_DEV int tg_chunk(int r, int c) {
   else return c ^ ((r >> 1) & 7);
 }
 
+// Global -> LDS copies of 16 / 4 bytes per lane (buffer_load ... lds): lane i
+// of the wave writes at LDS byte address lds + i * size; `lds` is wave-uniform
+// (the compiler places it in m0).
+typedef __attribute__((address_space(3))) void* tg_lds_ptr;
 KQ_DEV void tg_dma16(i32x4 rsrc, uint32_t lds, int32_t voff, int32_t soff) {
-  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
-               ::"s"(lds), "v"(voff), "s"(rsrc), "s"(soff) : "memory", "m0");
+  kq_rbl_lds(rsrc, (tg_lds_ptr)(uintptr_t)lds, 16, voff, soff, 0, 0);
 }
 KQ_DEV void tg_dma4(i32x4 rsrc, uint32_t lds, int32_t voff, int32_t soff) {
-  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, %3 offen lds"
-               ::"s"(lds), "v"(voff), "s"(rsrc), "s"(soff) : "memory", "m0");
+  kq_rbl_lds(rsrc, (tg_lds_ptr)(uintptr_t)lds, 4, voff, soff, 0, 0);
 }
 
 KQ_DEV float tg_round_act(float v, int dtype) {
