@@ -151,15 +151,19 @@ int kq_w4a16_gptq_gemm(const void* x, int x_dtype, const int32_t* qweight,
                        int group_size, void* workspace, size_t workspace_bytes,
                        void* stream);
 
-/* Load-time tiling of a W4A16 weight for the tiled kernels: tiles int32
- * [ceil(n/16)][k/8][16], word (u, r, c) holding q[row(8r + e)][16u + c] in
- * nibble e, row(k) = perm[k] when perm is given (GPTQ act-order: the stable
- * argsort of g_idx, so permuted row j has group j / group_size), else k;
- * columns past n are 0.  src_format 0: AWQ qweight [k, n/8]; 1: GPTQ qweight
- * [k/8, n].  Derived operand only; checkpoint buffers are untouched (the
- * reference caches derived runtime operands the same way,
- * quant_gemm_gpu.py:802-850; formats kairyu/quant/awq.py:14-36,
- * kairyu/quant/gptq.py:15-46). */
+/* Load-time tiling of a W4A16 weight for the tiled kernels: int32 words
+ * [ceil(n/16)][ceil(k/128) * 16][16] holding 16-column tiles of 128-k stages.
+ * The word of packed row r (k = 8r .. 8r+7) and column 16u + c holds
+ * q[row(8r + e)][16u + c] in nibble e; within tile u's stage t = r / 16 it
+ * sits at word (u * ceil(k/128) + t) * 256 + (kb * 16 + c) * 4 + s for
+ * r % 16 = 4s + kb, so the 4 words a lane (c, kb) of a 16x16x32 MFMA operand
+ * needs for a stage are 16 contiguous bytes.  row(k) = perm[k] when perm is
+ * given (GPTQ act-order: the stable argsort of g_idx, so permuted row j has
+ * group j / group_size), else k; rows past k/8 and columns past n are 0.
+ * src_format 0: AWQ qweight [k, n/8]; 1: GPTQ qweight [k/8, n].  Derived
+ * operand only; checkpoint buffers are untouched (the reference caches derived
+ * runtime operands the same way, quant_gemm_gpu.py:802-850; formats
+ * kairyu/quant/awq.py:14-36, kairyu/quant/gptq.py:15-46). */
 int kq_w4a16_tile_weights(const int32_t* qweight, int src_format, const int32_t* perm,
                           int32_t* tiles, int64_t n, int64_t k, void* stream);
 

@@ -24,6 +24,7 @@ typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef int i32x8 __attribute__((ext_vector_type(8)));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+typedef int i32x2 __attribute__((ext_vector_type(2)));
 
 namespace kq {
 
@@ -158,6 +159,8 @@ __device__ short kq_rbl_i16(i32x4 rsrc, int32_t voff, int32_t soff, int32_t aux)
     __asm("llvm.amdgcn.raw.buffer.load.i16");
 __device__ i32x4 kq_rbl_v4i32(i32x4 rsrc, int32_t voff, int32_t soff, int32_t aux)
     __asm("llvm.amdgcn.raw.buffer.load.v4i32");
+__device__ i32x2 kq_rbl_v2i32(i32x4 rsrc, int32_t voff, int32_t soff, int32_t aux)
+    __asm("llvm.amdgcn.raw.buffer.load.v2i32");
 // Global -> LDS without registers: lane i writes `size` (4, 12 or 16) bytes at
 // lds + i * size (lds wave-uniform); counts on vmcnt like any buffer load.
 __device__ void kq_rbl_lds(i32x4 rsrc, __attribute__((address_space(3))) void* lds, int32_t size,

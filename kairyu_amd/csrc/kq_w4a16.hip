@@ -57,6 +57,17 @@ enum { kLayoutRows = 0, kLayoutTiles = 1 };
 
 constexpr int kW4Cols = 64;   // columns per workgroup tile
 
+// Load-time tile layout of the W4A16 weights ("tiles"): 16-column tiles of
+// 128-k stages.  Within a tile's stage (16 packed rows of 8 k x 16 columns =
+// 1 KB), word (row 4s + kb, column c) sits at (kb * 16 + c) * 4 + s: the four
+// steps (32 k each) a lane (c, kb) of a 16x16x32 MFMA B operand consumes are
+// one contiguous 16 bytes.  Tile u, stage t starts at word (u * T + t) * 256
+// with T = ceil(K / 128) stages (rows past K / 8 are zero).
+__host__ __device__ inline int w4_stages(int K) { return (K + 127) / 128; }
+__host__ __device__ inline int64_t w4_tile_words(int N, int K) {
+  return (int64_t)((N + 15) / 16) * w4_stages(K) * 256;
+}
+
 struct W4Args {
   const uint16_t* x;     // activation rows (fp16 or bf16 per kernel template)
   int ldx;
@@ -182,7 +193,7 @@ struct NibbleConsts {
 // valid addresses and the surplus results are never stored).  PRED = true
 // guards every load (K tails, unaligned x).  U = steps per register batch
 // (two batches in flight), NT = weights streamed with non-temporal loads.
-template <int FMT, int MT, int GM, int XDT, bool PRED, int WAVES, int U, bool NT, bool TILED = false>
+template <int FMT, int MT, int GM, int XDT, bool PRED, int WAVES, int U, bool NT>
 __global__ void __launch_bounds__(64 * WAVES)
 w4a16_skinny_kernel(W4Args a) {
   __shared__ float red[(WAVES - 1) * MT * 16 * 64];
@@ -214,9 +225,12 @@ w4a16_skinny_kernel(W4Args a) {
   nc.c0 = 0x64006400u + (uint32_t)(lane & 0);  // keep the magics in VGPRs
   nc.c1 = 0x54005400u + (uint32_t)(lane & 0);
 
-  // loop-invariant 32-bit byte offsets of this lane
-  const uint32_t w_boff = (FMT == kGptq && a.layout == kLayoutTiles)
-                             ? (uint32_t)(((lcol_c >> 4) * (a.K / 8) + kb) * 64 + (lcol_c & 15) * 4)
+  // loop-invariant 32-bit byte offsets of this lane; tiles: the word of
+  // column lcol_c at stage 0, step 0 (column lcol_c + i is 16 bytes further,
+  // step s of stage t (t * 1024 + s * 4) bytes)
+  const bool tiles = FMT == kGptq && a.layout == kLayoutTiles;
+  const uint32_t w_boff = tiles
+                             ? (uint32_t)(((lcol_c >> 4) * w4_stages(a.K) * 64 + kb * 16 + (lcol_c & 15)) * 16)
                          : FMT == kGptq ? (uint32_t)(kb * a.N + lcol_c) * 4u
                                        : (uint32_t)(8 * kb * n8 + zword) * 4u;
   const uint32_t s_boff = (uint32_t)lcol_c * 2u;
@@ -237,23 +251,29 @@ w4a16_skinny_kernel(W4Args a) {
     else return group_of(a, PRED ? min(k, a.K - 1) : k);
   };
 
-  auto load_step = [&](W4Batch<FMT, MT, U>& b, int u, int st) {
+  auto load_weights_step = [&](W4Batch<FMT, MT, U>& b, int u, int st) {
     const int k = st * 32 + 8 * kb;
     const bool ok = !PRED || (k < a.K && col_ok);
-    if constexpr (FMT == kGptq && TILED) {
-      // tile-contiguous layout: [N/64][K/8][64] words
-      const uint32_t* base = a.qw + ((int64_t)tile * (a.K / 8) + (int64_t)st * 4) * 64;
-      b.wq[u] = ldw<u32x4, NT>(base, (uint32_t)(kb * 64 + 4 * j) * 4u);
-    } else if constexpr (FMT == kGptq) {
-      // rows: word row st*4 + kb starts at (st*4)*N; tiles: at (st*4)*16
-      const uint32_t* base = a.qw + (int64_t)st * 4 * (a.layout == kLayoutTiles ? 16 : a.N);
-      b.wq[u] = ok ? ldw<u32x4, NT>(base, w_boff) : u32x4{0u, 0u, 0u, 0u};
+    if constexpr (FMT == kGptq) {
+      if (tiles) {
+        // the 4 columns' words of this step, 16 bytes apart
+        const uint32_t* base = a.qw + (int64_t)(st >> 2) * 256 + (st & 3);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) b.wq[u][i] = ok ? ldw<uint32_t, NT>(base, w_boff + 16u * i) : 0u;
+      } else {
+        // rows: word row st*4 + kb starts at (st*4)*N
+        const uint32_t* base = a.qw + (int64_t)st * 4 * a.N;
+        b.wq[u] = ok ? ldw<u32x4, NT>(base, w_boff) : u32x4{0u, 0u, 0u, 0u};
+      }
     } else {
       const uint32_t* base = a.qw + (int64_t)st * 32 * n8;
 #pragma unroll
       for (int t = 0; t < 8; ++t)
         b.wd[u][t] = (!PRED || (ok && k + t < a.K)) ? ldw<uint32_t, NT>(base, w_boff + (uint32_t)(t * n8 * 4)) : 0u;
     }
+  };
+  auto load_rest = [&](W4Batch<FMT, MT, U>& b, int u, int st) {
+    const int k = st * 32 + 8 * kb;
     if constexpr (GM == kGLane) {
       const int g = step_group(st, k);
       b.sv[u] = ldb<u32x2>(a.sc + (int64_t)g * a.N, s_boff);
@@ -282,6 +302,11 @@ w4a16_skinny_kernel(W4Args a) {
         for (int d = 0; d < 4; ++d) b.xv[u][t][d] = hv[2 * d] | (hv[2 * d + 1] << 16);
       }
     }
+  };
+
+  auto load_step = [&](W4Batch<FMT, MT, U>& b, int u, int st) {
+    load_weights_step(b, u, st);
+    load_rest(b, u, st);
   };
 
   // derived per-group operands: zero pairs for the two magics and the
@@ -387,6 +412,26 @@ w4a16_skinny_kernel(W4Args a) {
 #pragma unroll
     for (int u = 0; u < U; ++u) load_step(b, u, st0 + u);
   };
+  // tiles, a stage-aligned batch of 4 steps: one 16-byte load per column
+  // holds its words of all 4 steps
+  auto load_batch = [&](W4Batch<FMT, MT, U>& b, int st0) {
+    if constexpr (FMT == kGptq && U == 4 && !PRED) {
+      if (tiles && (st0 & 3) == 0) {
+        const uint32_t* base = a.qw + (int64_t)(st0 >> 2) * 256;
+        u32x4 v[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] = ldw<u32x4, NT>(base, w_boff + 16u * i);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) b.wq[u][i] = v[i][u];
+          load_rest(b, u, st0 + u);
+        }
+        return;
+      }
+    }
+    load(b, st0);
+  };
   auto compute = [&](const W4Batch<FMT, MT, U>& b, int st0) {
 #pragma unroll
     for (int u = 0; u < U; ++u) compute_step(b, u, st0 + u);
@@ -396,12 +441,12 @@ w4a16_skinny_kernel(W4Args a) {
   const int nfull = max(0, wend - wbeg) / U;
   W4Batch<FMT, MT, U> b0, b1;
   int st = wbeg;
-  if (nfull > 0) load(b0, st);
+  if (nfull > 0) load_batch(b0, st);
   int bi = 0;
   for (; bi + 2 <= nfull; bi += 2, st += 2 * U) {
-    load(b1, st + U);
+    load_batch(b1, st + U);
     compute(b0, st);
-    if (bi + 2 < nfull) load(b0, st + 2 * U);
+    if (bi + 2 < nfull) load_batch(b0, st + 2 * U);
     compute(b1, st + U);
   }
   if (bi < nfull) {
@@ -483,7 +528,8 @@ w4a16_skinny_kernel(W4Args a) {
 // columns past N are computed but never stored.
 //
 // Weight layouts: LAYOUT_ROWS = qweight [K/8][N] (checkpoint GPTQ order);
-// LAYOUT_TILES = [ceil(N/16)][K/8][16] (each block's words contiguous).
+// LAYOUT_TILES = the lane-major stage tiles (w4_stages): a lane's words of a
+// stage are one 16-byte load.
 constexpr int kGvWaves = 16;
 
 struct GvPlan {
@@ -539,12 +585,30 @@ KQ_DEV void gv_load(const W4Args& a, const GvCtx& c, int unit, bool live, GvBloc
     b.sv[i] = (uint16_t)kq_rbl_i16(rs, c.slane, (g * a.N + unit * 16) * 2, 0);
     b.zw[i] = (uint32_t)kq_rbl_i32(rz, c.zlane, (g * (a.N / 8) + unit * 2) * 4, 0);
   }
+  if constexpr (LAYOUT == kLayoutTiles) {
+    // a lane's steps of one stage are 16 contiguous bytes: one load per
+    // stage (S = 2: the wave's half of a stage, 8 bytes)
+    const int T = w4_stages(a.K);
+    if constexpr (S >= 4) {
 #pragma unroll
-  for (int s = 0; s < S; ++s) {
-    const int32_t so = LAYOUT == kLayoutTiles
-                           ? (unit * (a.K / 8) + (c.st0 + s) * 4) * 64
-                           : (c.st0 + s) * 16 * a.N + unit * 64;
-    b.w[s] = (uint32_t)kq_rbl_i32(rw, c.wlane, so, kAuxNT);
+      for (int h = 0; h < S / 4; ++h) {
+        const int32_t so = (unit * T + (c.st0 >> 2) + h) * 1024;
+        const i32x4 v = kq_rbl_v4i32(rw, c.wlane, so, kAuxNT);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) b.w[4 * h + e] = (uint32_t)v[e];
+      }
+    } else {
+      const int32_t so = (unit * T + (c.st0 >> 2)) * 1024 + (c.st0 & 3) * 4;
+      const i32x2 v = kq_rbl_v2i32(rw, c.wlane, so, kAuxNT);
+      b.w[0] = (uint32_t)v[0];
+      b.w[1] = (uint32_t)v[1];
+    }
+  } else {
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      const int32_t so = (c.st0 + s) * 16 * a.N + unit * 64;
+      b.w[s] = (uint32_t)kq_rbl_i32(rw, c.wlane, so, kAuxNT);
+    }
   }
   __builtin_amdgcn_sched_barrier(0);
 }
@@ -607,12 +671,12 @@ w4a16_gemv_kernel(W4Args a, GvPlan p) {
 
   GvCtx c;
   const int ngroups = (a.K + a.G - 1) / a.G;
-  const int npad = (a.N + 15) / 16 * 16;
-  c.rw = make_rsrc(a.qw, (uint32_t)((a.K / 8) * (LAYOUT == kLayoutTiles ? npad : a.N) * 4));
+  c.rw = make_rsrc(a.qw, LAYOUT == kLayoutTiles ? (uint32_t)(w4_tile_words(a.N, a.K) * 4)
+                                                 : (uint32_t)((a.K / 8) * a.N * 4));
   c.rs = make_rsrc(a.sc, (uint32_t)(ngroups * a.N * 2));
   c.rz = make_rsrc(a.qz, (uint32_t)(ngroups * (a.N / 8) * 4));
   c.rnull = make_rsrc(a.qw, 0u);
-  c.wlane = LAYOUT == kLayoutTiles ? (kb * 16 + j) * 4 : (kb * a.N + j) * 4;
+  c.wlane = LAYOUT == kLayoutTiles ? lane * 16 : (kb * a.N + j) * 4;
   c.slane = j * 2;
   c.zlane = (j >> 3) * 4;
   c.st0 = wave * S;
@@ -752,13 +816,12 @@ w4a16_prefill_kernel(W4Args a, int mblocks, int tiles) {
   const int mb = t % mblocks, nb = t / mblocks;
   const int m0 = mb * S::BM, n0 = nb * S::BN;
   const int K = a.K, nst = K / 128;
-  const int npad = (a.N + 15) / 16 * 16;
   const int ngroups = K / a.G;
   const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)smem;
 
   // buffer resources: reads past them return zeros
   const i32x4 rx = make_rsrc(a.x, (uint32_t)((uint64_t)a.M * K * 2));
-  const i32x4 rw = make_rsrc(a.qw, (uint32_t)((uint64_t)(K / 8) * npad * 4));
+  const i32x4 rw = make_rsrc(a.qw, (uint32_t)(w4_tile_words(a.N, K) * 4));
   const i32x4 rs = make_rsrc(a.sc, (uint32_t)((uint64_t)ngroups * a.N * 2));
   const i32x4 rz = make_rsrc(a.qz, (uint32_t)((uint64_t)ngroups * (a.N / 8) * 4));
 
@@ -839,12 +902,16 @@ w4a16_prefill_kernel(W4Args a, int mblocks, int tiles) {
       zq1[tn] = nc.c1 + z * 0x00100010u;
       sq[tn] = sv * 0x00010001u;
     }
+    // the stage's four weight words of each column tile (one 16-byte read)
+    u32x4 W[TN];
+#pragma unroll
+    for (int tn = 0; tn < TN; ++tn) W[tn] = *(const u32x4*)(st + S::XBytes + (wn * TN + tn) * 1024 + lane * 16);
 #pragma unroll
     for (int s4 = 0; s4 < 4; ++s4) {
       u32x4 A[TN];
 #pragma unroll
       for (int tn = 0; tn < TN; ++tn) {
-        const uint32_t w = *(const uint32_t*)(st + S::XBytes + (wn * TN + tn) * 1024 + s4 * 256 + lane * 4);
+        const uint32_t w = W[tn][s4];
         const uint32_t y = w >> 8;
         A[tn] = u32x4{pk_sub_mul(and_or(w, nc.m0, nc.c0), zq0[tn], sq[tn]),
                       pk_sub_mul(and_or(w, nc.m1, nc.c1), zq1[tn], sq[tn]),
@@ -959,22 +1026,24 @@ w4a16_prep_x_kernel(const uint16_t* __restrict__ x, int dtype, int ldx,
 // column offset o sits at nibble (o % 2) * 4 + o / 2 (kairyu/quant/awq.py:14-36).
 KQ_DEV uint32_t awq_shift(int o) { return 4u * (uint32_t)((o & 1) * 4 + (o >> 1)); }
 
-// Load-time tiling: out word (u, r, c) of [ceil(N/16)][K/8][16] holds
-// q[row(8r + e)][16u + c] in nibble e, with row(k) = perm[k] (act-order) or k;
-// columns past N are 0.  Source: GPTQ qweight [K/8][N] (LSB-first along k) or
-// AWQ qweight [K][N/8].
+// Load-time tiling into the lane-major stage layout (see w4_stages): the
+// word of packed row r, column n holds q[row(8r + e)][n] in nibble e, with
+// row(k) = perm[k] (act-order) or k; rows past K/8 and columns past N are 0.
+// Source: GPTQ qweight [K/8][N] (LSB-first along k) or AWQ qweight [K][N/8].
 __global__ void w4_tile_kernel(const uint32_t* __restrict__ src, int awq, const int32_t* __restrict__ perm,
                                uint32_t* __restrict__ out, int N, int K) {
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const int kw8 = K / 8;
-  const int units = (N + 15) / 16;
-  if (idx >= (int64_t)units * kw8 * 16) return;
-  const int c = (int)(idx & 15);
-  const int r = (int)((idx >> 4) % kw8);
-  const int u = (int)((idx >> 4) / kw8);
+  const int T = w4_stages(K);
+  if (idx >= w4_tile_words(N, K)) return;
+  const int s4 = (int)(idx & 3);
+  const int lane = (int)((idx >> 2) & 63);
+  const int c = lane & 15, kb = lane >> 4;
+  const int t = (int)((idx >> 8) % T);
+  const int u = (int)((idx >> 8) / T);
+  const int r = t * 16 + s4 * 4 + kb;   // packed row: k = 8r .. 8r + 7
   const int n = u * 16 + c;
   uint32_t word = 0;
-  if (n < N) {
+  if (n < N && r < K / 8) {
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const int k = perm ? perm[8 * r + e] : 8 * r + e;
@@ -1037,7 +1106,9 @@ static W4Plan plan_w4(int M, int N, int K, bool needs_x16, size_t ws_bytes, bool
          p.x16_bytes + plane * p.splits * 2 <= ws_bytes)
     p.splits *= 2;
   p.partial_bytes = p.splits > 1 ? plane * p.splits : 0;
-  p.steps_per_split = (nsteps + p.splits - 1) / p.splits;
+  // whole 128-k stages per split, so that the tiled layout's 16-byte stage
+  // loads stay aligned (a split past the end gets no steps and stores zeros)
+  p.steps_per_split = ((nsteps + p.splits - 1) / p.splits + 3) / 4 * 4;
   return p;
 }
 
@@ -1097,7 +1168,7 @@ static bool gv_plan(const W4Args& a, int fmt, int gmode, GvPlan* p, int* S, int*
     tspg = spg;
   }
   if (((uintptr_t)a.x % 16) != 0 || (a.ldx % 8) != 0) return false;
-  if ((uint64_t)(a.K / 8) * (uint64_t)((a.N + 15) / 16 * 16) * 4u >= ((uint64_t)1 << 31)) return false;
+  if ((uint64_t)w4_tile_words(a.N, a.K) * 4u >= ((uint64_t)1 << 31)) return false;
   const int cus = device_cus();
   p->units = (a.N + 15) / 16;
   if (p->units * 2 < cus) return false;
@@ -1112,7 +1183,7 @@ static bool gv_plan(const W4Args& a, int fmt, int gmode, GvPlan* p, int* S, int*
 static bool prefill_applies(const W4Args& a, int gmode) {
   return a.layout == kLayoutTiles && a.M > 16 && gmode != kGroupsPerK && a.K % 128 == 0 &&
          a.G % 128 == 0 && (int64_t)a.M * a.K < ((int64_t)1 << 30) &&
-         (uint64_t)(a.K / 8) * (uint64_t)((a.N + 15) / 16 * 16) * 4u < ((uint64_t)1 << 31);
+         (uint64_t)w4_tile_words(a.N, a.K) * 4u < ((uint64_t)1 << 31);
 }
 
 template <int TM, int TN, int WM, int NS>
@@ -1364,7 +1435,7 @@ static int tiled_args(const char* what, const void* x, int x_dtype, const int32_
     set_error("%s: needs k %% 8 == 0, group_size %% 8 == 0, zero_offset 0 or 1", what);
     return KQ_EINVAL;
   }
-  if ((uint64_t)(k / 8) * (uint64_t)((n + 15) / 16 * 16) * 4u >= ((uint64_t)1 << 32)) {
+  if ((uint64_t)w4_tile_words((int)n, (int)k) * 4u >= ((uint64_t)1 << 32)) {
     set_error("%s: tiled weight exceeds 4 GiB", what);
     return KQ_EINVAL;
   }
@@ -1463,7 +1534,7 @@ extern "C" int kq_w4a16_tile_weights(const int32_t* qweight, int src_format, con
               (long long)k, src_format);
     return KQ_EINVAL;
   }
-  const int64_t words = (n + 15) / 16 * 16 * (k / 8);
+  const int64_t words = w4_tile_words((int)n, (int)k);
   hipLaunchKernelGGL(w4_tile_kernel, dim3((unsigned)((words + 255) / 256)), dim3(256), 0,
                      (hipStream_t)stream, (const uint32_t*)qweight, src_format == 0 ? 1 : 0, perm,
                      (uint32_t*)tiles, (int)n, (int)k);

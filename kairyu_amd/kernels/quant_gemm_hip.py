@@ -272,7 +272,9 @@ GIDX_PER_K = 2
 
 def _tile(qweight: torch.Tensor, src_format: int, perm: torch.Tensor | None, n: int, k: int,
           device: torch.device) -> torch.Tensor:
-    tiles = torch.empty(((n + 15) // 16, k // 8, 16), dtype=torch.int32, device=device)
+    # [column tile][ceil(K/128) stages x 16 packed rows][16 columns] words in
+    # the lane-major stage order of kq_w4a16_tile_weights
+    tiles = torch.empty(((n + 15) // 16, -(-k // 128) * 16, 16), dtype=torch.int32, device=device)
     _native.call(
         "kq_w4a16_tile_weights", qweight.data_ptr(), src_format, _native.ptr(perm),
         tiles.data_ptr(), n, k, _native.stream_handle(device),

@@ -340,23 +340,33 @@ def test_decode_gemv_matches_oracle(cuda, case):
     check_w4a16(out, module, x, label=str(case))
 
 
-def _untile(tiles: torch.Tensor, n: int) -> torch.Tensor:
-    """[U][K/8][16] tiles -> int [K, N] nibbles (test-side inverse of the tiling)."""
-    units, kw8, _ = tiles.shape
-    q = gptq_format.unpack_gptq_rows(tiles.cpu().permute(1, 0, 2).reshape(kw8, units * 16))
-    return q[:, :n]
+def _natural(tiles: torch.Tensor) -> torch.Tensor:
+    """Tiles [U][T*16][16] in the lane-major stage order -> [U][T*16 packed
+    rows][16 columns] (test-side inverse of the stage permutation: within a
+    stage, word (kb*16 + c)*4 + s holds packed row 4s + kb of column c)."""
+    units, rows, _ = tiles.shape
+    stages = rows // 16
+    return tiles.cpu().reshape(units, stages, 4, 16, 4).permute(0, 1, 4, 2, 3).reshape(units, rows, 16)
+
+
+def _untile(tiles: torch.Tensor, n: int, k: int) -> torch.Tensor:
+    """Tiles -> int [K, N] nibbles (test-side inverse of the tiling)."""
+    nat = _natural(tiles)
+    units, rows, _ = nat.shape
+    q = gptq_format.unpack_gptq_rows(nat.permute(1, 0, 2).reshape(rows, units * 16))
+    return q[:k, :n]
 
 
 def test_tiled_operands_are_exact_and_follow_updates(cuda):
     module = _awq_module(256, 72, group=32, seed=11, random_packed=True).to(cuda)
     tiles, qz = hip._awq_operands(module, torch.device(cuda))
     assert tiles.shape == (5, 32, 16)
-    assert torch.equal(_untile(tiles, 72), awq_format.unpack_awq(module.qweight.cpu()))
+    assert torch.equal(_untile(tiles, 72, 256), awq_format.unpack_awq(module.qweight.cpu()))
     assert torch.equal(gptq_format.unpack_gptq_cols(qz.cpu()), awq_format.unpack_awq(module.qzeros.cpu()))
-    assert int(tiles[4, :, 8:].abs().sum()) == 0  # columns past N
+    assert int(_natural(tiles)[4, :, 8:].abs().sum()) == 0  # columns past N
     module.qweight.copy_(awq_format.pack_awq(torch.randint(0, 16, (256, 72))).to(cuda))
     tiles2, _ = hip._awq_operands(module, torch.device(cuda))
-    assert torch.equal(_untile(tiles2, 72), awq_format.unpack_awq(module.qweight.cpu()))
+    assert torch.equal(_untile(tiles2, 72, 256), awq_format.unpack_awq(module.qweight.cpu()))
     # GPTQ act-order: tile rows follow the stable sort of g_idx
     g_idx = (torch.randperm(256, generator=torch.Generator().manual_seed(3)) // 32).to(torch.int32)
     gmod = _gptq_module(256, 64, group=32, seed=12, g_idx=g_idx, random_packed=True)
@@ -365,7 +375,24 @@ def test_tiled_operands_are_exact_and_follow_updates(cuda):
     mode, tiles, perm = hip._gptq_operands(gmod, torch.device(cuda))
     assert mode == hip.GIDX_PERMUTED
     q = gptq_format.unpack_gptq_rows(gmod.qweight.cpu())
-    assert torch.equal(_untile(tiles, 64), q[perm.cpu().long()])
+    assert torch.equal(_untile(tiles, 64, 256), q[perm.cpu().long()])
+
+
+def test_tiles_pad_a_partial_last_stage_with_zero_rows(cuda):
+    """K = 200 (25 packed rows): the tiling rounds up to two 128-k stages and
+    rows 25..31 hold zeros; N = 40 leaves columns 40..47 of the last tile zero."""
+    g_idx = (torch.randperm(200, generator=torch.Generator().manual_seed(4)) // 40).to(torch.int32)
+    module = _gptq_module(200, 40, group=40, seed=13, g_idx=g_idx, random_packed=True)
+    module.g_idx.copy_(g_idx)
+    module = module.to(cuda)
+    mode, tiles, perm = hip._gptq_operands(module, torch.device(cuda))
+    assert mode == hip.GIDX_PERMUTED and tiles.shape == (3, 32, 16)
+    nat = _natural(tiles)
+    assert int(nat[:, 25:, :].abs().sum()) == 0 and int(nat[2, :, 8:].abs().sum()) == 0
+    q = gptq_format.unpack_gptq_rows(module.qweight.cpu())
+    assert torch.equal(_untile(tiles, 40, 200), q[perm.cpu().long()])
+    x = torch.randn(3, 200, generator=torch.Generator().manual_seed(5)).to(torch.float16)
+    check_w4a16(module(x.to(cuda)), module, x, label="K=200 tiles")
 
 
 def test_checkpoint_layout_entry_points(cuda):
