@@ -151,21 +151,35 @@ int kq_w4a16_gptq_gemm(const void* x, int x_dtype, const int32_t* qweight,
                        int group_size, void* workspace, size_t workspace_bytes,
                        void* stream);
 
-/* Load-time tiling of a W4A16 weight for the tiled kernels: int32 words
- * [ceil(n/16)][ceil(k/128) * 16][16] holding 16-column tiles of 128-k stages.
- * The word of packed row r (k = 8r .. 8r+7) and column 16u + c holds
+/* Load-time tiled operand of a W4A16 weight for the tiled kernels:
+ * kq_w4a16_tiled_words(n, k, group_size) int32 words.  The first
+ * ceil(n/16) * ceil(k/128) * 256 words hold 16-column tiles of 128-k stages:
+ * the word of packed row r (k = 8r .. 8r+7) and column 16u + c holds
  * q[row(8r + e)][16u + c] in nibble e; within tile u's stage t = r / 16 it
  * sits at word (u * ceil(k/128) + t) * 256 + (kb * 16 + c) * 4 + s for
  * r % 16 = 4s + kb, so the 4 words a lane (c, kb) of a 16x16x32 MFMA operand
  * needs for a stage are 16 contiguous bytes.  row(k) = perm[k] when perm is
  * given (GPTQ act-order: the stable argsort of g_idx, so permuted row j has
  * group j / group_size), else k; rows past k/8 and columns past n are 0.
- * src_format 0: AWQ qweight [k, n/8]; 1: GPTQ qweight [k/8, n].  Derived
- * operand only; checkpoint buffers are untouched (the reference caches derived
- * runtime operands the same way, quant_gemm_gpu.py:802-850; formats
- * kairyu/quant/awq.py:14-36, kairyu/quant/gptq.py:15-46). */
+ * A scale/zero table follows: for tile u and group pair p, word
+ * (u * P + p) * 32 + c * 2 + (g & 1) = scales[g][16u + c] bits |
+ * (zero nibble + zero_offset) << 16 for g = 2p, 2p + 1, with
+ * P = ceil(ceil(k / group_size) / 2) (0 past the last group and past n).
+ * src_format 0: AWQ qweight [k, n/8]; 1: GPTQ qweight [k/8, n].  qzeros
+ * [groups, n/8] in natural nibble order and zero_offset as for
+ * kq_w4a16_tiled_gemm, scales fp16 [groups, n]; the tiled GEMM must be given
+ * the same three.  Derived operand only; checkpoint buffers are untouched (the
+ * reference caches derived runtime operands the same way,
+ * quant_gemm_gpu.py:802-850; formats kairyu/quant/awq.py:14-36,
+ * kairyu/quant/gptq.py:15-46). */
 int kq_w4a16_tile_weights(const int32_t* qweight, int src_format, const int32_t* perm,
-                          int32_t* tiles, int64_t n, int64_t k, void* stream);
+                          const int32_t* qzeros, int zero_offset, const void* scales,
+                          int32_t* tiles, int64_t n, int64_t k, int group_size, void* stream);
+
+/* int32 words of kq_w4a16_tile_weights' operand, or -1 for an unsupported
+ * shape (n, k multiples of 8, group_size a multiple of 8 below 65536, k below
+ * 2^24).  Sizing helper; no reference counterpart. */
+int64_t kq_w4a16_tiled_words(int64_t n, int64_t k, int group_size);
 
 /* AWQ qzeros [groups, n/8] (AWQ nibble order) -> natural nibble order
  * (column 8w + i in nibble i), values unchanged: the zero operand of
@@ -173,7 +187,8 @@ int kq_w4a16_tile_weights(const int32_t* qweight, int src_format, const int32_t*
 int kq_awq_natural_zeros(const int32_t* qzeros, int32_t* qzeros_n, int64_t n, int64_t groups,
                          void* stream);
 
-/* W4A16 on kq_w4a16_tile_weights' tiles: w = fp16((q - z) * s[group]) with
+/* W4A16 on kq_w4a16_tile_weights' operand (built from the same qzeros,
+ * zero_offset and scales as this call gets): w = fp16((q - z) * s[group]) with
  * z = stored nibble + zero_offset (GPTQ qzeros: 1; AWQ natural zeros: 0),
  * qzeros [groups, n/8] natural nibble order, scales fp16 [groups, n],
  * group = row / group_size of the (permuted) row; x fed to the dot as fp16

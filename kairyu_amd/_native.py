@@ -58,7 +58,8 @@ _SIGNATURES: dict[str, list] = {
         _P, _I, _P, _P, _P, _P, _P, _I, _P, _I, _P, _I64, _I64, _I64, _I, _P, _SZ, _P,
     ],
     "kq_gptq_permute_qweight": [_P, _P, _P, _I64, _I64, _P],
-    "kq_w4a16_tile_weights": [_P, _I, _P, _P, _I64, _I64, _P],
+    "kq_w4a16_tile_weights": [_P, _I, _P, _P, _I, _P, _P, _I64, _I64, _I, _P],
+    "kq_w4a16_tiled_words": [_I64, _I64, _I],
     "kq_awq_natural_zeros": [_P, _P, _I64, _I64, _P],
     "kq_w4a16_tiled_gemm": [
         _P, _I, _P, _P, _I, _P, _P, _P, _I, _P, _I64, _I64, _I64, _I, _P, _SZ, _P,
@@ -100,6 +101,7 @@ def _load() -> ctypes.CDLL:
             fn.argtypes = argtypes
             fn.restype = {"kq_last_error": ctypes.c_char_p,
                           "kq_w4a16_workspace_size": ctypes.c_size_t,
+                          "kq_w4a16_tiled_words": ctypes.c_int64,
                           "kq_w8a8_workspace_size": ctypes.c_size_t,
                           "kq_w8a8_linear_workspace_size": ctypes.c_size_t,
                           "kq_moe_workspace_size": ctypes.c_size_t}.get(name, ctypes.c_int)

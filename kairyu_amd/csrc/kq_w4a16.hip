@@ -67,6 +67,16 @@ __host__ __device__ inline int w4_stages(int K) { return (K + 127) / 128; }
 __host__ __device__ inline int64_t w4_tile_words(int N, int K) {
   return (int64_t)((N + 15) / 16) * w4_stages(K) * 256;
 }
+// The tiled operand continues with a scale/zero table read by the decode
+// GEMV: for tile u and group pair p (groups 2p, 2p + 1), 16 columns x 2
+// groups of one word each, scale bits | (zero nibble + zero offset) << 16, at
+// word (u * P + p) * 32 + c * 2 + (g & 1), P = ceil(groups / 2); groups past
+// the last and columns past N are 0.  A lane (c, kb) gets the scales and
+// zeros of its column for two consecutive groups with one 8-byte load.
+__host__ __device__ inline int w4_group_pairs(int K, int G) { return ((K + G - 1) / G + 1) / 2; }
+__host__ __device__ inline int64_t w4_tiled_words(int N, int K, int G) {
+  return w4_tile_words(N, K) + (int64_t)((N + 15) / 16) * w4_group_pairs(K, G) * 32;
+}
 
 struct W4Args {
   const uint16_t* x;     // activation rows (fp16 or bf16 per kernel template)
@@ -539,23 +549,30 @@ struct GvPlan {
 template <int S, int SPG>
 struct GvShape {
   static constexpr int kGroups = SPG >= S ? 1 : S / SPG;        // group slots per window
-  static constexpr int kDepth = (S + 2 * kGroups) > 16 ? 2 : ((S + 2 * kGroups) > 12 ? 3 : 4);  // blocks in flight
+  // blocks in flight per wave.  S = 8 (K = 4096): 3, measured on C2
+  // (N = 28672, M = 16): 13.8 us against 14.3 us with 4 and 13.9 with 2; more
+  // requests in flight do not add bandwidth here, they delay the first block.
+  static constexpr int kDepth = (S + 2 * kGroups) > 16 ? 2
+                                : (S >= 8 || (S + 2 * kGroups) > 12) ? 3 : 4;
   static constexpr int kRound = kDepth;  // blocks per reduction round (several rounds)
-  static constexpr int kOneRound = 2 * kDepth;  // a workgroup's whole share in one round
+  // a workgroup's whole share in one round (at least 8 blocks: 7 on C2)
+  static constexpr int kOneRound = 2 * kDepth < 8 ? 8 : 2 * kDepth;
 };
 
 template <int S, int SPG>
 struct GvBlock {
   uint32_t w[S];
-  uint32_t sv[GvShape<S, SPG>::kGroups];
-  uint32_t zw[GvShape<S, SPG>::kGroups];
+  uint32_t sv[GvShape<S, SPG>::kGroups];  // LAYOUT_ROWS: scale bits
+  uint32_t zw[GvShape<S, SPG>::kGroups];  // LAYOUT_ROWS: zero word; tiles: table word
 };
 
 struct GvCtx {
-  i32x4 rw, rs, rz;      // buffer resources: qweight, scales, qzeros
+  i32x4 rw, rs, rz;      // buffer resources: qweight (tiles: + table), scales, qzeros
   i32x4 rnull;           // zero-size resource (dead blocks)
   int32_t wlane;         // lane byte offset inside a step (layout dependent)
-  int32_t slane, zlane;  // lane byte offsets of its scale / zero word
+  int32_t slane, zlane;  // lane byte offsets of its scale / zero (tiles: table) word
+  int32_t tbase;         // tiles: byte offset of the scale/zero table
+  int pairs;             // tiles: group pairs per column tile
   int st0;               // first step of this wave
   int g0;                // group of the first step
 };
@@ -576,14 +593,31 @@ KQ_DEV i32x4 select_rsrc(bool live, const i32x4& r, const i32x4& dead) {
 
 template <int S, int SPG, int LAYOUT>
 KQ_DEV void gv_load(const W4Args& a, const GvCtx& c, int unit, bool live, GvBlock<S, SPG>& b) {
+  constexpr int NG = GvShape<S, SPG>::kGroups;
   const i32x4 rw = select_rsrc(live, c.rw, c.rnull);
-  const i32x4 rs = select_rsrc(live, c.rs, c.rnull);
-  const i32x4 rz = select_rsrc(live, c.rz, c.rnull);
+  if constexpr (LAYOUT == kLayoutTiles) {
+    // the window's scale/zero words from the table behind the tiles: one
+    // word (a single group) or 8 bytes per group pair (g0 is then even)
+    const int32_t so = c.tbase + (unit * c.pairs + (c.g0 >> 1)) * 128;
+    if constexpr (NG == 1) {
+      b.zw[0] = (uint32_t)kq_rbl_i32(rw, c.zlane, so + (c.g0 & 1) * 4, 0);
+    } else {
 #pragma unroll
-  for (int i = 0; i < GvShape<S, SPG>::kGroups; ++i) {
-    const int g = c.g0 + i;
-    b.sv[i] = (uint16_t)kq_rbl_i16(rs, c.slane, (g * a.N + unit * 16) * 2, 0);
-    b.zw[i] = (uint32_t)kq_rbl_i32(rz, c.zlane, (g * (a.N / 8) + unit * 2) * 4, 0);
+      for (int i = 0; i < NG / 2; ++i) {
+        const i32x2 v = kq_rbl_v2i32(rw, c.zlane, so + i * 128, 0);
+        b.zw[2 * i] = (uint32_t)v[0];
+        b.zw[2 * i + 1] = (uint32_t)v[1];
+      }
+    }
+  } else {
+    const i32x4 rs = select_rsrc(live, c.rs, c.rnull);
+    const i32x4 rz = select_rsrc(live, c.rz, c.rnull);
+#pragma unroll
+    for (int i = 0; i < NG; ++i) {
+      const int g = c.g0 + i;
+      b.sv[i] = (uint16_t)kq_rbl_i16(rs, c.slane, (g * a.N + unit * 16) * 2, 0);
+      b.zw[i] = (uint32_t)kq_rbl_i32(rz, c.zlane, (g * (a.N / 8) + unit * 2) * 4, 0);
+    }
   }
   if constexpr (LAYOUT == kLayoutTiles) {
     // a lane's steps of one stage are 16 contiguous bytes: one load per
@@ -613,7 +647,7 @@ KQ_DEV void gv_load(const W4Args& a, const GvCtx& c, int unit, bool live, GvBloc
   __builtin_amdgcn_sched_barrier(0);
 }
 
-template <int S, int SPG>
+template <int S, int SPG, int LAYOUT>
 KQ_DEV f32x4 gv_compute(const W4Args& a, const NibbleConsts& nc, uint32_t zsh,
                         const GvBlock<S, SPG>& b, const u32x4 (&A)[S]) {
   f32x4 acc{0.f, 0.f, 0.f, 0.f};
@@ -622,10 +656,16 @@ KQ_DEV f32x4 gv_compute(const W4Args& a, const NibbleConsts& nc, uint32_t zsh,
   for (int s = 0; s < S; ++s) {
     if (SPG >= S ? s == 0 : (s % SPG) == 0) {
       const int i = SPG >= S ? 0 : s / SPG;
-      const uint32_t z = ((b.zw[i] >> zsh) & 0xfu) + a.zoff;
+      uint32_t z;
+      if constexpr (LAYOUT == kLayoutTiles) {
+        z = b.zw[i] >> 16;                                   // zero offset included
+        sq = __builtin_amdgcn_perm(b.zw[i], b.zw[i], 0x05040504u);  // (scale, scale)
+      } else {
+        z = ((b.zw[i] >> zsh) & 0xfu) + a.zoff;
+        sq = b.sv[i] * 0x00010001u;
+      }
       zq0 = nc.c0 + z * 0x00010001u;   // (1024 + z) pair
       zq1 = nc.c1 + z * 0x00100010u;   // (64 + z) pair
-      sq = b.sv[i] * 0x00010001u;
     }
     const uint32_t w = b.w[s], y = w >> 8;
     const u32x4 B{pk_sub_mul(and_or(w, nc.m0, nc.c0), zq0, sq),   // k+0, k+4
@@ -637,8 +677,9 @@ KQ_DEV f32x4 gv_compute(const W4Args& a, const NibbleConsts& nc, uint32_t zsh,
   return acc;
 }
 
-// MODE kGvOne: the launch guarantees ncb <= 2*D blocks per workgroup, so one
-// round with the accumulators of all of them in registers (no outer loop).
+// MODE kGvOne: the launch guarantees ncb <= kOneRound blocks per workgroup,
+// so one round with the accumulators of all of them in registers (no outer
+// loop).
 // kGvShort: ncb <= D, one round of D blocks.  kGvSingle: every workgroup owns
 // exactly one block (D = U = 1).  The modes keep the slots past a share few:
 // their out-of-range loads move no data but still cost address-unit issue
@@ -671,14 +712,16 @@ w4a16_gemv_kernel(W4Args a, GvPlan p) {
 
   GvCtx c;
   const int ngroups = (a.K + a.G - 1) / a.G;
-  c.rw = make_rsrc(a.qw, LAYOUT == kLayoutTiles ? (uint32_t)(w4_tile_words(a.N, a.K) * 4)
+  c.rw = make_rsrc(a.qw, LAYOUT == kLayoutTiles ? (uint32_t)(w4_tiled_words(a.N, a.K, a.G) * 4)
                                                  : (uint32_t)((a.K / 8) * a.N * 4));
   c.rs = make_rsrc(a.sc, (uint32_t)(ngroups * a.N * 2));
   c.rz = make_rsrc(a.qz, (uint32_t)(ngroups * (a.N / 8) * 4));
   c.rnull = make_rsrc(a.qw, 0u);
   c.wlane = LAYOUT == kLayoutTiles ? lane * 16 : (kb * a.N + j) * 4;
   c.slane = j * 2;
-  c.zlane = (j >> 3) * 4;
+  c.zlane = LAYOUT == kLayoutTiles ? j * 8 : (j >> 3) * 4;
+  c.tbase = (int32_t)(w4_tile_words(a.N, a.K) * 4);
+  c.pairs = w4_group_pairs(a.K, a.G);
   c.st0 = wave * S;
   c.g0 = __builtin_amdgcn_readfirstlane(group_of(a, c.st0 * 32));
   const uint32_t zsh = 4u * (uint32_t)(j & 7);
@@ -715,7 +758,7 @@ w4a16_gemv_kernel(W4Args a, GvPlan p) {
 #pragma unroll
     for (int q = 0; q < U; ++q) {
       acc[q] = f32x4{0.f, 0.f, 0.f, 0.f};
-      if (q0 + q < ncb) acc[q] = gv_compute<S, SPG>(a, nc, zsh, buf[q % D], A);
+      if (q0 + q < ncb) acc[q] = gv_compute<S, SPG, LAYOUT>(a, nc, zsh, buf[q % D], A);
       // (ONE: the share has at most U blocks, so slots past U are never loaded)
       if (!ONE || q + D < U) gv_load<S, SPG, LAYOUT>(a, c, u0 + q0 + q + D, q0 + q + D < ncb, buf[q % D]);
     }
@@ -1055,6 +1098,25 @@ __global__ void w4_tile_kernel(const uint32_t* __restrict__ src, int awq, const 
   out[idx] = word;
 }
 
+// The scale/zero table behind the tiles (see w4_tiled_words), from natural
+// nibble order zeros [groups][N/8] and fp16 scales [groups][N].
+__global__ void w4_scale_zero_kernel(const uint32_t* __restrict__ qz, uint32_t zoff,
+                                     const uint16_t* __restrict__ sc, uint32_t* __restrict__ out,
+                                     int N, int K, int G) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int P = w4_group_pairs(K, G);
+  if (idx >= (int64_t)((N + 15) / 16) * P * 32) return;
+  const int h = (int)(idx & 1), c = (int)((idx >> 1) & 15);
+  const int p = (int)((idx >> 5) % P), u = (int)((idx >> 5) / P);
+  const int g = 2 * p + h, n = 16 * u + c;
+  uint32_t v = 0;
+  if (g < (K + G - 1) / G && n < N) {
+    const uint32_t z = ((qz[(int64_t)g * (N / 8) + (n >> 3)] >> (4 * (n & 7))) & 0xfu) + zoff;
+    v = (uint32_t)sc[(int64_t)g * N + n] | (z << 16);
+  }
+  out[idx] = v;
+}
+
 // AWQ zeros -> natural nibble order (column 8c + i in nibble i), values kept.
 __global__ void awq_natural_zeros_kernel(const uint32_t* __restrict__ qz, uint32_t* __restrict__ out,
                                          int64_t words) {
@@ -1168,7 +1230,7 @@ static bool gv_plan(const W4Args& a, int fmt, int gmode, GvPlan* p, int* S, int*
     tspg = spg;
   }
   if (((uintptr_t)a.x % 16) != 0 || (a.ldx % 8) != 0) return false;
-  if ((uint64_t)w4_tile_words(a.N, a.K) * 4u >= ((uint64_t)1 << 31)) return false;
+  if ((uint64_t)w4_tiled_words(a.N, a.K, a.G) * 4u >= ((uint64_t)1 << 31)) return false;
   const int cus = device_cus();
   p->units = (a.N + 15) / 16;
   if (p->units * 2 < cus) return false;
@@ -1422,6 +1484,13 @@ extern "C" int kq_w4a16_gptq_gemm(const void* x, int x_dtype, const int32_t* qwe
                 (hipStream_t)stream);
 }
 
+// Shapes the tiled operand supports (32-bit k and group arithmetic of the
+// kernels; whole packed rows and 8-row group chunks).
+static bool tiled_shape_ok(int64_t n, int64_t k, int64_t group_size) {
+  return n >= 8 && k >= 8 && (n % 8) == 0 && (k % 8) == 0 && n <= 0x7fffffff && k < (1 << 24) &&
+         group_size >= 8 && (group_size % 8) == 0 && group_size < (1 << 16);
+}
+
 // Arguments of the tiled entry points (validated; a.layout = tiles).
 static int tiled_args(const char* what, const void* x, int x_dtype, const int32_t* tiles,
                       const int32_t* qzeros, int zero_offset, const void* scales,
@@ -1435,8 +1504,9 @@ static int tiled_args(const char* what, const void* x, int x_dtype, const int32_
     set_error("%s: needs k %% 8 == 0, group_size %% 8 == 0, zero_offset 0 or 1", what);
     return KQ_EINVAL;
   }
-  if ((uint64_t)w4_tile_words((int)n, (int)k) * 4u >= ((uint64_t)1 << 32)) {
-    set_error("%s: tiled weight exceeds 4 GiB", what);
+  if (!tiled_shape_ok(n, k, group_size) ||
+      (uint64_t)w4_tiled_words((int)n, (int)k, group_size) * 4u >= ((uint64_t)1 << 32)) {
+    set_error("%s: tiled weight exceeds 4 GiB or bad shape", what);
     return KQ_EINVAL;
   }
   W4Args a{};
@@ -1526,18 +1596,33 @@ extern "C" int kq_w4a16_tiled_gemm_noalloc(const void* x, int x_dtype, const int
                 (size_t)KQ_W4A16_NOALLOC_SCRATCH_BYTES, (hipStream_t)stream);
 }
 
+extern "C" int64_t kq_w4a16_tiled_words(int64_t n, int64_t k, int group_size) {
+  if (!tiled_shape_ok(n, k, group_size)) return -1;
+  return w4_tiled_words((int)n, (int)k, group_size);
+}
+
 extern "C" int kq_w4a16_tile_weights(const int32_t* qweight, int src_format, const int32_t* perm,
-                                     int32_t* tiles, int64_t n, int64_t k, void* stream) {
-  if (n < 8 || k < 8 || (n % 8) != 0 || (k % 8) != 0 || n > 0x7fffffff || k > 0x7fffffff ||
-      (src_format != 0 && src_format != 1)) {
-    set_error("kq_w4a16_tile_weights: bad arguments n=%lld k=%lld format=%d", (long long)n,
-              (long long)k, src_format);
+                                     const int32_t* qzeros, int zero_offset, const void* scales,
+                                     int32_t* tiles, int64_t n, int64_t k, int group_size,
+                                     void* stream) {
+  if (!tiled_shape_ok(n, k, group_size) || (src_format != 0 && src_format != 1) ||
+      (zero_offset != 0 && zero_offset != 1)) {
+    set_error("kq_w4a16_tile_weights: bad arguments n=%lld k=%lld group=%d format=%d zero_offset=%d",
+              (long long)n, (long long)k, group_size, src_format, zero_offset);
+    return KQ_EINVAL;
+  }
+  if ((uint64_t)w4_tiled_words((int)n, (int)k, group_size) * 4u >= ((uint64_t)1 << 32)) {
+    set_error("kq_w4a16_tile_weights: tiled weight exceeds 4 GiB");
     return KQ_EINVAL;
   }
   const int64_t words = w4_tile_words((int)n, (int)k);
   hipLaunchKernelGGL(w4_tile_kernel, dim3((unsigned)((words + 255) / 256)), dim3(256), 0,
                      (hipStream_t)stream, (const uint32_t*)qweight, src_format == 0 ? 1 : 0, perm,
                      (uint32_t*)tiles, (int)n, (int)k);
+  const int64_t table = w4_tiled_words((int)n, (int)k, group_size) - words;
+  hipLaunchKernelGGL(w4_scale_zero_kernel, dim3((unsigned)((table + 255) / 256)), dim3(256), 0,
+                     (hipStream_t)stream, (const uint32_t*)qzeros, (uint32_t)zero_offset,
+                     (const uint16_t*)scales, (uint32_t*)tiles + words, (int)n, (int)k, group_size);
   return check_launch("kq_w4a16_tile_weights");
 }
 

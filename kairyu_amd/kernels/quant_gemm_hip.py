@@ -270,14 +270,24 @@ GIDX_PERMUTED = 1
 GIDX_PER_K = 2
 
 
-def _tile(qweight: torch.Tensor, src_format: int, perm: torch.Tensor | None, n: int, k: int,
-          device: torch.device) -> torch.Tensor:
-    # [column tile][ceil(K/128) stages x 16 packed rows][16 columns] words in
-    # the lane-major stage order of kq_w4a16_tile_weights
-    tiles = torch.empty(((n + 15) // 16, -(-k // 128) * 16, 16), dtype=torch.int32, device=device)
+def tile_operand(qweight: torch.Tensor, src_format: int, perm: torch.Tensor | None,
+                 qzeros: torch.Tensor, zero_offset: int, scales: torch.Tensor, n: int, k: int,
+                 group: int, device: torch.device) -> torch.Tensor | None:
+    """Flat int32 tiled operand of ``kq_w4a16_tile_weights``: the
+    [column tile][ceil(K/128) stages x 16 packed rows][16 columns] words in
+    lane-major stage order, then the per-tile scale/zero table.  ``qzeros``
+    is in natural nibble order; the tiled GEMM is called with the same
+    ``qzeros``, ``zero_offset`` and ``scales``.  None for a shape the tiled
+    kernels do not take (``kq_w4a16_tiled_words``)."""
+
+    words = int(_native.library().kq_w4a16_tiled_words(n, k, group))
+    if words < 0:
+        return None
+    tiles = torch.empty(words, dtype=torch.int32, device=device)
     _native.call(
         "kq_w4a16_tile_weights", qweight.data_ptr(), src_format, _native.ptr(perm),
-        tiles.data_ptr(), n, k, _native.stream_handle(device),
+        qzeros.data_ptr(), zero_offset, scales.data_ptr(), tiles.data_ptr(), n, k, group,
+        _native.stream_handle(device),
     )
     return tiles
 
@@ -305,22 +315,23 @@ def _awq_operands(module, device: torch.device):
     layout.
     """
 
-    qweight, qzeros = module.qweight, module.qzeros
+    qweight, qzeros, scales = module.qweight, module.qzeros, module.scales
     k, n, group = module.in_features, module.out_features, module.group_size
     if k % 8 != 0 or group % 8 != 0:
         return None
-    key = (id(qweight), qweight._version, id(qzeros), qzeros._version, str(device))
+    key = (id(qweight), qweight._version, id(qzeros), qzeros._version, id(scales),
+           scales._version, str(device))
     cached = module.__dict__.get("_kq_awq_operands")
     if cached is not None and cached[0] == key:
         return cached[1]
     _refuse_under_capture("AWQ")
-    tiles = _tile(qweight, 0, None, n, k, device)
     qzeros_n = torch.empty_like(qzeros)
     _native.call(
         "kq_awq_natural_zeros", qzeros.data_ptr(), qzeros_n.data_ptr(), n, qzeros.shape[0],
         _native.stream_handle(device),
     )
-    result = (tiles, qzeros_n)
+    tiles = tile_operand(qweight, 0, None, qzeros_n, 0, scales, n, k, group, device)
+    result = None if tiles is None else (tiles, qzeros_n)
     object.__setattr__(module, "_kq_awq_operands", (key, result))
     return result
 
@@ -362,8 +373,9 @@ def _gptq_operands(module, device: torch.device):
     per-element group path on the checkpoint buffers.
     """
 
-    g_idx, qweight = module.g_idx, module.qweight
-    key = (id(g_idx), g_idx._version, id(qweight), qweight._version, str(device))
+    g_idx, qweight, qzeros, scales = module.g_idx, module.qweight, module.qzeros, module.scales
+    key = (id(g_idx), g_idx._version, id(qweight), qweight._version, id(qzeros), qzeros._version,
+           id(scales), scales._version, str(device))
     cached = module.__dict__.get("_kq_gptq_operands")
     if cached is not None and cached[0] == key:
         return cached[1]
@@ -374,12 +386,16 @@ def _gptq_operands(module, device: torch.device):
     result = (GIDX_PER_K, qweight, None)
     if group % 8 == 0:
         if torch.equal(gi, natural):
-            result = (GIDX_UNIFORM, _tile(qweight, 1, None, n, k, device), None)
+            tiles = tile_operand(qweight, 1, None, qzeros, 1, scales, n, k, group, device)
+            if tiles is not None:
+                result = (GIDX_UNIFORM, tiles, None)
         else:
             perm = torch.argsort(gi, stable=True)
             if torch.equal(gi[perm], natural):
                 perm32 = perm.to(torch.int32).contiguous()
-                result = (GIDX_PERMUTED, _tile(qweight, 1, perm32, n, k, device), perm32)
+                tiles = tile_operand(qweight, 1, perm32, qzeros, 1, scales, n, k, group, device)
+                if tiles is not None:
+                    result = (GIDX_PERMUTED, tiles, perm32)
     object.__setattr__(module, "_kq_gptq_operands", (key, result))
     return result
 

@@ -13,8 +13,8 @@ for this package's quantized formats:
   per-token activation quantization and one GEMM serve all projections.
 * AWQ / GPTQ W4A16 (``AwqLinear``, ``GptqLinear``): ``N`` is the packed minor
   dimension of those checkpoints, so their buffers stay untouched; the pack
-  keeps derived operands (the 16-column weight tiles of every projection
-  stacked along ``N``, their zeros and fp16 scales side by side), rebuilt when
+  keeps derived operands (the projections' columns side by side, tiled as one
+  weight with its zeros and fp16 scales), rebuilt when
   a source tensor's version changes, as the single-module derived operands
   are.  GPTQ projections pack when they share one ``g_idx`` (uniform groups,
   or one act-order permutation, so one activation gather serves all).
@@ -209,10 +209,17 @@ class QuantLinearPack:
                     else hip._f32(m.weight_scale) for m in mods]).contiguous()
             elif self._scheme == "awq":
                 ops = [hip._awq_operands(m, device) for m in mods]
-                d["tiles"] = torch.cat([t for t, _ in ops], dim=0)
+                if any(op is None for op in ops):
+                    raise RuntimeError("AWQ pack requires tileable projections")
                 d["zeros"] = torch.cat([z for _, z in ops], dim=1).contiguous()
                 d["scales"] = torch.cat([m.scales for m in mods], dim=1).contiguous()
                 d["perm"], d["zero_offset"], d["mode"] = None, 0, hip.GIDX_UNIFORM
+                # the packed columns tiled as one weight (tiles and their
+                # scale/zero table)
+                d["tiles"] = hip.tile_operand(
+                    torch.cat([m.qweight for m in mods], dim=1).contiguous(), 0, None, d["zeros"], 0,
+                    d["scales"], sum(self._out_features), mods[0].in_features, mods[0].group_size,
+                    device)
                 for m in mods:  # the pack holds the only tiled copy
                     m.__dict__.pop("_kq_awq_operands", None)
             else:
@@ -225,10 +232,13 @@ class QuantLinearPack:
                     raise RuntimeError("GPTQ pack requires uniform or act-order groups")
                 if any(mode != ops[0][0] for mode, _, _ in ops):
                     raise RuntimeError("packed GPTQ projections need one group mode")
-                d["tiles"] = torch.cat([t for _, t, _ in ops], dim=0)
                 d["zeros"] = torch.cat([m.qzeros for m in mods], dim=1).contiguous()
                 d["scales"] = torch.cat([m.scales for m in mods], dim=1).contiguous()
                 d["perm"], d["zero_offset"], d["mode"] = ops[0][2], 1, ops[0][0]
+                d["tiles"] = hip.tile_operand(
+                    torch.cat([m.qweight for m in mods], dim=1).contiguous(), 1, d["perm"],
+                    d["zeros"], 1, d["scales"], sum(self._out_features), mods[0].in_features,
+                    mods[0].group_size, device)
                 for m in mods:
                     m.__dict__.pop("_kq_gptq_operands", None)
         self._derived, self._derived_key = d, key

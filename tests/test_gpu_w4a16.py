@@ -340,34 +340,57 @@ def test_decode_gemv_matches_oracle(cuda, case):
     check_w4a16(out, module, x, label=str(case))
 
 
-def _natural(tiles: torch.Tensor) -> torch.Tensor:
-    """Tiles [U][T*16][16] in the lane-major stage order -> [U][T*16 packed
-    rows][16 columns] (test-side inverse of the stage permutation: within a
-    stage, word (kb*16 + c)*4 + s holds packed row 4s + kb of column c)."""
-    units, rows, _ = tiles.shape
-    stages = rows // 16
-    return tiles.cpu().reshape(units, stages, 4, 16, 4).permute(0, 1, 4, 2, 3).reshape(units, rows, 16)
+def _natural(tiles: torch.Tensor, n: int, k: int) -> torch.Tensor:
+    """The tile part of a tiled operand in the lane-major stage order ->
+    [U][T*16 packed rows][16 columns] (test-side inverse of the stage
+    permutation: within a stage, word (kb*16 + c)*4 + s holds packed row
+    4s + kb of column c)."""
+    units, stages = -(-n // 16), -(-k // 128)
+    words = tiles.cpu()[:units * stages * 256]
+    return words.reshape(units, stages, 4, 16, 4).permute(0, 1, 4, 2, 3).reshape(units, stages * 16, 16)
 
 
 def _untile(tiles: torch.Tensor, n: int, k: int) -> torch.Tensor:
-    """Tiles -> int [K, N] nibbles (test-side inverse of the tiling)."""
-    nat = _natural(tiles)
+    """Tiled operand -> int [K, N] nibbles (test-side inverse of the tiling)."""
+    nat = _natural(tiles, n, k)
     units, rows, _ = nat.shape
     q = gptq_format.unpack_gptq_rows(nat.permute(1, 0, 2).reshape(rows, units * 16))
     return q[:k, :n]
 
 
+def _table(tiles: torch.Tensor, n: int, k: int, group: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """Scale/zero table behind the tiles -> (fp16 scales [groups][N], zeros
+    [groups][N] with the zero offset included), test-side inverse: word
+    (u*P + p)*32 + c*2 + h holds group 2p + h of column 16u + c."""
+    units, stages, groups = -(-n // 16), -(-k // 128), -(-k // group)
+    pairs = -(-groups // 2)
+    words = tiles.cpu()[units * stages * 256:]
+    assert words.numel() == units * pairs * 32
+    t = words.reshape(units, pairs, 16, 2).permute(1, 3, 0, 2).reshape(pairs * 2, units * 16)
+    pad = t[groups:].abs().sum() + t[:, n:].abs().sum()
+    assert int(pad) == 0  # groups past the last, columns past N
+    t = t[:groups, :n]
+    return (t & 0xFFFF).to(torch.int16).view(torch.float16), t >> 16
+
+
 def test_tiled_operands_are_exact_and_follow_updates(cuda):
     module = _awq_module(256, 72, group=32, seed=11, random_packed=True).to(cuda)
     tiles, qz = hip._awq_operands(module, torch.device(cuda))
-    assert tiles.shape == (5, 32, 16)
+    assert tiles.shape == (5 * 2 * 256 + 5 * 4 * 32,)
     assert torch.equal(_untile(tiles, 72, 256), awq_format.unpack_awq(module.qweight.cpu()))
     assert torch.equal(gptq_format.unpack_gptq_cols(qz.cpu()), awq_format.unpack_awq(module.qzeros.cpu()))
-    assert int(_natural(tiles)[4, :, 8:].abs().sum()) == 0  # columns past N
+    assert int(_natural(tiles, 72, 256)[4, :, 8:].abs().sum()) == 0  # columns past N
+    scales, zeros = _table(tiles, 72, 256, 32)
+    assert torch.equal(scales, module.scales.cpu())
+    assert torch.equal(zeros, awq_format.unpack_awq(module.qzeros.cpu()))
     module.qweight.copy_(awq_format.pack_awq(torch.randint(0, 16, (256, 72))).to(cuda))
     tiles2, _ = hip._awq_operands(module, torch.device(cuda))
     assert torch.equal(_untile(tiles2, 72, 256), awq_format.unpack_awq(module.qweight.cpu()))
-    # GPTQ act-order: tile rows follow the stable sort of g_idx
+    # a scale update rebuilds the table
+    module.scales.mul_(2)
+    tiles3, _ = hip._awq_operands(module, torch.device(cuda))
+    assert torch.equal(_table(tiles3, 72, 256, 32)[0], module.scales.cpu())
+    # GPTQ act-order: tile rows follow the stable sort of g_idx; zeros carry +1
     g_idx = (torch.randperm(256, generator=torch.Generator().manual_seed(3)) // 32).to(torch.int32)
     gmod = _gptq_module(256, 64, group=32, seed=12, g_idx=g_idx, random_packed=True)
     gmod.g_idx.copy_(g_idx)
@@ -376,21 +399,28 @@ def test_tiled_operands_are_exact_and_follow_updates(cuda):
     assert mode == hip.GIDX_PERMUTED
     q = gptq_format.unpack_gptq_rows(gmod.qweight.cpu())
     assert torch.equal(_untile(tiles, 64, 256), q[perm.cpu().long()])
+    scales, zeros = _table(tiles, 64, 256, 32)
+    assert torch.equal(scales, gmod.scales.cpu())
+    assert torch.equal(zeros, gptq_format.unpack_gptq_cols(gmod.qzeros.cpu()) + 1)
 
 
 def test_tiles_pad_a_partial_last_stage_with_zero_rows(cuda):
     """K = 200 (25 packed rows): the tiling rounds up to two 128-k stages and
-    rows 25..31 hold zeros; N = 40 leaves columns 40..47 of the last tile zero."""
+    rows 25..31 hold zeros; N = 40 leaves columns 40..47 of the last tile zero;
+    5 groups leave the second word of the last group pair zero."""
     g_idx = (torch.randperm(200, generator=torch.Generator().manual_seed(4)) // 40).to(torch.int32)
     module = _gptq_module(200, 40, group=40, seed=13, g_idx=g_idx, random_packed=True)
     module.g_idx.copy_(g_idx)
     module = module.to(cuda)
     mode, tiles, perm = hip._gptq_operands(module, torch.device(cuda))
-    assert mode == hip.GIDX_PERMUTED and tiles.shape == (3, 32, 16)
-    nat = _natural(tiles)
+    assert mode == hip.GIDX_PERMUTED and tiles.shape == (3 * 2 * 256 + 3 * 3 * 32,)
+    nat = _natural(tiles, 40, 200)
     assert int(nat[:, 25:, :].abs().sum()) == 0 and int(nat[2, :, 8:].abs().sum()) == 0
     q = gptq_format.unpack_gptq_rows(module.qweight.cpu())
     assert torch.equal(_untile(tiles, 40, 200), q[perm.cpu().long()])
+    scales, zeros = _table(tiles, 40, 200, 40)
+    assert torch.equal(scales, module.scales.cpu())
+    assert torch.equal(zeros, gptq_format.unpack_gptq_cols(module.qzeros.cpu()) + 1)
     x = torch.randn(3, 200, generator=torch.Generator().manual_seed(5)).to(torch.float16)
     check_w4a16(module(x.to(cuda)), module, x, label="K=200 tiles")
 

@@ -16,7 +16,7 @@ HEADER = Path(__file__).resolve().parents[1] / "include" / "kairyu_quant.h"
 
 def declared_symbols() -> set[str]:
     text = HEADER.read_text()
-    return set(re.findall(r"^\s*(?:int|const char\*|size_t)\s+(kq_\w+)\s*\(", text, re.M))
+    return set(re.findall(r"^\s*(?:int|int64_t|const char\*|size_t)\s+(kq_\w+)\s*\(", text, re.M))
 
 
 def test_header_declarations_are_bound():
@@ -40,6 +40,14 @@ def test_exported_symbols_in_dynamic_table():
                          capture_output=True, text=True, check=True).stdout
     exported = set(re.findall(r"\sT\s(kq_\w+)", out))
     assert declared_symbols() <= exported
+
+
+def test_tiled_operand_size():
+    # tiles (2 units x 2 stages x 256 words) + table (2 units x 3 group pairs x 32)
+    assert _native.library().kq_w4a16_tiled_words(24, 256, 48) == 2 * 2 * 256 + 2 * 3 * 32
+    assert _native.library().kq_w4a16_tiled_words(28672, 4096, 128) == 1792 * 32 * 256 + 1792 * 16 * 32
+    assert _native.library().kq_w4a16_tiled_words(20, 256, 128) == -1  # n % 8
+    assert _native.library().kq_w4a16_tiled_words(24, 256, 12) == -1   # group % 8
 
 
 def test_bad_shapes_fail_closed_without_touching_the_device():
