@@ -455,7 +455,8 @@ def main() -> int:
     parser.add_argument("--no-cpu", action="store_true")
     parser.add_argument("--no-headline", action="store_true",
                         help="skip the headline measurement (profiling one sweep row)")
-    parser.add_argument("--only", default=None, help="substring filter for sweep entries")
+    parser.add_argument("--only", default=None,
+                        help="substring filter for sweep entries ('a|b': either)")
     parser.add_argument("--copy-calibration", action="store_true",
                         help="only run 256 MiB device-to-device copies (HBM counter calibration)")
     args = parser.parse_args()
@@ -498,7 +499,7 @@ def main() -> int:
     sweep = []
     if not args.no_sweep:
         for name, dtype, builder in sweep_entries():
-            if args.only and args.only not in name:
+            if args.only and not any(part in name for part in args.only.split("|")):
                 continue
             wl = builder()
             print(f"[bench] sweep {name}", file=sys.stderr, flush=True)

@@ -694,7 +694,14 @@ w4a16_gemv_kernel(W4Args a, GvPlan p) {
   constexpr int U = MODE == kGvSingle ? 1
                     : MODE == kGvShort ? D
                     : (MODE == kGvOne ? GvShape<S, SPG>::kOneRound : GvShape<S, SPG>::kRound);
-  __shared__ float red[kGvWaves][U * 4][64];
+  // LDS: per wave, first its x slice (16 rows x S*32 halves, rows padded by
+  // 16 bytes), later its row of partial sums; the wave is done with x before
+  // it writes partial sums, so the two share the wave's region.
+  constexpr int kXRow = S * 64 + 16;                       // bytes per staged x row
+  constexpr int kWaveLds = (16 * kXRow > U * 4 * 64 * 4) ? 16 * kXRow : U * 4 * 64 * 4;
+  __shared__ __attribute__((aligned(16))) char lds[kGvWaves * kWaveLds];
+  static_assert(kGvWaves * kWaveLds <= 160 * 1024, "LDS");
+  auto red = [&](int w, int i) -> float* { return (float*)(lds + w * kWaveLds) + i * 64; };
   const int lane = lane_id();
   const int wave = __builtin_amdgcn_readfirstlane(wave_id());
   const int j = lane & 15, kb = lane >> 4;
@@ -730,12 +737,22 @@ w4a16_gemv_kernel(W4Args a, GvPlan p) {
   // They are requested before the weights: loads complete in issue order, so
   // the first block's compute then waits for x and that block only, not for
   // every block in flight (which would leave HBM idle between the first
-  // window and the loads the compute issues).
+  // window and the loads the compute issues).  The loads read whole 128-byte
+  // lines (8 lanes per row, 8 rows per instruction: half the line requests
+  // of the MFMA lane order, which reads 64 bytes of 16 rows); the wave then
+  // moves them into the MFMA lane order through its own LDS region (no
+  // barrier: only this wave reads it).  Measured C1 (N = K = 4096, M = 16,
+  // one column block per workgroup, x 80% of a workgroup's bytes): see the
+  // kernel table.
   u32x4 X[S];
   {
-    const uint16_t* xr = a.x + (int64_t)min(j, a.M - 1) * a.ldx + c.st0 * 32 + 8 * kb;
+    const int rsub = lane >> 3, csub = lane & 7;
 #pragma unroll
-    for (int s = 0; s < S; ++s) X[s] = *(const u32x4*)(xr + s * 32);
+    for (int i = 0; i < S; ++i) {
+      const int q = i * 8 + rsub;                 // row chunk: row q % 16, 128 B chunk q / 16
+      const int row = q & 15, cc = q >> 4;
+      X[i] = *(const u32x4*)(a.x + (int64_t)min(row, a.M - 1) * a.ldx + c.st0 * 32 + cc * 64 + csub * 8);
+    }
   }
 
   // rolling window: block q's weights were requested D blocks earlier.  No
@@ -747,6 +764,19 @@ w4a16_gemv_kernel(W4Args a, GvPlan p) {
   GvBlock<S, SPG> buf[D];
 #pragma unroll
   for (int d = 0; d < D; ++d) gv_load<S, SPG, LAYOUT>(a, c, u0 + d, d < ncb, buf[d]);
+
+  // x in the MFMA lane order (the weight loads above stay in flight)
+  {
+    const int rsub = lane >> 3, csub = lane & 7;
+    char* mine = lds + wave * kWaveLds;
+#pragma unroll
+    for (int i = 0; i < S; ++i) {
+      const int q = i * 8 + rsub;
+      *(u32x4*)(mine + (q & 15) * kXRow + (q >> 4) * 128 + csub * 16) = X[i];
+    }
+#pragma unroll
+    for (int s = 0; s < S; ++s) X[s] = *(const u32x4*)(mine + j * kXRow + s * 64 + kb * 16);
+  }
 
   u32x4 A[S];
 #pragma unroll
@@ -767,14 +797,14 @@ w4a16_gemv_kernel(W4Args a, GvPlan p) {
 #pragma unroll
     for (int q = 0; q < U; ++q)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) red[wave][q * 4 + r][lane] = acc[q][r];
+      for (int r = 0; r < 4; ++r) red(wave, q * 4 + r)[lane] = acc[q][r];
     __syncthreads();
     for (int i = wave; i < U * 4; i += kGvWaves) {   // one output per thread
       const int q = i >> 2, r = i & 3;
       if (q0 + q >= ncb) continue;
-      float v = red[0][i][lane];
+      float v = red(0, i)[lane];
 #pragma unroll
-      for (int w = 1; w < kGvWaves; ++w) v = __fadd_rn(v, red[w][i][lane]);
+      for (int w = 1; w < kGvWaves; ++w) v = __fadd_rn(v, red(w, i)[lane]);
       const int m = 4 * kb + r;
       const int n = (u0 + q0 + q) * 16 + j;
       if (m < a.M && n < a.N) {
