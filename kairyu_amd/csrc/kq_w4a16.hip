@@ -741,9 +741,9 @@ w4a16_gemv_kernel(W4Args a, GvPlan p) {
   // lines (8 lanes per row, 8 rows per instruction: half the line requests
   // of the MFMA lane order, which reads 64 bytes of 16 rows); the wave then
   // moves them into the MFMA lane order through its own LDS region (no
-  // barrier: only this wave reads it).  Measured C1 (N = K = 4096, M = 16,
-  // one column block per workgroup, x 80% of a workgroup's bytes): see the
-  // kernel table.
+  // barrier: only this wave reads it).  Measured: C1 (N = K = 4096, M = 16,
+  // one column block per workgroup, x 80% of a workgroup's bytes) 6.47 ->
+  // 5.30 us; C2 M = 16 13.85 -> 13.50 us.
   u32x4 X[S];
   {
     const int rsub = lane >> 3, csub = lane & 7;
