@@ -160,18 +160,18 @@ def gemm_launcher(workload, copies: int):
             ops = [hip._gptq_operands(mod, device) for mod in mods]
             mode, _, perm = ops[0]
             x16 = x[:, perm.long()].contiguous() if mode == hip.GIDX_PERMUTED else x
-            operands = [(t, mod.qzeros, 1, mod.scales) for mod, (_, t, _) in zip(mods, ops)]
+            operands = [(t.tiles, t.zeros, t.zero_offset, mod.scales) for mod, (_, t, _) in zip(mods, ops)]
         else:
             ops = [hip._awq_operands(mod, device) for mod in mods]
             x16 = x
-            operands = [(t, z, 0, mod.scales) for mod, (t, z) in zip(mods, ops)]
+            operands = [(t.tiles, t.zeros, t.zero_offset, mod.scales) for mod, t in zip(mods, ops)]
         out = torch.empty((m, n), device=device, dtype=x.dtype)
         ws = _native.workspace(device, int(_native.library().kq_w4a16_workspace_size(m, n, k, 0)))
 
         def launch(i):
             tiles, zeros, zoff, scales = operands[i % copies]
             _native.call("kq_w4a16_tiled_gemm", x16.data_ptr(), _native.dtype_code(x16.dtype),
-                         tiles.data_ptr(), zeros.data_ptr(), zoff, scales.data_ptr(), None, None,
+                         tiles.data_ptr(), _native.ptr(zeros), zoff, scales.data_ptr(), None, None,
                          _native.DTYPE_NONE, out.data_ptr(), m, n, k, group, ws.data_ptr(), ws.numel(),
                          _native.stream_handle(device))
 

@@ -165,8 +165,12 @@ int kq_w4a16_gptq_gemm(const void* x, int x_dtype, const int32_t* qweight,
  * (u * P + p) * 32 + c * 2 + (g & 1) = scales[g][16u + c] bits |
  * (zero nibble + zero_offset) << 16 for g = 2p, 2p + 1, with
  * P = ceil(ceil(k / group_size) / 2) (0 past the last group and past n).
+ * With qzeros null (one zero, zero_offset in 0..16, for every group and
+ * column: symmetric checkpoints) the table holds scales alone, word
+ * (u * P + p) * 16 + c = scales[2p][16u + c] | scales[2p + 1][16u + c] << 16,
+ * followed by ceil(k / group_size) * n/8 words of zero nibbles.
  * src_format 0: AWQ qweight [k, n/8]; 1: GPTQ qweight [k/8, n].  qzeros
- * [groups, n/8] in natural nibble order and zero_offset as for
+ * [groups, n/8] in natural nibble order (or null) and zero_offset as for
  * kq_w4a16_tiled_gemm, scales fp16 [groups, n]; the tiled GEMM must be given
  * the same three.  Derived operand only; checkpoint buffers are untouched (the
  * reference caches derived runtime operands the same way,
@@ -176,10 +180,11 @@ int kq_w4a16_tile_weights(const int32_t* qweight, int src_format, const int32_t*
                           const int32_t* qzeros, int zero_offset, const void* scales,
                           int32_t* tiles, int64_t n, int64_t k, int group_size, void* stream);
 
-/* int32 words of kq_w4a16_tile_weights' operand, or -1 for an unsupported
- * shape (n, k multiples of 8, group_size a multiple of 8 below 65536, k below
- * 2^24).  Sizing helper; no reference counterpart. */
-int64_t kq_w4a16_tiled_words(int64_t n, int64_t k, int group_size);
+/* int32 words of kq_w4a16_tile_weights' operand (one_zero: built with qzeros
+ * null), or -1 for an unsupported shape (n, k multiples of 8, group_size a
+ * multiple of 8 below 65536, k below 2^24).  Sizing helper; no reference
+ * counterpart. */
+int64_t kq_w4a16_tiled_words(int64_t n, int64_t k, int group_size, int one_zero);
 
 /* AWQ qzeros [groups, n/8] (AWQ nibble order) -> natural nibble order
  * (column 8w + i in nibble i), values unchanged: the zero operand of
@@ -189,7 +194,8 @@ int kq_awq_natural_zeros(const int32_t* qzeros, int32_t* qzeros_n, int64_t n, in
 
 /* W4A16 on kq_w4a16_tile_weights' operand (built from the same qzeros,
  * zero_offset and scales as this call gets): w = fp16((q - z) * s[group]) with
- * z = stored nibble + zero_offset (GPTQ qzeros: 1; AWQ natural zeros: 0),
+ * z = stored nibble + zero_offset (GPTQ qzeros: 1; AWQ natural zeros: 0;
+ * qzeros null: z = zero_offset in 0..16 everywhere, for an operand tiled so),
  * qzeros [groups, n/8] natural nibble order, scales fp16 [groups, n],
  * group = row / group_size of the (permuted) row; x fed to the dot as fp16
  * (bf16 saturated to +-65504), fp32 accumulation, out in x_dtype.  perm

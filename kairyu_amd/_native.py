@@ -59,7 +59,7 @@ _SIGNATURES: dict[str, list] = {
     ],
     "kq_gptq_permute_qweight": [_P, _P, _P, _I64, _I64, _P],
     "kq_w4a16_tile_weights": [_P, _I, _P, _P, _I, _P, _P, _I64, _I64, _I, _P],
-    "kq_w4a16_tiled_words": [_I64, _I64, _I],
+    "kq_w4a16_tiled_words": [_I64, _I64, _I, _I],
     "kq_awq_natural_zeros": [_P, _P, _I64, _I64, _P],
     "kq_w4a16_tiled_gemm": [
         _P, _I, _P, _P, _I, _P, _P, _P, _I, _P, _I64, _I64, _I64, _I, _P, _SZ, _P,

@@ -54,6 +54,8 @@ enum { kXF16 = 0, kXBF16 = 1 };
 // (checkpoint GPTQ order) or 16-column tiles [ceil(N/16)][K/8][16] (each
 // tile's words contiguous, built at load time by kq_w4a16_tile_weights)
 enum { kLayoutRows = 0, kLayoutTiles = 1 };
+// decode GEMV only: tiles whose table holds scales alone (one zero for all)
+constexpr int kLayoutTilesZu = 2;
 
 constexpr int kW4Cols = 64;   // columns per workgroup tile
 
@@ -73,9 +75,21 @@ __host__ __device__ inline int64_t w4_tile_words(int N, int K) {
 // word (u * P + p) * 32 + c * 2 + (g & 1), P = ceil(groups / 2); groups past
 // the last and columns past N are 0.  A lane (c, kb) gets the scales and
 // zeros of its column for two consecutive groups with one 8-byte load.
+// With one zero for every group and column (symmetric checkpoints, "zu") the
+// table holds the scales alone, word (u * P + p) * 16 + c = scale of group 2p
+// | scale of group 2p + 1 << 16 (4 bytes per lane and group pair, 2 bytes per
+// group and column as in the checkpoint), followed by groups x N/8 zero
+// words of nibble 0 (the zero is then the zero offset) for the kernels that
+// read zero words.
 __host__ __device__ inline int w4_group_pairs(int K, int G) { return ((K + G - 1) / G + 1) / 2; }
-__host__ __device__ inline int64_t w4_tiled_words(int N, int K, int G) {
-  return w4_tile_words(N, K) + (int64_t)((N + 15) / 16) * w4_group_pairs(K, G) * 32;
+__host__ __device__ inline int64_t w4_table_words(int N, int K, int G, bool zu) {
+  return (int64_t)((N + 15) / 16) * w4_group_pairs(K, G) * (zu ? 16 : 32);
+}
+__host__ __device__ inline int64_t w4_zero_area_words(int N, int K, int G, bool zu) {
+  return zu ? (int64_t)((K + G - 1) / G) * (N / 8) : 0;
+}
+__host__ __device__ inline int64_t w4_tiled_words(int N, int K, int G, bool zu) {
+  return w4_tile_words(N, K) + w4_table_words(N, K, G, zu) + w4_zero_area_words(N, K, G, zu);
 }
 
 struct W4Args {
@@ -98,6 +112,7 @@ struct W4Args {
   float* partials;       // [splits][M][N] when splits > 1
   uint32_t zoff;         // added to stored zero nibbles (GPTQ 1, natural-order AWQ 0)
   int layout;            // kLayoutRows (qweight [K/8][N]) or kLayoutTiles
+  int zu;                // tiles built with one zero for every group and column (zoff)
 };
 
 KQ_DEV int group_of(const W4Args& a, int k) {
@@ -595,7 +610,16 @@ template <int S, int SPG, int LAYOUT>
 KQ_DEV void gv_load(const W4Args& a, const GvCtx& c, int unit, bool live, GvBlock<S, SPG>& b) {
   constexpr int NG = GvShape<S, SPG>::kGroups;
   const i32x4 rw = select_rsrc(live, c.rw, c.rnull);
-  if constexpr (LAYOUT == kLayoutTiles) {
+  if constexpr (LAYOUT == kLayoutTilesZu) {
+    // scales alone: one 2-byte scale (a single group) or 4 bytes per group pair
+    const int32_t so = c.tbase + (unit * c.pairs + (c.g0 >> 1)) * 64;
+    if constexpr (NG == 1) {
+      b.zw[0] = (uint16_t)kq_rbl_i16(rw, c.zlane, so + (c.g0 & 1) * 2, 0);
+    } else {
+#pragma unroll
+      for (int i = 0; i < NG / 2; ++i) b.zw[i] = (uint32_t)kq_rbl_i32(rw, c.zlane, so + i * 64, 0);
+    }
+  } else if constexpr (LAYOUT == kLayoutTiles) {
     // the window's scale/zero words from the table behind the tiles: one
     // word (a single group) or 8 bytes per group pair (g0 is then even)
     const int32_t so = c.tbase + (unit * c.pairs + (c.g0 >> 1)) * 128;
@@ -619,7 +643,7 @@ KQ_DEV void gv_load(const W4Args& a, const GvCtx& c, int unit, bool live, GvBloc
       b.zw[i] = (uint32_t)kq_rbl_i32(rz, c.zlane, (g * (a.N / 8) + unit * 2) * 4, 0);
     }
   }
-  if constexpr (LAYOUT == kLayoutTiles) {
+  if constexpr (LAYOUT != kLayoutRows) {
     // a lane's steps of one stage are 16 contiguous bytes: one load per
     // stage (S = 2: the wave's half of a stage, 8 bytes)
     const int T = w4_stages(a.K);
@@ -657,7 +681,12 @@ KQ_DEV f32x4 gv_compute(const W4Args& a, const NibbleConsts& nc, uint32_t zsh,
     if (SPG >= S ? s == 0 : (s % SPG) == 0) {
       const int i = SPG >= S ? 0 : s / SPG;
       uint32_t z;
-      if constexpr (LAYOUT == kLayoutTiles) {
+      if constexpr (LAYOUT == kLayoutTilesZu) {
+        z = a.zoff;                                          // the operand's one zero
+        sq = GvShape<S, SPG>::kGroups == 1 ? b.zw[0] * 0x00010001u
+                            : __builtin_amdgcn_perm(b.zw[i >> 1], b.zw[i >> 1],
+                                                    (i & 1) ? 0x07060706u : 0x05040504u);
+      } else if constexpr (LAYOUT == kLayoutTiles) {
         z = b.zw[i] >> 16;                                   // zero offset included
         sq = __builtin_amdgcn_perm(b.zw[i], b.zw[i], 0x05040504u);  // (scale, scale)
       } else {
@@ -719,14 +748,15 @@ w4a16_gemv_kernel(W4Args a, GvPlan p) {
 
   GvCtx c;
   const int ngroups = (a.K + a.G - 1) / a.G;
-  c.rw = make_rsrc(a.qw, LAYOUT == kLayoutTiles ? (uint32_t)(w4_tiled_words(a.N, a.K, a.G) * 4)
-                                                 : (uint32_t)((a.K / 8) * a.N * 4));
+  c.rw = make_rsrc(a.qw, LAYOUT != kLayoutRows
+                            ? (uint32_t)(w4_tiled_words(a.N, a.K, a.G, LAYOUT == kLayoutTilesZu) * 4)
+                            : (uint32_t)((a.K / 8) * a.N * 4));
   c.rs = make_rsrc(a.sc, (uint32_t)(ngroups * a.N * 2));
   c.rz = make_rsrc(a.qz, (uint32_t)(ngroups * (a.N / 8) * 4));
   c.rnull = make_rsrc(a.qw, 0u);
-  c.wlane = LAYOUT == kLayoutTiles ? lane * 16 : (kb * a.N + j) * 4;
+  c.wlane = LAYOUT != kLayoutRows ? lane * 16 : (kb * a.N + j) * 4;
   c.slane = j * 2;
-  c.zlane = LAYOUT == kLayoutTiles ? j * 8 : (j >> 3) * 4;
+  c.zlane = LAYOUT == kLayoutTilesZu ? j * 4 : LAYOUT == kLayoutTiles ? j * 8 : (j >> 3) * 4;
   c.tbase = (int32_t)(w4_tile_words(a.N, a.K) * 4);
   c.pairs = w4_group_pairs(a.K, a.G);
   c.st0 = wave * S;
@@ -1129,20 +1159,35 @@ __global__ void w4_tile_kernel(const uint32_t* __restrict__ src, int awq, const 
 }
 
 // The scale/zero table behind the tiles (see w4_tiled_words), from natural
-// nibble order zeros [groups][N/8] and fp16 scales [groups][N].
+// nibble order zeros [groups][N/8] (null: one zero, zoff) and fp16 scales
+// [groups][N]; with one zero the scale-only table and the zero-word area.
 __global__ void w4_scale_zero_kernel(const uint32_t* __restrict__ qz, uint32_t zoff,
                                      const uint16_t* __restrict__ sc, uint32_t* __restrict__ out,
                                      int N, int K, int G) {
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const int P = w4_group_pairs(K, G);
-  if (idx >= (int64_t)((N + 15) / 16) * P * 32) return;
+  const bool zu = qz == nullptr;
+  const int P = w4_group_pairs(K, G), groups = (K + G - 1) / G;
+  const int64_t table = w4_table_words(N, K, G, zu);
+  if (idx >= table) {
+    if (idx < table + w4_zero_area_words(N, K, G, zu)) out[idx] = 0u;  // zero nibbles
+    return;
+  }
+  auto scale = [&](int g, int n) -> uint32_t {
+    return g < groups && n < N ? (uint32_t)sc[(int64_t)g * N + n] : 0u;
+  };
+  if (zu) {
+    const int c = (int)(idx & 15), p = (int)((idx >> 4) % P), u = (int)((idx >> 4) / P);
+    const int n = 16 * u + c;
+    out[idx] = scale(2 * p, n) | (scale(2 * p + 1, n) << 16);
+    return;
+  }
   const int h = (int)(idx & 1), c = (int)((idx >> 1) & 15);
   const int p = (int)((idx >> 5) % P), u = (int)((idx >> 5) / P);
   const int g = 2 * p + h, n = 16 * u + c;
   uint32_t v = 0;
-  if (g < (K + G - 1) / G && n < N) {
+  if (g < groups && n < N) {
     const uint32_t z = ((qz[(int64_t)g * (N / 8) + (n >> 3)] >> (4 * (n & 7))) & 0xfu) + zoff;
-    v = (uint32_t)sc[(int64_t)g * N + n] | (z << 16);
+    v = scale(g, n) | (z << 16);
   }
   out[idx] = v;
 }
@@ -1260,7 +1305,7 @@ static bool gv_plan(const W4Args& a, int fmt, int gmode, GvPlan* p, int* S, int*
     tspg = spg;
   }
   if (((uintptr_t)a.x % 16) != 0 || (a.ldx % 8) != 0) return false;
-  if ((uint64_t)w4_tiled_words(a.N, a.K, a.G) * 4u >= ((uint64_t)1 << 31)) return false;
+  if ((uint64_t)w4_tiled_words(a.N, a.K, a.G, a.zu != 0) * 4u >= ((uint64_t)1 << 31)) return false;
   const int cus = device_cus();
   p->units = (a.N + 15) / 16;
   if (p->units * 2 < cus) return false;
@@ -1307,7 +1352,12 @@ static void launch_gv_s(const W4Args& a, const GvPlan& p, int layout, hipStream_
                                                        : kGvRounds;
   const dim3 g(p.wgs), b(64 * kGvWaves);
 #define KQ_GV_LAUNCH(L, M) hipLaunchKernelGGL((w4a16_gemv_kernel<XDT, S, SPG, L, M>), g, b, 0, st, a, p)
-  if (layout == kLayoutTiles) {
+  if (layout == kLayoutTiles && a.zu) {
+    if (mode == kGvSingle) KQ_GV_LAUNCH(kLayoutTilesZu, kGvSingle);
+    else if (mode == kGvShort) KQ_GV_LAUNCH(kLayoutTilesZu, kGvShort);
+    else if (mode == kGvOne) KQ_GV_LAUNCH(kLayoutTilesZu, kGvOne);
+    else KQ_GV_LAUNCH(kLayoutTilesZu, kGvRounds);
+  } else if (layout == kLayoutTiles) {
     if (mode == kGvSingle) KQ_GV_LAUNCH(kLayoutTiles, kGvSingle);
     else if (mode == kGvShort) KQ_GV_LAUNCH(kLayoutTiles, kGvShort);
     else if (mode == kGvOne) KQ_GV_LAUNCH(kLayoutTiles, kGvOne);
@@ -1530,18 +1580,25 @@ static int tiled_args(const char* what, const void* x, int x_dtype, const int32_
     set_error("%s: dimensions exceed int32", what);
     return KQ_EINVAL;
   }
-  if (k % 8 != 0 || group_size % 8 != 0 || (zero_offset != 0 && zero_offset != 1)) {
-    set_error("%s: needs k %% 8 == 0, group_size %% 8 == 0, zero_offset 0 or 1", what);
+  const bool zu = qzeros == nullptr;
+  if (k % 8 != 0 || group_size % 8 != 0 || zero_offset < 0 || zero_offset > (zu ? 16 : 1)) {
+    set_error("%s: needs k %% 8 == 0, group_size %% 8 == 0, zero_offset 0 or 1 (0..16 without "
+              "qzeros)", what);
     return KQ_EINVAL;
   }
   if (!tiled_shape_ok(n, k, group_size) ||
-      (uint64_t)w4_tiled_words((int)n, (int)k, group_size) * 4u >= ((uint64_t)1 << 32)) {
+      (uint64_t)w4_tiled_words((int)n, (int)k, group_size, zu) * 4u >= ((uint64_t)1 << 32)) {
     set_error("%s: tiled weight exceeds 4 GiB or bad shape", what);
     return KQ_EINVAL;
   }
   W4Args a{};
   a.x = (const uint16_t*)x; a.x_dtype = x_dtype; a.ldx = (int)k;
   a.qw = (const uint32_t*)tiles; a.qz = (const uint32_t*)qzeros; a.sc = (const uint16_t*)scales;
+  // one zero: the other kernels read the operand's zero-nibble words
+  if (zu)
+    a.qz = (const uint32_t*)tiles + w4_tile_words((int)n, (int)k) +
+           w4_table_words((int)n, (int)k, group_size, true);
+  a.zu = zu ? 1 : 0;
   a.perm = perm;
   a.bias = bias; a.bias_dtype = bias_dtype; a.out = (uint16_t*)out; a.out_dtype = x_dtype;
   a.M = (int)m; a.N = (int)n; a.K = (int)k; a.G = group_size; a.zoff = (uint32_t)zero_offset;
@@ -1626,22 +1683,23 @@ extern "C" int kq_w4a16_tiled_gemm_noalloc(const void* x, int x_dtype, const int
                 (size_t)KQ_W4A16_NOALLOC_SCRATCH_BYTES, (hipStream_t)stream);
 }
 
-extern "C" int64_t kq_w4a16_tiled_words(int64_t n, int64_t k, int group_size) {
+extern "C" int64_t kq_w4a16_tiled_words(int64_t n, int64_t k, int group_size, int one_zero) {
   if (!tiled_shape_ok(n, k, group_size)) return -1;
-  return w4_tiled_words((int)n, (int)k, group_size);
+  return w4_tiled_words((int)n, (int)k, group_size, one_zero != 0);
 }
 
 extern "C" int kq_w4a16_tile_weights(const int32_t* qweight, int src_format, const int32_t* perm,
                                      const int32_t* qzeros, int zero_offset, const void* scales,
                                      int32_t* tiles, int64_t n, int64_t k, int group_size,
                                      void* stream) {
+  const bool zu = qzeros == nullptr;
   if (!tiled_shape_ok(n, k, group_size) || (src_format != 0 && src_format != 1) ||
-      (zero_offset != 0 && zero_offset != 1)) {
+      zero_offset < 0 || zero_offset > (zu ? 16 : 1)) {
     set_error("kq_w4a16_tile_weights: bad arguments n=%lld k=%lld group=%d format=%d zero_offset=%d",
               (long long)n, (long long)k, group_size, src_format, zero_offset);
     return KQ_EINVAL;
   }
-  if ((uint64_t)w4_tiled_words((int)n, (int)k, group_size) * 4u >= ((uint64_t)1 << 32)) {
+  if ((uint64_t)w4_tiled_words((int)n, (int)k, group_size, zu) * 4u >= ((uint64_t)1 << 32)) {
     set_error("kq_w4a16_tile_weights: tiled weight exceeds 4 GiB");
     return KQ_EINVAL;
   }
@@ -1649,7 +1707,7 @@ extern "C" int kq_w4a16_tile_weights(const int32_t* qweight, int src_format, con
   hipLaunchKernelGGL(w4_tile_kernel, dim3((unsigned)((words + 255) / 256)), dim3(256), 0,
                      (hipStream_t)stream, (const uint32_t*)qweight, src_format == 0 ? 1 : 0, perm,
                      (uint32_t*)tiles, (int)n, (int)k);
-  const int64_t table = w4_tiled_words((int)n, (int)k, group_size) - words;
+  const int64_t table = w4_tiled_words((int)n, (int)k, group_size, zu) - words;
   hipLaunchKernelGGL(w4_scale_zero_kernel, dim3((unsigned)((table + 255) / 256)), dim3(256), 0,
                      (hipStream_t)stream, (const uint32_t*)qzeros, (uint32_t)zero_offset,
                      (const uint16_t*)scales, (uint32_t*)tiles + words, (int)n, (int)k, group_size);

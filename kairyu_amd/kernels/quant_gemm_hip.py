@@ -12,6 +12,8 @@ floating-point ``[out, in]`` weight and there is no dequantized fallback.
 
 from __future__ import annotations
 
+from typing import NamedTuple
+
 from functools import lru_cache
 
 import torch
@@ -270,26 +272,52 @@ GIDX_PERMUTED = 1
 GIDX_PER_K = 2
 
 
+class TiledOperand(NamedTuple):
+    """A W4A16 weight as the tiled kernels read it: ``tiles`` (flat int32,
+    ``kq_w4a16_tile_weights``) and the ``zeros`` / ``zero_offset`` arguments
+    the tiled GEMM takes with it (``zeros`` None: one zero, ``zero_offset``,
+    for every group and column)."""
+
+    tiles: torch.Tensor
+    zeros: torch.Tensor | None
+    zero_offset: int
+
+
+def _one_zero(qzeros: torch.Tensor) -> int | None:
+    """The nibble every word of natural-order ``qzeros`` repeats, or None
+    (one host read at load time)."""
+
+    flat = qzeros.reshape(-1)
+    nibble = int(flat[0].item()) & 0xF
+    word = nibble * 0x11111111
+    word = word - (1 << 32) if word >= (1 << 31) else word
+    return nibble if bool((flat == word).all().item()) else None
+
+
 def tile_operand(qweight: torch.Tensor, src_format: int, perm: torch.Tensor | None,
                  qzeros: torch.Tensor, zero_offset: int, scales: torch.Tensor, n: int, k: int,
-                 group: int, device: torch.device) -> torch.Tensor | None:
-    """Flat int32 tiled operand of ``kq_w4a16_tile_weights``: the
-    [column tile][ceil(K/128) stages x 16 packed rows][16 columns] words in
-    lane-major stage order, then the per-tile scale/zero table.  ``qzeros``
-    is in natural nibble order; the tiled GEMM is called with the same
-    ``qzeros``, ``zero_offset`` and ``scales``.  None for a shape the tiled
-    kernels do not take (``kq_w4a16_tiled_words``)."""
+                 group: int, device: torch.device) -> TiledOperand | None:
+    """The tiled operand of ``kq_w4a16_tile_weights``: the [column
+    tile][ceil(K/128) stages x 16 packed rows][16 columns] words in lane-major
+    stage order, then the per-tile scale/zero table; ``qzeros`` is in natural
+    nibble order.  When every zero is the same (symmetric checkpoints) the
+    operand is built with one zero (``qzeros`` null in the C ABI): the decode
+    GEMV then reads 2 bytes of scale per group and column and no zeros.  None
+    for a shape the tiled kernels do not take (``kq_w4a16_tiled_words``)."""
 
-    words = int(_native.library().kq_w4a16_tiled_words(n, k, group))
+    nibble = _one_zero(qzeros)
+    one = nibble is not None
+    words = int(_native.library().kq_w4a16_tiled_words(n, k, group, int(one)))
     if words < 0:
         return None
     tiles = torch.empty(words, dtype=torch.int32, device=device)
+    zeros, zoff = (None, nibble + zero_offset) if one else (qzeros, zero_offset)
     _native.call(
         "kq_w4a16_tile_weights", qweight.data_ptr(), src_format, _native.ptr(perm),
-        qzeros.data_ptr(), zero_offset, scales.data_ptr(), tiles.data_ptr(), n, k, group,
+        _native.ptr(zeros), zoff, scales.data_ptr(), tiles.data_ptr(), n, k, group,
         _native.stream_handle(device),
     )
-    return tiles
+    return TiledOperand(tiles, zeros, zoff)
 
 
 def _refuse_under_capture(scheme: str) -> None:
@@ -303,8 +331,17 @@ def _refuse_under_capture(scheme: str) -> None:
         )
 
 
-def _awq_operands(module, device: torch.device):
-    """(tiles, natural-order qzeros) of an AWQ module, or None.
+def awq_natural_zeros(qzeros: torch.Tensor, n: int, device: torch.device) -> torch.Tensor:
+    """AWQ ``qzeros`` in natural nibble order (``kq_awq_natural_zeros``)."""
+
+    natural = torch.empty_like(qzeros)
+    _native.call("kq_awq_natural_zeros", qzeros.data_ptr(), natural.data_ptr(), n, qzeros.shape[0],
+                 _native.stream_handle(device))
+    return natural
+
+
+def _awq_operands(module, device: torch.device) -> TiledOperand | None:
+    """The tiled operand of an AWQ module, or None.
 
     The W4A16 kernels stream 16-column tiles of K-packed words
     (``kq_w4a16_tile_weights``); shapes with ``k % 8 == 0`` and
@@ -325,13 +362,8 @@ def _awq_operands(module, device: torch.device):
     if cached is not None and cached[0] == key:
         return cached[1]
     _refuse_under_capture("AWQ")
-    qzeros_n = torch.empty_like(qzeros)
-    _native.call(
-        "kq_awq_natural_zeros", qzeros.data_ptr(), qzeros_n.data_ptr(), n, qzeros.shape[0],
-        _native.stream_handle(device),
-    )
-    tiles = tile_operand(qweight, 0, None, qzeros_n, 0, scales, n, k, group, device)
-    result = None if tiles is None else (tiles, qzeros_n)
+    result = tile_operand(qweight, 0, None, awq_natural_zeros(qzeros, n, device), 0, scales, n, k,
+                          group, device)
     object.__setattr__(module, "_kq_awq_operands", (key, result))
     return result
 
@@ -350,8 +382,8 @@ def awq_linear_forward(x: torch.Tensor, module, *, add_bias: bool = True) -> tor
     if tiled is not None:
         _native.call(
             "kq_w4a16_tiled_gemm",
-            flat.data_ptr(), _native.dtype_code(flat.dtype), tiled[0].data_ptr(),
-            tiled[1].data_ptr(), 0, module.scales.data_ptr(), None, *common,
+            flat.data_ptr(), _native.dtype_code(flat.dtype), tiled.tiles.data_ptr(),
+            _native.ptr(tiled.zeros), tiled.zero_offset, module.scales.data_ptr(), None, *common,
         )
     else:
         _native.call(
@@ -363,7 +395,9 @@ def awq_linear_forward(x: torch.Tensor, module, *, add_bias: bool = True) -> tor
 
 
 def _gptq_operands(module, device: torch.device):
-    """(gidx_mode, weight operand, perm or None) for a GPTQ module.
+    """(gidx_mode, weight operand, perm or None) for a GPTQ module: the
+    operand is a ``TiledOperand`` for the uniform and act-order modes, else
+    the checkpoint ``qweight``.
 
     ``g_idx == k // group_size`` and an act-order ``g_idx`` whose stable sort
     groups every ``group_size`` rows together run on a derived, non-persistent
@@ -386,16 +420,16 @@ def _gptq_operands(module, device: torch.device):
     result = (GIDX_PER_K, qweight, None)
     if group % 8 == 0:
         if torch.equal(gi, natural):
-            tiles = tile_operand(qweight, 1, None, qzeros, 1, scales, n, k, group, device)
-            if tiles is not None:
-                result = (GIDX_UNIFORM, tiles, None)
+            tiled = tile_operand(qweight, 1, None, qzeros, 1, scales, n, k, group, device)
+            if tiled is not None:
+                result = (GIDX_UNIFORM, tiled, None)
         else:
             perm = torch.argsort(gi, stable=True)
             if torch.equal(gi[perm], natural):
                 perm32 = perm.to(torch.int32).contiguous()
-                tiles = tile_operand(qweight, 1, perm32, qzeros, 1, scales, n, k, group, device)
-                if tiles is not None:
-                    result = (GIDX_PERMUTED, tiles, perm32)
+                tiled = tile_operand(qweight, 1, perm32, qzeros, 1, scales, n, k, group, device)
+                if tiled is not None:
+                    result = (GIDX_PERMUTED, tiled, perm32)
     object.__setattr__(module, "_kq_gptq_operands", (key, result))
     return result
 
@@ -414,8 +448,9 @@ def gptq_linear_forward(x: torch.Tensor, module, *, add_bias: bool = True) -> to
     if mode in (GIDX_UNIFORM, GIDX_PERMUTED):
         _native.call(
             "kq_w4a16_tiled_gemm",
-            flat.data_ptr(), _native.dtype_code(flat.dtype), weight.data_ptr(),
-            module.qzeros.data_ptr(), 1, module.scales.data_ptr(), _native.ptr(perm), *common,
+            flat.data_ptr(), _native.dtype_code(flat.dtype), weight.tiles.data_ptr(),
+            _native.ptr(weight.zeros), weight.zero_offset, module.scales.data_ptr(),
+            _native.ptr(perm), *common,
         )
     else:
         g_idx = module.g_idx if module.g_idx.dtype == torch.int32 else module.g_idx.to(torch.int32)

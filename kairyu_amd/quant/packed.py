@@ -208,18 +208,18 @@ class QuantLinearPack:
                     hip._f32(m.weight_scale).expand(m.out_features) if m.weight_scale.numel() == 1
                     else hip._f32(m.weight_scale) for m in mods]).contiguous()
             elif self._scheme == "awq":
-                ops = [hip._awq_operands(m, device) for m in mods]
-                if any(op is None for op in ops):
-                    raise RuntimeError("AWQ pack requires tileable projections")
-                d["zeros"] = torch.cat([z for _, z in ops], dim=1).contiguous()
-                d["scales"] = torch.cat([m.scales for m in mods], dim=1).contiguous()
-                d["perm"], d["zero_offset"], d["mode"] = None, 0, hip.GIDX_UNIFORM
                 # the packed columns tiled as one weight (tiles and their
                 # scale/zero table)
-                d["tiles"] = hip.tile_operand(
-                    torch.cat([m.qweight for m in mods], dim=1).contiguous(), 0, None, d["zeros"], 0,
+                zeros = torch.cat([hip.awq_natural_zeros(m.qzeros, m.out_features, device)
+                                   for m in mods], dim=1).contiguous()
+                d["scales"] = torch.cat([m.scales for m in mods], dim=1).contiguous()
+                d["perm"], d["mode"] = None, hip.GIDX_UNIFORM
+                d["tiled"] = hip.tile_operand(
+                    torch.cat([m.qweight for m in mods], dim=1).contiguous(), 0, None, zeros, 0,
                     d["scales"], sum(self._out_features), mods[0].in_features, mods[0].group_size,
                     device)
+                if d["tiled"] is None:
+                    raise RuntimeError("AWQ pack requires tileable projections")
                 for m in mods:  # the pack holds the only tiled copy
                     m.__dict__.pop("_kq_awq_operands", None)
             else:
@@ -232,12 +232,12 @@ class QuantLinearPack:
                     raise RuntimeError("GPTQ pack requires uniform or act-order groups")
                 if any(mode != ops[0][0] for mode, _, _ in ops):
                     raise RuntimeError("packed GPTQ projections need one group mode")
-                d["zeros"] = torch.cat([m.qzeros for m in mods], dim=1).contiguous()
+                zeros = torch.cat([m.qzeros for m in mods], dim=1).contiguous()
                 d["scales"] = torch.cat([m.scales for m in mods], dim=1).contiguous()
-                d["perm"], d["zero_offset"], d["mode"] = ops[0][2], 1, ops[0][0]
-                d["tiles"] = hip.tile_operand(
+                d["perm"], d["mode"] = ops[0][2], ops[0][0]
+                d["tiled"] = hip.tile_operand(
                     torch.cat([m.qweight for m in mods], dim=1).contiguous(), 1, d["perm"],
-                    d["zeros"], 1, d["scales"], sum(self._out_features), mods[0].in_features,
+                    zeros, 1, d["scales"], sum(self._out_features), mods[0].in_features,
                     mods[0].group_size, device)
                 for m in mods:
                     m.__dict__.pop("_kq_gptq_operands", None)
@@ -285,7 +285,7 @@ class QuantLinearPack:
             ws = hip._w4_workspace(hidden.device, m_rows, n, k, d["mode"])
             _native.call(
                 "kq_w4a16_tiled_gemm", flat.data_ptr(), _native.dtype_code(flat.dtype),
-                d["tiles"].data_ptr(), d["zeros"].data_ptr(), d["zero_offset"],
+                d["tiled"].tiles.data_ptr(), _native.ptr(d["tiled"].zeros), d["tiled"].zero_offset,
                 d["scales"].data_ptr(), _native.ptr(d["perm"]), *bias_args, out.data_ptr(),
                 m_rows, n, k, first.group_size, ws.data_ptr(), ws.numel(), stream,
             )

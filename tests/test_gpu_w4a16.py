@@ -358,50 +358,109 @@ def _untile(tiles: torch.Tensor, n: int, k: int) -> torch.Tensor:
     return q[:k, :n]
 
 
-def _table(tiles: torch.Tensor, n: int, k: int, group: int) -> tuple[torch.Tensor, torch.Tensor]:
-    """Scale/zero table behind the tiles -> (fp16 scales [groups][N], zeros
-    [groups][N] with the zero offset included), test-side inverse: word
-    (u*P + p)*32 + c*2 + h holds group 2p + h of column 16u + c."""
+def _table(op, n: int, k: int, group: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """Scale/zero table behind the tiles of a ``TiledOperand`` -> (fp16
+    scales [groups][N], zeros [groups][N] with the zero offset included),
+    test-side inverse: word (u*P + p)*32 + c*2 + h holds group 2p + h of
+    column 16u + c; with one zero, word (u*P + p)*16 + c holds the scales of
+    groups 2p (low half) and 2p + 1, followed by groups x N/8 zero words."""
     units, stages, groups = -(-n // 16), -(-k // 128), -(-k // group)
     pairs = -(-groups // 2)
-    words = tiles.cpu()[units * stages * 256:]
-    assert words.numel() == units * pairs * 32
-    t = words.reshape(units, pairs, 16, 2).permute(1, 3, 0, 2).reshape(pairs * 2, units * 16)
+    words = op.tiles.cpu()[units * stages * 256:]
+    if op.zeros is None:
+        assert words.numel() == units * pairs * 16 + groups * (n // 8)
+        assert int(words[units * pairs * 16:].abs().sum()) == 0  # zero nibbles
+        t = words[:units * pairs * 16].reshape(units, pairs, 16)
+        t = torch.stack([t & 0xFFFF, (t >> 16) & 0xFFFF], dim=2)  # [u][p][h][c]
+        t = t.permute(1, 2, 0, 3).reshape(pairs * 2, units * 16)
+        zeros = torch.full((groups, n), op.zero_offset, dtype=torch.int32)
+    else:
+        assert words.numel() == units * pairs * 32
+        t = words.reshape(units, pairs, 16, 2).permute(1, 3, 0, 2).reshape(pairs * 2, units * 16)
+        zeros = (t[:groups, :n] >> 16)
+        t = t & 0xFFFF
     pad = t[groups:].abs().sum() + t[:, n:].abs().sum()
     assert int(pad) == 0  # groups past the last, columns past N
-    t = t[:groups, :n]
-    return (t & 0xFFFF).to(torch.int16).view(torch.float16), t >> 16
+    return t[:groups, :n].to(torch.int16).view(torch.float16), zeros
 
 
 def test_tiled_operands_are_exact_and_follow_updates(cuda):
     module = _awq_module(256, 72, group=32, seed=11, random_packed=True).to(cuda)
-    tiles, qz = hip._awq_operands(module, torch.device(cuda))
+    op = hip._awq_operands(module, torch.device(cuda))
+    tiles, qz = op.tiles, op.zeros
     assert tiles.shape == (5 * 2 * 256 + 5 * 4 * 32,)
     assert torch.equal(_untile(tiles, 72, 256), awq_format.unpack_awq(module.qweight.cpu()))
     assert torch.equal(gptq_format.unpack_gptq_cols(qz.cpu()), awq_format.unpack_awq(module.qzeros.cpu()))
     assert int(_natural(tiles, 72, 256)[4, :, 8:].abs().sum()) == 0  # columns past N
-    scales, zeros = _table(tiles, 72, 256, 32)
+    scales, zeros = _table(op, 72, 256, 32)
     assert torch.equal(scales, module.scales.cpu())
     assert torch.equal(zeros, awq_format.unpack_awq(module.qzeros.cpu()))
     module.qweight.copy_(awq_format.pack_awq(torch.randint(0, 16, (256, 72))).to(cuda))
-    tiles2, _ = hip._awq_operands(module, torch.device(cuda))
+    tiles2 = hip._awq_operands(module, torch.device(cuda)).tiles
     assert torch.equal(_untile(tiles2, 72, 256), awq_format.unpack_awq(module.qweight.cpu()))
     # a scale update rebuilds the table
     module.scales.mul_(2)
-    tiles3, _ = hip._awq_operands(module, torch.device(cuda))
-    assert torch.equal(_table(tiles3, 72, 256, 32)[0], module.scales.cpu())
+    op3 = hip._awq_operands(module, torch.device(cuda))
+    assert torch.equal(_table(op3, 72, 256, 32)[0], module.scales.cpu())
     # GPTQ act-order: tile rows follow the stable sort of g_idx; zeros carry +1
     g_idx = (torch.randperm(256, generator=torch.Generator().manual_seed(3)) // 32).to(torch.int32)
     gmod = _gptq_module(256, 64, group=32, seed=12, g_idx=g_idx, random_packed=True)
     gmod.g_idx.copy_(g_idx)
     gmod = gmod.to(cuda)
-    mode, tiles, perm = hip._gptq_operands(gmod, torch.device(cuda))
-    assert mode == hip.GIDX_PERMUTED
+    mode, op, perm = hip._gptq_operands(gmod, torch.device(cuda))
+    assert mode == hip.GIDX_PERMUTED and op.zeros is not None
     q = gptq_format.unpack_gptq_rows(gmod.qweight.cpu())
-    assert torch.equal(_untile(tiles, 64, 256), q[perm.cpu().long()])
-    scales, zeros = _table(tiles, 64, 256, 32)
+    assert torch.equal(_untile(op.tiles, 64, 256), q[perm.cpu().long()])
+    scales, zeros = _table(op, 64, 256, 32)
     assert torch.equal(scales, gmod.scales.cpu())
     assert torch.equal(zeros, gptq_format.unpack_gptq_cols(gmod.qzeros.cpu()) + 1)
+
+
+# One zero for every group and column (symmetric checkpoints): the operand
+# holds scales alone and the decode GEMV reads no zeros.  Shapes: the GEMV
+# with two groups per window (4-byte scale-pair loads), one group per window
+# (2-byte loads), four groups per window, act-order; the skinny kernel
+# (K % 512 != 0) and the prefill GEMM read the operand's zero-nibble words.
+_ONE_ZERO_CASES = [
+    # (fmt, m, k, n, group, dtype, act_order, zero nibble)
+    ("gptq", 16, 4096, 2048, 128, torch.float16, False, 7),
+    ("gptq", 3, 1024, 4096, 1024, torch.bfloat16, True, 7),
+    ("gptq", 5, 2048, 4096, 32, torch.float16, False, 3),
+    ("awq", 1, 4096, 2048, 64, torch.float16, False, 8),
+    ("gptq", 7, 4128, 2056, 128, torch.float16, True, 7),
+    ("gptq", 100, 1024, 392, 128, torch.bfloat16, True, 7),
+    ("awq", 64, 2048, 512, 128, torch.float16, False, 0),
+]
+
+
+@pytest.mark.parametrize("case", _ONE_ZERO_CASES, ids=lambda c: "-".join(map(str, c[:5])) + ("-ao" if c[6] else ""))
+def test_one_zero_operand_matches_oracle(cuda, case):
+    fmt, m, k, n, group, dtype, act_order, nibble = case
+    banner(f"one zero {case}")
+    seed = 7 * m + k + n
+    gen = torch.Generator().manual_seed(seed)
+    groups = -(-k // group)
+    if fmt == "awq":
+        module = _awq_module(k, n, group=group, seed=seed, random_packed=True)
+        module.qzeros.copy_(awq_format.pack_awq(torch.full((groups, n), nibble)))
+    else:
+        g_idx = (torch.randperm(k, generator=gen) // group).to(torch.int32) if act_order else None
+        module = _gptq_module(k, n, group=group, seed=seed, g_idx=g_idx, random_packed=True)
+        if g_idx is not None:
+            module.g_idx.copy_(g_idx)
+        module.qzeros.copy_(gptq_format.pack_gptq_cols(torch.full((groups, n), nibble)))
+    module = module.to(cuda)
+    x = torch.randn(m, k, generator=gen).to(dtype)
+    out = module(x.to(cuda))
+    if fmt == "awq":
+        op = module._kq_awq_operands[1]
+        assert op.zeros is None and op.zero_offset == nibble
+    else:
+        op = module._kq_gptq_operands[1][1]
+        assert op.zeros is None and op.zero_offset == nibble + 1
+    scales, zeros = _table(op, n, k, group)
+    assert torch.equal(scales, module.scales.cpu())
+    check_w4a16(out, module, x, label=f"one zero {case}")
 
 
 def test_tiles_pad_a_partial_last_stage_with_zero_rows(cuda):
@@ -412,13 +471,13 @@ def test_tiles_pad_a_partial_last_stage_with_zero_rows(cuda):
     module = _gptq_module(200, 40, group=40, seed=13, g_idx=g_idx, random_packed=True)
     module.g_idx.copy_(g_idx)
     module = module.to(cuda)
-    mode, tiles, perm = hip._gptq_operands(module, torch.device(cuda))
-    assert mode == hip.GIDX_PERMUTED and tiles.shape == (3 * 2 * 256 + 3 * 3 * 32,)
-    nat = _natural(tiles, 40, 200)
+    mode, op, perm = hip._gptq_operands(module, torch.device(cuda))
+    assert mode == hip.GIDX_PERMUTED and op.tiles.shape == (3 * 2 * 256 + 3 * 3 * 32,)
+    nat = _natural(op.tiles, 40, 200)
     assert int(nat[:, 25:, :].abs().sum()) == 0 and int(nat[2, :, 8:].abs().sum()) == 0
     q = gptq_format.unpack_gptq_rows(module.qweight.cpu())
-    assert torch.equal(_untile(tiles, 40, 200), q[perm.cpu().long()])
-    scales, zeros = _table(tiles, 40, 200, 40)
+    assert torch.equal(_untile(op.tiles, 40, 200), q[perm.cpu().long()])
+    scales, zeros = _table(op, 40, 200, 40)
     assert torch.equal(scales, module.scales.cpu())
     assert torch.equal(zeros, gptq_format.unpack_gptq_cols(module.qzeros.cpu()) + 1)
     x = torch.randn(3, 200, generator=torch.Generator().manual_seed(5)).to(torch.float16)

@@ -43,11 +43,16 @@ def test_exported_symbols_in_dynamic_table():
 
 
 def test_tiled_operand_size():
+    lib = _native.library()
     # tiles (2 units x 2 stages x 256 words) + table (2 units x 3 group pairs x 32)
-    assert _native.library().kq_w4a16_tiled_words(24, 256, 48) == 2 * 2 * 256 + 2 * 3 * 32
-    assert _native.library().kq_w4a16_tiled_words(28672, 4096, 128) == 1792 * 32 * 256 + 1792 * 16 * 32
-    assert _native.library().kq_w4a16_tiled_words(20, 256, 128) == -1  # n % 8
-    assert _native.library().kq_w4a16_tiled_words(24, 256, 12) == -1   # group % 8
+    assert lib.kq_w4a16_tiled_words(24, 256, 48, 0) == 2 * 2 * 256 + 2 * 3 * 32
+    assert lib.kq_w4a16_tiled_words(28672, 4096, 128, 0) == 1792 * 32 * 256 + 1792 * 16 * 32
+    # one zero: scale-only table (16 words per unit and pair) + groups x n/8 zero words
+    assert lib.kq_w4a16_tiled_words(24, 256, 48, 1) == 2 * 2 * 256 + 2 * 3 * 16 + 6 * 3
+    assert (lib.kq_w4a16_tiled_words(28672, 4096, 128, 1)
+            == 1792 * 32 * 256 + 1792 * 16 * 16 + 32 * 3584)
+    assert lib.kq_w4a16_tiled_words(20, 256, 128, 0) == -1  # n % 8
+    assert lib.kq_w4a16_tiled_words(24, 256, 12, 0) == -1   # group % 8
 
 
 def test_bad_shapes_fail_closed_without_touching_the_device():

@@ -22,11 +22,11 @@ SCRATCH_BYTES = 16 << 20
 
 def _operands(module, cuda):
     if hasattr(module, "g_idx"):
-        mode, tiles, perm = hip._gptq_operands(module, cuda)
+        mode, op, perm = hip._gptq_operands(module, cuda)
         assert mode in (hip.GIDX_UNIFORM, hip.GIDX_PERMUTED)
-        return tiles, module.qzeros, 1, perm
-    tiles, zeros = hip._awq_operands(module, cuda)
-    return tiles, zeros, 0, None
+        return op.tiles, op.zeros, op.zero_offset, perm
+    op = hip._awq_operands(module, cuda)
+    return op.tiles, op.zeros, op.zero_offset, None
 
 
 def _run(entry, module, x, cuda):
@@ -35,7 +35,7 @@ def _run(entry, module, x, cuda):
     n = module.out_features
     out = torch.empty(m, n, device=cuda, dtype=x.dtype)
     bias = module.bias
-    args = [x.data_ptr(), _native.dtype_code(x.dtype), tiles.data_ptr(), zeros.data_ptr(), zero_offset,
+    args = [x.data_ptr(), _native.dtype_code(x.dtype), tiles.data_ptr(), _native.ptr(zeros), zero_offset,
             module.scales.data_ptr(), _native.ptr(perm), _native.ptr(bias),
             _native.dtype_code(None if bias is None else bias.dtype), out.data_ptr(), m, n, k,
             module.group_size]
