@@ -1125,6 +1125,40 @@ w4a16_prep_x_kernel(const uint16_t* __restrict__ x, int dtype, int ldx,
   }
 }
 
+// The act-order gather of the decode GEMV (M <= 16, K % 8 == 0, 16-byte
+// aligned x rows): workgroup (c, m) stages row m of x in LDS while the perm
+// slice it gathers is in flight (one memory round trip, where reading perm
+// and then x through it takes two), then gathers 1024 outputs from LDS, 8
+// consecutive ones per thread with one 16-byte store.
+__global__ void __launch_bounds__(128)
+w4a16_prep_x_row_kernel(const uint16_t* __restrict__ x, int dtype, int ldx,
+                        const int32_t* __restrict__ perm, int K, uint16_t* __restrict__ x16) {
+  extern __shared__ __attribute__((aligned(16))) uint16_t srow[];  // K halves
+  const int m = blockIdx.y;
+  const int j0 = blockIdx.x * 1024 + (int)threadIdx.x * 8;
+  const bool mine = j0 < K;
+  i32x4 p0{0, 0, 0, 0}, p1{0, 0, 0, 0};
+  if (mine) {
+    p0 = *(const i32x4*)(perm + j0);
+    p1 = *(const i32x4*)(perm + j0 + 4);
+  }
+  const uint16_t* row = x + (int64_t)m * ldx;
+#pragma unroll 4
+  for (int c = threadIdx.x; c < K / 8; c += 128) *(u32x4*)(srow + 8 * c) = *(const u32x4*)(row + 8 * c);
+  __syncthreads();
+  if (!mine) return;
+  uint16_t h[8];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    h[e] = act_bits(srow[p0[e]], dtype);
+    h[e + 4] = act_bits(srow[p1[e]], dtype);
+  }
+  u32x4 v;
+#pragma unroll
+  for (int d = 0; d < 4; ++d) v[d] = (uint32_t)h[2 * d] | ((uint32_t)h[2 * d + 1] << 16);
+  *(u32x4*)(x16 + (int64_t)m * K + j0) = v;
+}
+
 // AWQ word (k, c) holds column 8c + [0,2,4,6,1,3,5,7][i] in nibble i, so
 // column offset o sits at nibble (o % 2) * 4 + o / 2 (kairyu/quant/awq.py:14-36).
 KQ_DEV uint32_t awq_shift(int o) { return 4u * (uint32_t)((o & 1) * 4 + (o >> 1)); }
@@ -1434,9 +1468,9 @@ static int run_w4(const char* what, int fmt, W4Args a, int gmode, void* workspac
         return KQ_EWORKSPACE;
       }
       uint16_t* x16 = (uint16_t*)workspace;
-      const int64_t threads = ((int64_t)a.M * a.K + 7) / 8;
-      hipLaunchKernelGGL(w4a16_prep_x_kernel, dim3((unsigned)((threads + 63) / 64)), dim3(64), 0,
-                         stream, a.x, a.x_dtype, a.ldx, a.perm, a.M, a.K, x16);
+      // (gv_plan: M <= 16, K <= 4096, K % 512 == 0, 16-byte aligned x rows)
+      hipLaunchKernelGGL(w4a16_prep_x_row_kernel, dim3((unsigned)((a.K + 1023) / 1024), (unsigned)a.M),
+                         dim3(128), (size_t)a.K * 2, stream, a.x, a.x_dtype, a.ldx, a.perm, a.K, x16);
       a.x = x16;
       a.ldx = a.K;
       xdt = kXF16;
