@@ -27,7 +27,9 @@ C5), each row with
 The top-level ``cpu_baseline`` is the headline row's.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-sweep]
-                       [--no-cpu] [--no-headline] [--only SUBSTRING]
+                       [--no-cpu] [--no-headline] [--only SUBSTRING[|SUBSTRING]]
+       python bench.py --floors            (empty kernel per graph step)
+       python bench.py --copy-calibration  (256 MiB copies for counter scaling)
 """
 
 from __future__ import annotations
@@ -457,6 +459,8 @@ def main() -> int:
                         help="skip the headline measurement (profiling one sweep row)")
     parser.add_argument("--only", default=None,
                         help="substring filter for sweep entries ('a|b': either)")
+    parser.add_argument("--floors", action="store_true",
+                        help="only time an empty kernel per step of a HIP graph (the launch floor)")
     parser.add_argument("--copy-calibration", action="store_true",
                         help="only run 256 MiB device-to-device copies (HBM counter calibration)")
     args = parser.parse_args()
@@ -471,6 +475,13 @@ def main() -> int:
 
     baseline = json.loads((ROOT / "BASELINE.json").read_text())
     torch.cuda.set_device(0)
+    if args.floors:
+        # torch's spin kernel with a zero cycle count: a launch that does no
+        # work, 100 per captured graph
+        clock_warmup(0.5)
+        ms = _graph_ms(lambda i: torch.cuda._sleep(0), 1, 100)
+        print(json.dumps({"empty_kernel_per_graph_step_us": round(ms * 1e3, 3)}), flush=True)
+        return 0
     if args.copy_calibration:
         # a plain copy of known size: FETCH_SIZE / WRITE_SIZE per dispatch of
         # this kernel calibrate the counters against 268435456 bytes each way
