@@ -209,6 +209,34 @@ int kq_w4a16_tiled_gemm(const void* x, int x_dtype, const int32_t* tiles, const 
                         int bias_dtype, void* out, int64_t m, int64_t n, int64_t k, int group_size,
                         void* workspace, size_t workspace_bytes, void* stream);
 
+/* Packed gate/up projection with SwiGLU: out[m][n] = silu(gate) * up for
+ * n < i_width, computed as torch does on fp16/bf16 tensors (gate and up
+ * rounded to x_dtype, silu = g / (1 + exp(-g)) in fp32 rounded, the product
+ * rounded; kairyu/models/layers.py:243-244 `silu(gate_proj(x)) *
+ * up_proj(x)`).  `tiles` is kq_w4a16_tile_weights' operand over 2 * i_width
+ * columns in which 16-column blocks of gate (block b: gate columns 16b..16b+15)
+ * and up alternate; qzeros / scales / bias (nullable) are in that column
+ * order too.  Decode shapes (the GEMV's conditions, at most 8 column blocks
+ * per CU) apply SwiGLU in the GEMV's epilogue; other shapes run the tiled
+ * GEMM into the workspace and one elementwise pass
+ * (kq_w4a16_swiglu_workspace_size bytes).  No reference counterpart: the
+ * reference packs gate/up only for dense and NVFP4 projections
+ * (kairyu/models/packed_linear.py:58-149) and applies SwiGLU separately. */
+int kq_w4a16_tiled_swiglu_gemm(const void* x, int x_dtype, const int32_t* tiles,
+                               const int32_t* qzeros, int zero_offset, const void* scales,
+                               const int32_t* perm, const void* bias, int bias_dtype, void* out,
+                               int64_t m, int64_t i_width, int64_t k, int group_size,
+                               void* workspace, size_t workspace_bytes, void* stream);
+size_t kq_w4a16_swiglu_workspace_size(int64_t m, int64_t i_width, int64_t k, int gidx_mode);
+
+/* dst[m][n] = silu(gate) * up (as kq_w4a16_tiled_swiglu_gemm) from src
+ * [m][2 * i_width] (row stride ld_src elements, dtype fp16 or bf16): gate
+ * column n and up column i_width + n, or with `interleaved` 16-column blocks
+ * of gate and up alternating.  SwiGLU of a packed W8A8 gate/up output
+ * (kairyu/models/layers.py:243-244). */
+int kq_swiglu(const void* src, int64_t ld_src, int interleaved, int dtype, void* dst, int64_t m,
+              int64_t i_width, void* stream);
+
 /* Allocation-free form of kq_w4a16_tiled_gemm, same arguments and results
  * except `workspace`: the call's scratch (act-order activation gather, the
  * prefill GEMM's staged activations, split-K partial sums) lives in a fixed

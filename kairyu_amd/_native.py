@@ -68,6 +68,11 @@ _SIGNATURES: dict[str, list] = {
         _P, _I, _P, _P, _I, _P, _P, _P, _I, _P, _I64, _I64, _I64, _I, _P,
     ],
     "kq_w4a16_workspace_size": [_I64, _I64, _I64, _I],
+    "kq_w4a16_tiled_swiglu_gemm": [
+        _P, _I, _P, _P, _I, _P, _P, _P, _I, _P, _I64, _I64, _I64, _I, _P, _SZ, _P,
+    ],
+    "kq_w4a16_swiglu_workspace_size": [_I64, _I64, _I64, _I],
+    "kq_swiglu": [_P, _I64, _I, _I, _P, _I64, _I64, _P],
     "kq_moe_route_topk": [_P, _I, _I64, _I64, _I, _I, _P, _P, _P],
     "kq_act_quant_fp8_blocks": [_P, _I, _I64, _I64, _I64, _P, _P, _P],
     "kq_block_fp8_gemm": [_P, _P, _P, _P, _P, _I, _P, _I, _I64, _I64, _I64, _P],
@@ -101,6 +106,7 @@ def _load() -> ctypes.CDLL:
             fn.argtypes = argtypes
             fn.restype = {"kq_last_error": ctypes.c_char_p,
                           "kq_w4a16_workspace_size": ctypes.c_size_t,
+                          "kq_w4a16_swiglu_workspace_size": ctypes.c_size_t,
                           "kq_w4a16_tiled_words": ctypes.c_int64,
                           "kq_w8a8_workspace_size": ctypes.c_size_t,
                           "kq_w8a8_linear_workspace_size": ctypes.c_size_t,

@@ -113,6 +113,7 @@ struct W4Args {
   uint32_t zoff;         // added to stored zero nibbles (GPTQ 1, natural-order AWQ 0)
   int layout;            // kLayoutRows (qweight [K/8][N]) or kLayoutTiles
   int zu;                // tiles built with one zero for every group and column (zoff)
+  int swiglu;            // N = 2I gate/up columns interleaved by 16; out [M][I] = silu(gate) * up
 };
 
 KQ_DEV int group_of(const W4Args& a, int k) {
@@ -201,6 +202,20 @@ KQ_DEV uint32_t and_or(uint32_t x, uint32_t mask, uint32_t magic) {
   uint32_t r;
   asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(x), "s"(mask), "v"(magic));
   return r;
+}
+
+// silu(gate) * up as torch computes it on fp16 / bf16 tensors (layers.py
+// `silu(gate_proj(x)) * up_proj(x)`, kairyu/models/layers.py:243-244): gate and
+// up rounded to the activation dtype, silu in fp32 (x / (1 + exp(-x)), IEEE
+// division) rounded, the product in fp32 rounded.
+KQ_DEV float round_act(float v, int dtype) {
+  if (dtype == KQ_DTYPE_BF16) return (float)(__bf16)v;
+  return (float)(_Float16)v;
+}
+KQ_DEV uint16_t swiglu_bits(float gate, float up, int dtype) {
+  const float g = round_act(gate, dtype), u = round_act(up, dtype);
+  const float s = round_act(__fdiv_rn(g, __fadd_rn(1.0f, expf(-g))), dtype);
+  return f32_to_out(__fmul_rn(s, u), dtype);
 }
 
 // Nibble pairs of a 32-bit word as fp16 (base + q) pairs: OR-ing the nibble at
@@ -715,7 +730,10 @@ KQ_DEV f32x4 gv_compute(const W4Args& a, const NibbleConsts& nc, uint32_t zsh,
 // slots.  kGvRounds: several rounds of U blocks.
 enum { kGvRounds = 0, kGvOne = 1, kGvSingle = 2, kGvShort = 3 };
 
-template <int XDT, int S, int SPG, int LAYOUT, int MODE>
+// SWIGLU (one-round mode, tiled operand over gate/up columns interleaved by
+// 16): workgroup shares are whole gate/up unit pairs and the epilogue writes
+// silu(gate) * up into out [M][N/2].
+template <int XDT, int S, int SPG, int LAYOUT, int MODE, bool SWIGLU = false>
 __global__ void __launch_bounds__(64 * kGvWaves)
 w4a16_gemv_kernel(W4Args a, GvPlan p) {
   constexpr bool ONE = MODE != kGvRounds;
@@ -734,11 +752,14 @@ w4a16_gemv_kernel(W4Args a, GvPlan p) {
   const int lane = lane_id();
   const int wave = __builtin_amdgcn_readfirstlane(wave_id());
   const int j = lane & 15, kb = lane >> 4;
-  // balanced unit range of this workgroup
-  const int base = p.units / p.wgs, rem = p.units % p.wgs;
+  // balanced unit range of this workgroup (SWIGLU: balanced in unit pairs)
+  constexpr int kUnitsPer = SWIGLU ? 2 : 1;
+  const int items = p.units / kUnitsPer;
+  const int base = items / p.wgs, rem = items % p.wgs;
   const int bid = blockIdx.x;
-  const int u0 = bid * base + min(bid, rem);
-  const int ncb = base + (bid < rem ? 1 : 0);
+  const int u0 = (bid * base + min(bid, rem)) * kUnitsPer;
+  const int ncb = (base + (bid < rem ? 1 : 0)) * kUnitsPer;
+  static_assert(!SWIGLU || (MODE == kGvOne && U % 2 == 0), "SwiGLU GEMV runs one round of unit pairs");
 
   NibbleConsts nc;
   nc.m0 = __builtin_amdgcn_readfirstlane(0x000f000fu);
@@ -829,6 +850,30 @@ w4a16_gemv_kernel(W4Args a, GvPlan p) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) red(wave, q * 4 + r)[lane] = acc[q][r];
     __syncthreads();
+    if constexpr (SWIGLU) {
+      // one gate/up pair per thread: unit 2pp holds gate columns, 2pp + 1 up
+      const int width = a.N / 2;
+      for (int i = wave; i < (U / 2) * 4; i += kGvWaves) {
+        const int pp = i >> 2, r = i & 3, qg = 2 * pp, qu = qg + 1;
+        if (qu >= ncb) continue;
+        float g = red(0, qg * 4 + r)[lane], u = red(0, qu * 4 + r)[lane];
+#pragma unroll
+        for (int w = 1; w < kGvWaves; ++w) {
+          g = __fadd_rn(g, red(w, qg * 4 + r)[lane]);
+          u = __fadd_rn(u, red(w, qu * 4 + r)[lane]);
+        }
+        const int m = 4 * kb + r;
+        const int col = (u0 + qg) * 16 + j;  // gate column of the interleaved operand
+        if (m < a.M) {
+          if (a.bias_dtype != KQ_DTYPE_NONE) {
+            g = __fadd_rn(g, load_as_f32(a.bias, a.bias_dtype, col));
+            u = __fadd_rn(u, load_as_f32(a.bias, a.bias_dtype, col + 16));
+          }
+          a.out[(int64_t)m * width + ((u0 + qg) >> 1) * 16 + j] = swiglu_bits(g, u, a.out_dtype);
+        }
+      }
+      return;
+    }
     for (int i = wave; i < U * 4; i += kGvWaves) {   // one output per thread
       const int q = i >> 2, r = i & 3;
       if (q0 + q >= ncb) continue;
@@ -1159,6 +1204,26 @@ w4a16_prep_x_row_kernel(const uint16_t* __restrict__ x, int dtype, int ldx,
   *(u32x4*)(x16 + (int64_t)m * K + j0) = v;
 }
 
+// out[m][n] = silu(gate) * up (swiglu_bits) from a [M][2I] gate/up output:
+// gate column n and up column I + n, or (interleaved) the 16-column blocks of
+// gate and up alternating.  Two outputs per thread.
+__global__ void __launch_bounds__(256)
+swiglu_kernel(const uint16_t* __restrict__ src, int64_t ld_src, int interleaved, int dtype,
+              uint16_t* __restrict__ dst, int64_t M, int64_t I) {
+  const int64_t idx = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 2;
+  if (idx >= M * I) return;
+  const int64_t m = idx / I, n = idx % I;  // I even: both outputs in row m
+#pragma unroll
+  for (int e = 0; e < 2; ++e) {
+    const int64_t c = n + e;
+    const int64_t gc = interleaved ? (c >> 4) * 32 + (c & 15) : c;
+    const int64_t uc = interleaved ? gc + 16 : I + c;
+    const float g = load_as_f32(src + m * ld_src, dtype, gc);
+    const float u = load_as_f32(src + m * ld_src, dtype, uc);
+    dst[m * I + c] = swiglu_bits(g, u, dtype);
+  }
+}
+
 // AWQ word (k, c) holds column 8c + [0,2,4,6,1,3,5,7][i] in nibble i, so
 // column offset o sits at nibble (o % 2) * 4 + o / 2 (kairyu/quant/awq.py:14-36).
 KQ_DEV uint32_t awq_shift(int o) { return 4u * (uint32_t)((o & 1) * 4 + (o >> 1)); }
@@ -1343,6 +1408,16 @@ static bool gv_plan(const W4Args& a, int fmt, int gmode, GvPlan* p, int* S, int*
   const int cus = device_cus();
   p->units = (a.N + 15) / 16;
   if (p->units * 2 < cus) return false;
+  if (a.swiglu) {
+    // whole gate/up unit pairs per workgroup, one round (at most 8 units)
+    if (a.layout != kLayoutTiles || (a.N % 32) != 0) return false;
+    const int pairs = p->units / 2;
+    p->wgs = std::min(cus, pairs);
+    if (2 * ((pairs + p->wgs - 1) / p->wgs) > 8) return false;
+    *S = s;
+    *SPG = tspg;
+    return true;
+  }
   p->wgs = std::min(cus, p->units);
   *S = s;
   *SPG = tspg;
@@ -1386,6 +1461,12 @@ static void launch_gv_s(const W4Args& a, const GvPlan& p, int layout, hipStream_
                                                        : kGvRounds;
   const dim3 g(p.wgs), b(64 * kGvWaves);
 #define KQ_GV_LAUNCH(L, M) hipLaunchKernelGGL((w4a16_gemv_kernel<XDT, S, SPG, L, M>), g, b, 0, st, a, p)
+  if (a.swiglu) {
+    // (gv_plan: tiled operand, at most kOneRound units per workgroup)
+    if (a.zu) hipLaunchKernelGGL((w4a16_gemv_kernel<XDT, S, SPG, kLayoutTilesZu, kGvOne, true>), g, b, 0, st, a, p);
+    else hipLaunchKernelGGL((w4a16_gemv_kernel<XDT, S, SPG, kLayoutTiles, kGvOne, true>), g, b, 0, st, a, p);
+    return;
+  }
   if (layout == kLayoutTiles && a.zu) {
     if (mode == kGvSingle) KQ_GV_LAUNCH(kLayoutTilesZu, kGvSingle);
     else if (mode == kGvShort) KQ_GV_LAUNCH(kLayoutTilesZu, kGvShort);
@@ -1549,6 +1630,17 @@ extern "C" size_t kq_w4a16_workspace_size(int64_t m, int64_t n, int64_t k, int g
   return std::max(p.x16_bytes + p.partial_bytes, x16);
 }
 
+// Offset of the SwiGLU two-pass intermediate: after the GEMM's own scratch.
+static size_t swiglu_ws_offset(int64_t m, int64_t n, int64_t k, int gmode) {
+  return (kq_w4a16_workspace_size(m, n, k, gmode) + 255) / 256 * 256;
+}
+
+extern "C" size_t kq_w4a16_swiglu_workspace_size(int64_t m, int64_t i_width, int64_t k,
+                                                 int gidx_mode) {
+  if (m <= 0 || i_width <= 0 || k <= 0) return 0;
+  return swiglu_ws_offset(m, 2 * i_width, k, gidx_mode) + (size_t)m * (size_t)(2 * i_width) * 2;
+}
+
 extern "C" int kq_w4a16_awq_gemm(const void* x, int x_dtype, const int32_t* qweight,
                                  const int32_t* qzeros, const void* scales, const void* bias,
                                  int bias_dtype, void* out, int64_t m, int64_t n, int64_t k,
@@ -1652,6 +1744,72 @@ extern "C" int kq_w4a16_tiled_gemm(const void* x, int x_dtype, const int32_t* ti
   if (status != KQ_OK) return status;
   return run_w4("kq_w4a16_tiled_gemm", kGptq, a, perm ? kGroupsPermuted : kGroupsUniform,
                 workspace, workspace_bytes, (hipStream_t)stream);
+}
+
+// Packed gate/up projection with SwiGLU (layers.py:243-244): the tiled operand
+// covers 2I columns, 16-column blocks of gate and up alternating.  Decode
+// shapes run the GEMV with the SwiGLU epilogue; others the tiled GEMM into
+// the workspace (after its own scratch) and the elementwise pass.
+static size_t swiglu_ws_offset(int64_t m, int64_t n, int64_t k, int gmode);
+
+extern "C" int kq_w4a16_tiled_swiglu_gemm(const void* x, int x_dtype, const int32_t* tiles,
+                                          const int32_t* qzeros, int zero_offset,
+                                          const void* scales, const int32_t* perm,
+                                          const void* bias, int bias_dtype, void* out, int64_t m,
+                                          int64_t i_width, int64_t k, int group_size,
+                                          void* workspace, size_t workspace_bytes, void* stream) {
+  const char* what = "kq_w4a16_tiled_swiglu_gemm";
+  if (i_width < 16 || (i_width % 16) != 0 || i_width > 0x3fffffff) {
+    set_error("%s: the activation width must be a positive multiple of 16 (got %lld)", what,
+              (long long)i_width);
+    return KQ_EINVAL;
+  }
+  const int64_t n = 2 * i_width;
+  W4Args a{};
+  int status = tiled_args(what, x, x_dtype, tiles, qzeros, zero_offset, scales, perm, bias,
+                          bias_dtype, out, m, n, k, group_size, &a);
+  if (status != KQ_OK) return status;
+  const int gmode = perm ? kGroupsPermuted : kGroupsUniform;
+  GvPlan gp{};
+  int s_ = 0, spg_ = 0;
+  a.swiglu = 1;
+  if (a.M > 0 && gv_plan(a, kGptq, gmode, &gp, &s_, &spg_))
+    return run_w4(what, kGptq, a, gmode, workspace, workspace_bytes, (hipStream_t)stream);
+  // two passes: [m][2I] in the activation dtype after the GEMM's scratch
+  a.swiglu = 0;
+  if (m == 0) return KQ_OK;
+  const size_t off = swiglu_ws_offset(m, n, k, gmode);
+  const size_t need = off + (size_t)m * (size_t)n * 2;
+  if (workspace == nullptr || workspace_bytes < need) {
+    set_error("%s: workspace of %zu bytes is smaller than the %zu bytes this call needs", what,
+              workspace ? workspace_bytes : (size_t)0, need);
+    return KQ_EWORKSPACE;
+  }
+  uint16_t* mid = (uint16_t*)((char*)workspace + off);
+  a.out = mid;
+  status = run_w4(what, kGptq, a, gmode, workspace, off, (hipStream_t)stream);
+  if (status != KQ_OK) return status;
+  const int64_t pairs = m * i_width / 2;
+  hipLaunchKernelGGL(swiglu_kernel, dim3((unsigned)((pairs + 255) / 256)), dim3(256), 0,
+                     (hipStream_t)stream, (const uint16_t*)mid, n, 1, x_dtype, (uint16_t*)out, m,
+                     i_width);
+  return check_launch(what);
+}
+
+extern "C" int kq_swiglu(const void* src, int64_t ld_src, int interleaved, int dtype, void* dst,
+                         int64_t m, int64_t i_width, void* stream) {
+  if (m < 0 || i_width < 2 || (i_width % 2) != 0 || ld_src < 2 * i_width ||
+      (interleaved && (i_width % 16) != 0) || (dtype != KQ_DTYPE_F16 && dtype != KQ_DTYPE_BF16)) {
+    set_error("kq_swiglu: bad arguments m=%lld i=%lld ld=%lld dtype=%d", (long long)m,
+              (long long)i_width, (long long)ld_src, dtype);
+    return KQ_EINVAL;
+  }
+  if (m == 0) return KQ_OK;
+  const int64_t pairs = m * i_width / 2;
+  hipLaunchKernelGGL(swiglu_kernel, dim3((unsigned)((pairs + 255) / 256)), dim3(256), 0,
+                     (hipStream_t)stream, (const uint16_t*)src, ld_src, interleaved, dtype,
+                     (uint16_t*)dst, m, i_width);
+  return check_launch("kq_swiglu");
 }
 
 // ---------------------------------------------------------------------------

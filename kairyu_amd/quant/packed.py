@@ -19,6 +19,12 @@ for this package's quantized formats:
   are.  GPTQ projections pack when they share one ``g_idx`` (uniform groups,
   or one act-order permutation, so one activation gather serves all).
 
+``swiglu(x)`` of a (gate, up) pack returns ``silu(gate(x)) * up(x)``, the
+reference MLP's activation (``kairyu/models/layers.py:243-244``), with
+torch's fp16 / bf16 roundings; for W4A16 in one call whose decode GEMV applies
+SwiGLU in its epilogue (gate and up 16-column blocks interleaved in a derived
+tiled operand), for W8A8 as the packed GEMM plus one elementwise pass.
+
 ``create`` returns ``None`` for anything it cannot pack exactly (mixed
 formats, in-features, devices, biases, group sizes, static input scales,
 ``g_idx``; hooked or re-bound modules; ``N`` not a multiple of 16 for the
@@ -56,7 +62,8 @@ def _key(tensors) -> tuple:
 class QuantLinearPack:
     """Several same-format quantized projections executed as one."""
 
-    __slots__ = ("_projections", "_scheme", "_out_features", "_weight", "_derived", "_derived_key")
+    __slots__ = ("_projections", "_scheme", "_out_features", "_weight", "_derived", "_derived_key",
+                 "_swiglu", "_swiglu_key")
 
     def __init__(self, projections: tuple[nn.Module, ...], scheme: str,
                  weight: torch.Tensor | None) -> None:
@@ -66,6 +73,8 @@ class QuantLinearPack:
         self._weight = weight
         self._derived: dict[str, torch.Tensor | int | None] | None = None
         self._derived_key: tuple | None = None
+        self._swiglu: dict | None = None
+        self._swiglu_key: tuple | None = None
 
     # ------------------------------------------------------------ creation
     @classmethod
@@ -250,6 +259,98 @@ class QuantLinearPack:
             raise RuntimeError("canonical projection buffers no longer match the packed storage")
         if hidden.device.type != "cuda":
             return tuple(m(hidden) for m in self._projections)
+        out = self._packed(hidden)
+        lead = hidden.shape[:-1]
+        return tuple(part.reshape(*lead, part.shape[-1]) for part in out.split(self._out_features, -1))
+
+    def swiglu(self, hidden: torch.Tensor) -> torch.Tensor:
+        """``silu(gate(x)) * up(x)`` of a (gate, up) pack, as the reference's
+        MLP computes it (``kairyu/models/layers.py:243-244``) with torch's
+        roundings on fp16/bf16 tensors.  W4A16 packs run one call whose decode
+        GEMV applies SwiGLU in its epilogue (gate and up columns interleaved
+        by 16 in a derived tiled operand, ``kq_w4a16_tiled_swiglu_gemm``);
+        W8A8 packs run the packed GEMM and one elementwise pass
+        (``kq_swiglu``)."""
+
+        if len(self._projections) != 2 or self._out_features[0] != self._out_features[1]:
+            raise ValueError("swiglu needs a (gate, up) pack of equal widths")
+        if not self.is_current():
+            raise RuntimeError("canonical projection buffers no longer match the packed storage")
+        gate, up = self._projections
+        if hidden.device.type != "cuda":
+            return nn.functional.silu(gate(hidden)) * up(hidden)
+        from kairyu_amd import _native
+        from kairyu_amd.kernels import quant_gemm_hip as hip
+
+        width = self._out_features[0]
+        lead = hidden.shape[:-1]
+        stream = _native.stream_handle(hidden.device)
+        if self._scheme in ("fp8", "int8"):
+            both = self._packed(hidden)
+            act = torch.empty((both.shape[0], width), device=hidden.device, dtype=hidden.dtype)
+            _native.call("kq_swiglu", both.data_ptr(), both.stride(0), 0,
+                         _native.dtype_code(hidden.dtype), act.data_ptr(), both.shape[0], width, stream)
+            return act.reshape(*lead, width)
+        flat, _ = hip._prepare(hidden, gate, self._scheme, allocate_output=False)
+        hip._validate_layout(up, self._scheme)
+        d = self._swiglu_operands(hidden.device)
+        m_rows, k = flat.shape
+        act = torch.empty((m_rows, width), device=hidden.device, dtype=hidden.dtype)
+        bias = d["bias"] if gate._add_local_bias() else None
+        ws = hip._workspace(hidden.device, int(_native.library().kq_w4a16_swiglu_workspace_size(
+            m_rows, width, k, d["mode"])))
+        _native.call(
+            "kq_w4a16_tiled_swiglu_gemm", flat.data_ptr(), _native.dtype_code(flat.dtype),
+            d["tiled"].tiles.data_ptr(), _native.ptr(d["tiled"].zeros), d["tiled"].zero_offset,
+            d["scales"].data_ptr(), _native.ptr(d["perm"]), _native.ptr(bias),
+            _native.dtype_code(None if bias is None else bias.dtype), act.data_ptr(), m_rows, width,
+            k, gate.group_size, ws.data_ptr(), ws.numel(), stream,
+        )
+        return act.reshape(*lead, width)
+
+    def _swiglu_operands(self, device: torch.device) -> dict:
+        """The (gate, up) pair tiled as one weight whose 16-column blocks of
+        gate and up alternate (the SwiGLU epilogue holds both halves of a
+        pair), with its scales, zeros and bias in the same column order."""
+
+        key = (_key(self._sources()), str(device))
+        if self._swiglu is not None and self._swiglu_key == key:
+            return self._swiglu
+        from kairyu_amd.kernels import quant_gemm_hip as hip
+
+        hip._refuse_under_capture(self._scheme.upper())
+        gate, up = self._projections
+
+        def mix(a: torch.Tensor, b: torch.Tensor, block: int) -> torch.Tensor:
+            # column blocks of a and b alternating: [a0, b0, a1, b1, ...]
+            a2, b2 = a.reshape(a.shape[0], -1, block), b.reshape(b.shape[0], -1, block)
+            return torch.stack([a2, b2], dim=2).reshape(a.shape[0], -1).contiguous()
+
+        d: dict = {"bias": None}
+        with torch.no_grad():
+            if gate.bias is not None:
+                d["bias"] = mix(gate.bias.detach().reshape(1, -1), up.bias.detach().reshape(1, -1), 16).reshape(-1)
+            d["scales"] = mix(gate.scales, up.scales, 16)
+            if self._scheme == "awq":
+                zeros = mix(hip.awq_natural_zeros(gate.qzeros, gate.out_features, device),
+                            hip.awq_natural_zeros(up.qzeros, up.out_features, device), 2)
+                qweight, fmt, zoff, d["perm"], d["mode"] = mix(gate.qweight, up.qweight, 2), 0, 0, None, hip.GIDX_UNIFORM
+            else:
+                mode, _, perm = hip._gptq_operands(gate, device)
+                if mode == hip.GIDX_PER_K:
+                    raise RuntimeError("GPTQ swiglu pack requires uniform or act-order groups")
+                zeros = mix(gate.qzeros, up.qzeros, 2)
+                qweight, fmt, zoff, d["perm"], d["mode"] = mix(gate.qweight, up.qweight, 16), 1, 1, perm, mode
+            d["tiled"] = hip.tile_operand(qweight, fmt, d["perm"], zeros, zoff, d["scales"],
+                                          2 * gate.out_features, gate.in_features, gate.group_size, device)
+            if d["tiled"] is None:
+                raise RuntimeError("swiglu pack requires tileable projections")
+        self._swiglu, self._swiglu_key = d, key
+        return d
+
+    def _packed(self, hidden: torch.Tensor) -> torch.Tensor:
+        """The projections' outputs side by side, [rows, sum(out_features)]."""
+
         from kairyu_amd import _native
         from kairyu_amd.kernels import quant_gemm_hip as hip
 
@@ -289,5 +390,4 @@ class QuantLinearPack:
                 d["scales"].data_ptr(), _native.ptr(d["perm"]), *bias_args, out.data_ptr(),
                 m_rows, n, k, first.group_size, ws.data_ptr(), ws.numel(), stream,
             )
-        lead = hidden.shape[:-1]
-        return tuple(part.reshape(*lead, part.shape[-1]) for part in out.split(self._out_features, -1))
+        return out

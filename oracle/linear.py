@@ -172,3 +172,19 @@ def fp8_forward_fast(x_bits, x_scale, w_decoded, w_scale, out_dtype="bfloat16") 
     acc = e4m3_decode(x_bits) @ np.asarray(w_decoded, np.float32).T
     ws = np.asarray(w_scale, np.float32).reshape(1, -1)
     return to_dtype(((acc * x_scale).astype(np.float32) * ws).astype(np.float32), out_dtype)
+
+
+def swiglu_reference(gate_pre, up_pre, dtype: str) -> np.ndarray:
+    """``silu(gate) * up`` as the reference MLP computes it on fp16 / bf16
+    tensors (``kairyu/models/layers.py:243-244``:
+    ``down_proj(silu(gate_proj(h)) * up_proj(h))``): the projections' outputs
+    are tensors of the activation dtype, torch's silu evaluates
+    ``x / (1 + exp(-x))`` in fp32 and rounds, and the product is formed in
+    fp32 and rounded.  ``gate_pre`` / ``up_pre``: the projections' values
+    before their final cast."""
+
+    g = to_dtype(np.asarray(gate_pre, np.float64).astype(np.float32), dtype).astype(np.float32)
+    u = to_dtype(np.asarray(up_pre, np.float64).astype(np.float32), dtype).astype(np.float32)
+    with np.errstate(over="ignore"):
+        s = to_dtype(g / (np.float32(1.0) + np.exp(-g)), dtype).astype(np.float32)
+    return to_dtype(s * u, dtype)

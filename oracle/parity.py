@@ -36,7 +36,7 @@ from __future__ import annotations
 
 import numpy as np
 
-from .linear import error_metrics
+from .linear import error_metrics, swiglu_reference
 
 U32 = 2.0 ** -24
 _MANTISSA = {"float16": 10, "bfloat16": 7, "float32": 23}
@@ -156,3 +156,27 @@ def moe_check(actual, expected, dtype: str, ulps: float = 8.0, frac: float = 0.9
     if not metrics["ok"]:
         metrics["why"] = f"{within:.4f} within {ulps} ulp (need {frac}), rel_rmse {metrics['rel_rmse']:.3e}"
     return metrics
+
+
+def swiglu_check(actual, gate_pre, up_pre, dtype: str, gate_slack=0.0, up_slack=0.0,
+                 rmse_factor: float = 3.0) -> dict:
+    """``silu(gate) * up`` outputs against ``oracle.linear.swiglu_reference``
+    of the projections' exact values.  The device's gate and up may round to
+    a neighbour of the oracle's (their accumulation slack moves a value near a
+    rounding boundary), so the bound propagates one ulp plus the slack of
+    each input through the function: ``|silu'(g) u| (ulp(g) + gate_slack) +
+    |silu(g)| (ulp(u) + up_slack)``, plus one ulp of the output and of silu's
+    own rounding (times |u|); and the relative RMSE stays within
+    ``rmse_factor`` x the output's rounding RMSE."""
+
+    out = np.asarray(actual, np.float64)
+    ref = np.asarray(swiglu_reference(gate_pre, up_pre, dtype), np.float64)
+    gp = np.asarray(gate_pre, np.float64)
+    up = np.asarray(up_pre, np.float64)
+    sig = 1.0 / (1.0 + np.exp(-np.clip(gp, -80.0, 80.0)))
+    silu = gp * sig
+    dsilu = sig * (1.0 + gp * (1.0 - sig))
+    eg = ulp(gp, dtype) + np.asarray(gate_slack, np.float64)
+    eu = ulp(up, dtype) + np.asarray(up_slack, np.float64)
+    slack = np.abs(dsilu * up) * eg + np.abs(silu) * eu + ulp(silu, dtype) * np.abs(up)
+    return ulp_check(out, ref, dtype, slack, ulps=1.0, rmse_factor=rmse_factor)

@@ -10,7 +10,7 @@ import torch
 
 from oracle import linear as olinear
 from oracle.parity import (  # noqa: F401  (re-exported for the tests)
-    U32, e4m3_mfma_slack, fp16_mfma_slack, moe_check, rounding_rel_rmse, ulp, ulp_check)
+    U32, e4m3_mfma_slack, fp16_mfma_slack, moe_check, rounding_rel_rmse, swiglu_check, ulp, ulp_check)
 
 DTYPE_NAME = {torch.float16: "float16", torch.bfloat16: "bfloat16", torch.float32: "float32"}
 
@@ -135,4 +135,55 @@ def assert_moe_close(actual, expected, dtype: str, label: str = "", **criteria) 
           f"{metrics['within']:.5f} normwise {metrics['normwise_max']:.3e} "
           f"rel_rmse {metrics['rel_rmse']:.3e}", flush=True)
     assert metrics["ok"], f"{label} {metrics}"
+    return metrics
+
+
+def projection_pre(module, x: torch.Tensor, add_bias: bool = True) -> tuple[np.ndarray, np.ndarray]:
+    """(value before the final cast, accumulation slack) of a quantized
+    projection on ``x`` as the oracle computes it: W4A16 and FP8 with their
+    MFMA slack, INT8 exact (``((acc * xs) * ws) + bias`` in fp32, no slack)."""
+
+    from kairyu_amd.quant.linear import AwqLinear, Fp8Linear, GptqLinear, Int8Linear
+    from oracle.numerics import e4m3_decode
+
+    xs = np32(x.reshape(-1, x.shape[-1]))
+    bias = _bias_of(module, add_bias)
+    xd = DTYPE_NAME[x.dtype]
+    if isinstance(module, AwqLinear):
+        pre, terms = olinear.awq_reference(xs, module.qweight.cpu().numpy(), module.qzeros.cpu().numpy(),
+                                           np32(module.scales), module.group_size, xd, bias)
+        return pre, fp16_mfma_slack(terms, module.in_features)
+    if isinstance(module, GptqLinear):
+        pre, terms = olinear.gptq_reference(xs, module.qweight.cpu().numpy(), module.qzeros.cpu().numpy(),
+                                            np32(module.scales), module.g_idx.cpu().numpy(), xd, bias)
+        return pre, fp16_mfma_slack(terms, module.in_features)
+    if isinstance(module, Int8Linear):
+        _, _, x_scale, acc = olinear.int8_forward(xs, module.weight.cpu().numpy(), np32(module.weight_scale),
+                                                   None)
+        ws = np32(module.weight_scale).reshape(1, -1)
+        pre = (acc.astype(np.float32) * x_scale).astype(np.float32) * ws
+        if bias is not None:
+            pre = (pre + bias.reshape(1, -1)).astype(np.float32)
+        return pre.astype(np.float64), np.zeros(pre.shape)
+    assert isinstance(module, Fp8Linear)
+    w_bits, w_scale = bits(module.weight), np32(module.weight_scale)
+    _, x_bits, x_scale, pre = olinear.fp8_forward(xs, w_bits, w_scale, bias)
+    terms = olinear.fp8_abs_terms(x_bits, w_bits, x_scale, w_scale)
+    ws = np.abs(w_scale.astype(np.float64)).reshape(-1, 1)
+    x_mag = np.abs(e4m3_decode(x_bits)) * np.abs(np.asarray(x_scale, np.float64)).reshape(-1, 1)
+    w_mag = np.abs(e4m3_decode(w_bits)) * (ws if ws.size > 1 else ws.reshape(1, 1))
+    return pre, e4m3_mfma_slack(terms, module.in_features, x_mag, w_mag)
+
+
+def check_swiglu(out: torch.Tensor, gate, up, x: torch.Tensor, label: str = "") -> dict:
+    """``silu(gate(x)) * up(x)`` of a device call against the oracle's
+    projections (``oracle.parity.swiglu_check``)."""
+
+    gp, gs = projection_pre(gate, x)
+    upre, us = projection_pre(up, x)
+    dtype = DTYPE_NAME[out.dtype]
+    metrics = swiglu_check(np32(out).reshape(gp.shape), gp, upre, dtype, gs, us)
+    print(f"[parity] {label} swiglu ulp bins {metrics.get('ulp_bins')}: {metrics.get('ulp_hist')} "
+          f"max {metrics.get('max_ulp', 0):.3f} rel_rmse {metrics.get('rel_rmse', 0):.3e}", flush=True)
+    assert metrics["ok"], f"{label}: {metrics.get('why')}"
     return metrics

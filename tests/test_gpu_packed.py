@@ -129,3 +129,91 @@ def test_pack_graph_replays_match_eager(cuda):
             assert torch.equal(a, b)
         pack4(x)  # eager work between replays
         torch.cuda.synchronize()
+
+
+# ---------------------------------------------------------------- SwiGLU
+# silu(gate(x)) * up(x) of a (gate, up) pack (kairyu/models/layers.py:243-244).
+# W4A16: one kq_w4a16_tiled_swiglu_gemm call; decode shapes (here N = 2 x 4096
+# on K = 4096) apply SwiGLU in the GEMV epilogue, others run the tiled GEMM
+# and the elementwise pass.  W8A8: the packed GEMM and kq_swiglu.
+_SWIGLU_CASES = [
+    # (scheme, m, k, width, dtype, bias)
+    ("gptq", 1, 4096, 4096, torch.float16, False),
+    ("gptq", 16, 4096, 4096, torch.bfloat16, True),
+    ("gptq-ao", 4, 4096, 4096, torch.float16, False),
+    ("gptq-sym", 16, 4096, 4096, torch.float16, False),
+    ("gptq-sym-ao", 1, 4096, 4096, torch.bfloat16, False),
+    ("awq", 5, 4096, 4096, torch.float16, True),
+    ("gptq", 100, 1024, 1024, torch.bfloat16, False),      # prefill: GEMM + elementwise pass
+    ("gptq-sym-ao", 7, 4128, 512, torch.float16, False),   # skinny shape: two passes
+    ("awq", 64, 2048, 1024, torch.float16, False),
+    ("fp8", 1, 2048, 2048, torch.bfloat16, True),
+    ("fp8", 300, 1024, 1024, torch.float16, False),
+    ("int8", 16, 2048, 1024, torch.bfloat16, True),
+]
+
+
+def _swiglu_pair(scheme, k, width, bias, seed):
+    gen = torch.Generator().manual_seed(seed)
+    if scheme in ("fp8", "int8"):
+        make = _fp8 if scheme == "fp8" else _int8
+        mods = [make(k, width, seed + i) for i in range(2)]
+        if not bias:
+            for m in mods:
+                m.bias = None
+        return mods
+    group = 128
+    mods = []
+    for i in range(2):
+        if scheme == "awq":
+            mods.append(_awq_module(k, width, group=group, seed=seed + i, bias=bias, random_packed=True))
+            continue
+        g_idx = None
+        if scheme.endswith("-ao"):
+            g_idx = (torch.randperm(k, generator=torch.Generator().manual_seed(seed)) // group).to(torch.int32)
+        m = _gptq_module(k, width, group=group, seed=seed + i, bias=bias, g_idx=g_idx, random_packed=True)
+        if g_idx is not None:
+            m.g_idx.copy_(g_idx)
+        if "-sym" in scheme:
+            from kairyu_amd.quant import gptq as gptq_format
+            m.qzeros.copy_(gptq_format.pack_gptq_cols(torch.full((m.qzeros.shape[0], width), 7)))
+        mods.append(m)
+    return mods
+
+
+@pytest.mark.parametrize("case", _SWIGLU_CASES, ids=lambda c: "-".join(map(str, c[:4])) + ("-b" if c[5] else ""))
+def test_swiglu_pack_matches_oracle(cuda, case):
+    from gpu_helpers import check_swiglu
+
+    scheme, m, k, width, dtype, bias = case
+    banner(f"swiglu pack {case}")
+    gate, up = (mod.to(cuda) for mod in _swiglu_pair(scheme, k, width, bias, seed=31 * m + k))
+    pack = QuantLinearPack.create([gate, up])
+    assert pack is not None
+    x = torch.randn(m, k, generator=torch.Generator().manual_seed(m + k)).to(dtype)
+    out = pack.swiglu(x.to(cuda))
+    assert out.shape == (m, width) and out.dtype == dtype
+    check_swiglu(out, gate, up, x, label=str(case))
+    # the same call again (derived operands cached) gives the same bits
+    assert torch.equal(pack.swiglu(x.to(cuda)), out)
+
+
+def test_swiglu_pack_in_a_graph(cuda):
+    """Decode GEMV with the SwiGLU epilogue captured once and replayed."""
+
+    gate, up = (mod.to(cuda) for mod in _swiglu_pair("gptq-sym-ao", 4096, 4096, False, seed=5))
+    pack = QuantLinearPack.create([gate, up])
+    x = torch.randn(16, 4096, generator=torch.Generator().manual_seed(6)).to(torch.float16).to(cuda)
+    eager = pack.swiglu(x).clone()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        pack.swiglu(x)
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = pack.swiglu(x)
+    for _ in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager)

@@ -15,7 +15,7 @@ from __future__ import annotations
 import numpy as np
 import pytest
 
-from gpu_helpers import assert_ulp_close, e4m3_mfma_slack, fp16_mfma_slack, ulp
+from gpu_helpers import assert_ulp_close, e4m3_mfma_slack, fp16_mfma_slack, swiglu_check, ulp
 from oracle import formats, linear as olinear
 from oracle.numerics import e4m3_decode, fp16_round, to_dtype
 
@@ -114,3 +114,50 @@ def test_fp8_bound_accepts_the_mfma_window_and_rejects_mistakes(k, outliers):
     doubled[:, 128:256] *= 2.0
     with pytest.raises(AssertionError):
         assert_ulp_close(device(doubled), pre, "bfloat16", slack, label="K block twice")
+
+
+def test_swiglu_reference_matches_torch_on_cpu():
+    """The oracle's SwiGLU against torch's own fp16 / bf16 ``silu(g) * u`` on
+    the CPU (the operation the reference MLP runs, layers.py:243-244)."""
+
+    import torch
+
+    rng = np.random.default_rng(9)
+    g = (rng.standard_normal((256, 512)) * 4).astype(np.float32)
+    u = rng.standard_normal((256, 512)).astype(np.float32)
+    for name, tdt in (("bfloat16", torch.bfloat16), ("float16", torch.float16)):
+        ref = olinear.swiglu_reference(g, u, name)
+        t = (torch.nn.functional.silu(torch.from_numpy(g).to(tdt)) * torch.from_numpy(u).to(tdt)).float().numpy()
+        differ = ref != t
+        # bf16 identical; fp16 differs only where silu(g) sits on a rounding
+        # boundary (one input value here, g = -2.725): the libraries' exp
+        # differ in the last fp32 ulp, the silu rounds the other way and the
+        # product moves by one or two ulp
+        assert differ.mean() < 1e-3, (name, int(differ.sum()))
+        assert np.all(np.abs(ref - t)[differ] <= 2 * ulp(np.maximum(np.abs(ref), np.abs(t))[differ], name))
+        assert len(np.unique(to_dtype(g[differ], name))) <= 2
+
+
+def test_swiglu_bound_accepts_fp32_accumulation_and_rejects_mistakes():
+    x, qweight, qzeros, scales, g_idx = _gptq_case(m=8, k=2048, n=512)
+    k = x.shape[1]
+    half = 256
+    pre, terms = olinear.gptq_reference(x, qweight, qzeros, scales, g_idx, "float16")
+    slack = fp16_mfma_slack(terms, k)
+    w = formats.w4a16_weight_fp16(formats.gptq_dequantize(qweight, qzeros, scales, g_idx))
+    dev = _fp32_chunked(x, w, 32).astype(np.float64)
+    gp, up_ = pre[:, :half], pre[:, half:]
+    gs, us = slack[:, :half], slack[:, half:]
+    device = olinear.swiglu_reference(dev[:, :half], dev[:, half:], "float16")
+    assert swiglu_check(device, gp, up_, "float16", gs, us)["ok"]
+    swapped = olinear.swiglu_reference(dev[:, half:], dev[:, :half], "float16")
+    assert not swiglu_check(swapped, gp, up_, "float16", gs, us)["ok"]
+    dropped = x.copy()
+    dropped[:, 700] = 0.0
+    dev2 = _fp32_chunked(dropped, w, 32).astype(np.float64)
+    assert not swiglu_check(olinear.swiglu_reference(dev2[:, :half], dev2[:, half:], "float16"),
+                            gp, up_, "float16", gs, us)["ok"]
+    no_silu = olinear.swiglu_reference(dev[:, :half], dev[:, half:], "float16") * 0 + \
+        to_dtype((to_dtype(dev[:, :half].astype(np.float32), "float16") *
+                  to_dtype(dev[:, half:].astype(np.float32), "float16")).astype(np.float32), "float16")
+    assert not swiglu_check(no_silu, gp, up_, "float16", gs, us)["ok"]
