@@ -19,6 +19,10 @@ Pinning (how each function is known to be right, see tests/test_oracle_*.py):
   formats.quantize_int8_*      reference fixture; torch.round half-even identity
   linear.int8_*                exactness proof: int64 matmul == fp64 BLAS matmul
   linear.fp8_*                 e4m3 products exact in fp64 (closed form)
+  linear.swiglu_reference      torch's own fp16 / bf16 silu(g) * u on the CPU
+                               (the reference MLP's operation, layers.py:243-244):
+                               bf16 identical, fp16 within 2 ulp on a silu
+                               rounding boundary (tests/test_parity_bounds.py)
   moe.route_*                  reference fixtures (test_moe_precision.py:97-154)
   moe.combine_*                reference fixtures (test_moe_precision.py:138-154,194-226)
   parity                       the device-output criteria (ulp bound with the
