@@ -19,6 +19,9 @@ C5), each row with
     (gathered fp16 x, quantized int8 / e4m3 rows), its algorithmic bytes or
     FLOPs per launch over the per-launch time (none for C5, whose kernels are
     split in ``profiles/``);
+  * ``vendor_gemm`` (W8A8 prefill rows, M > 64): the vendor library
+    (hipBLASLt through torch) on the same quantized operands and weight
+    copies, with the ratio of its time to the ``gemm`` time;
   * ``cpu_baseline`` and ``parity`` (unless ``--no-cpu``): the repo's CPU
     restatement of the reference path timed on a bounded sample of the row's
     workload on this host's cores, and the device output on the same sample
@@ -221,6 +224,56 @@ def measure_gemm(workload, steps: int, dtype: str) -> dict | None:
     return {"kernel": kernel, "us": round(ms * 1e3, 3), "bytes_per_launch": nbytes,
             "flops_per_launch": flops, "bound": workload.bound, "achieved": round(achieved, 1),
             "unit": "GB/s" if hbm else "TFLOP/s", "peak": peak, "frac": round(achieved / peak, 4)}
+
+
+def vendor_gemm(workload, steps: int) -> dict | None:
+    """The vendor library on the same quantized operands, for the W8A8
+    prefill rows (M > 64): hipBLASLt through torch._scaled_mm (e4m3 x e4m3,
+    fp32 row scales x fp32 column scales, bf16 out: the same epilogue) or
+    torch._int_mm (int8 x int8 -> int32, no scale epilogue).  Timed eagerly
+    with events over `steps` calls rotating the same weight copies as
+    measure_gemm (library calls stay out of graph capture)."""
+
+    import torch
+
+    from kairyu_amd import workloads
+    from kairyu_amd.kernels import quant_gemm_hip as hip
+    from kairyu_amd.quant.linear import Fp8Linear, Int8Linear
+
+    module, x = workload.module, workload.x
+    m, k = x.shape
+    if not isinstance(module, (Fp8Linear, Int8Linear)) or m <= 64:
+        return None
+    n = module.out_features
+    copies = _copies(module)
+    mods = workloads.replicas(workload, copies)
+    fp8 = isinstance(module, Fp8Linear)
+    xq, xs = hip._quantize_activation(x, torch.float8_e4m3fn if fp8 else torch.int8,
+                                      448.0 if fp8 else 127.0)
+    if fp8:
+        sa = xs.reshape(m, 1).float()
+        sbs = [hip._f32(mod.weight_scale).reshape(1, -1).expand(1, n).contiguous() for mod in mods]
+        call = lambda i: torch._scaled_mm(xq, mods[i % copies].weight.t(), scale_a=sa,  # noqa: E731
+                                          scale_b=sbs[i % copies], out_dtype=x.dtype)
+        lib = "hipBLASLt via torch._scaled_mm (row-wise fp32 scales, bf16 out)"
+    else:
+        call = lambda i: torch._int_mm(xq, mods[i % copies].weight.t())  # noqa: E731
+        lib = "hipBLASLt via torch._int_mm (int32 out, no scale epilogue)"
+    try:
+        for i in range(max(5, copies)):
+            call(i)
+        torch.cuda.synchronize()
+    except RuntimeError as exc:  # an older torch without row-wise scaling
+        return {"library": lib, "error": str(exc)[:200]}
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for i in range(steps):
+        call(i)
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / steps
+    return {"library": lib, "us": round(ms * 1e3, 3),
+            "achieved": round(2 * m * n * k / (ms * 1e-3) / 1e12, 1), "unit": "TFLOP/s"}
 
 
 # ------------------------------------------------------------ CPU baselines
@@ -520,6 +573,13 @@ def main() -> int:
             print(f"[bench]   op {row['us']} us  {row['gb_per_s']} GB/s  {row['tflops']} TFLOPS"
                   + (f"; gemm {row['gemm']['us']} us {row['gemm']['achieved']} {row['gemm']['unit']}"
                      if row["gemm"] else ""), file=sys.stderr, flush=True)
+            vendor = vendor_gemm(wl, max(20, min(args.steps, 100)))
+            if vendor is not None:
+                row["vendor_gemm"] = vendor
+                if "us" in vendor:
+                    vendor["vendor_us_over_ours"] = round(vendor["us"] / row["gemm"]["us"], 3)
+                    print(f"[bench]   vendor {vendor['us']} us {vendor['achieved']} TFLOP/s "
+                          f"({vendor['library']})", file=sys.stderr, flush=True)
             if not args.no_cpu:
                 out = wl.module(wl.x)
                 torch.cuda.synchronize()
