@@ -93,6 +93,51 @@ KQ_DEV float load_row_regs(const uint16_t* row, int64_t k, int dtype, bool vec_o
   return m;
 }
 
+// The same row held as raw 16-bit pairs (4 registers per chunk instead of 8:
+// more rows in flight per CU).  Elements at or beyond `k` read as 0.
+template <int NCH>
+KQ_DEV void load_row_raw(const uint16_t* row, int64_t k, bool vec_ok, u32x4 raw[NCH]) {
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    const int64_t i = ((int64_t)threadIdx.x + (int64_t)blockDim.x * c) * 8;
+    if (vec_ok && i + 8 <= k) {
+      raw[c] = *(const u32x4*)(row + i);
+    } else {
+      uint32_t w[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t lo = i + 2 * j < k ? row[i + 2 * j] : 0u;
+        const uint32_t hi = i + 2 * j + 1 < k ? row[i + 2 * j + 1] : 0u;
+        w[j] = lo | (hi << 16);
+      }
+      raw[c] = u32x4{w[0], w[1], w[2], w[3]};
+    }
+  }
+}
+
+// max |bits| of the row as fp32 bits: the 16-bit magnitudes order like their
+// values (inf above every finite value, NaN above inf) in fp16 and bf16 alike,
+// so the widened maximum magnitude is the fp32 amax of a finite row, inf for a
+// row with inf and NaN for a row with NaN
+template <int NCH>
+KQ_DEV uint32_t row_abs_bits_raw(const u32x4 raw[NCH], int dtype) {
+  uint32_t m = 0;
+#pragma unroll
+  for (int c = 0; c < NCH; ++c)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) m = max(m, max(raw[c][j] & 0x7fffu, (raw[c][j] >> 16) & 0x7fffu));
+  return __float_as_uint(dtype == KQ_DTYPE_BF16 ? bf16_to_f32((uint16_t)m) : f16_to_f32((uint16_t)m));
+}
+
+KQ_DEV void widen8(u32x4 raw, int dtype, float v[8]) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const uint16_t lo = (uint16_t)(raw[j] & 0xffffu), hi = (uint16_t)(raw[j] >> 16);
+    v[2 * j] = dtype == KQ_DTYPE_BF16 ? bf16_to_f32(lo) : f16_to_f32(lo);
+    v[2 * j + 1] = dtype == KQ_DTYPE_BF16 ? bf16_to_f32(hi) : f16_to_f32(hi);
+  }
+}
+
 template <int NCH>
 __global__ void __launch_bounds__(1024)
 row_amax_kernel(const uint16_t* __restrict__ x, int dtype, int64_t k, int64_t ldx,
@@ -119,9 +164,9 @@ act_quant_i8_kernel(const uint16_t* __restrict__ x, int dtype, int64_t k, int64_
                     bool vec_ok, int8_t* __restrict__ xq, float* __restrict__ xscale) {
   __shared__ float red[16];
   const int64_t r = blockIdx.x;
-  float v[NCH][8];
-  load_row_regs<NCH>(x + r * ldx, k, dtype, vec_ok, v);
-  const uint32_t abits = block_max_u32(row_abs_bits<NCH>(v), (uint32_t*)red);
+  u32x4 raw[NCH];
+  load_row_raw<NCH>(x + r * ldx, k, vec_ok, raw);
+  const uint32_t abits = block_max_u32(row_abs_bits_raw<NCH>(raw, dtype), (uint32_t*)red);
   const bool fast = abits < 0x7f800000u;
   const float s = __fdiv_rn(max_keep_nan(__uint_as_float(abits), 1e-12f), 127.0f);
   const float rs = __fdiv_rn(1.0f, s);
@@ -129,11 +174,13 @@ act_quant_i8_kernel(const uint16_t* __restrict__ x, int dtype, int64_t k, int64_
   for (int c = 0; c < NCH; ++c) {
     const int64_t i = ((int64_t)threadIdx.x + (int64_t)blockDim.x * c) * 8;
     if (i >= k) break;
+    float v[8];
+    widen8(raw[c], dtype, v);
     uint32_t packed[2] = {0u, 0u};
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      const float q = fast ? __builtin_rintf(fminf(fmaxf(div_by_recip(v[c][e], s, rs), -127.0f), 127.0f))
-                           : __builtin_rintf(clamp_keep_nan(__fdiv_rn(v[c][e], s), 127.0f));
+      const float q = fast ? __builtin_rintf(fminf(fmaxf(div_by_recip(v[e], s, rs), -127.0f), 127.0f))
+                           : __builtin_rintf(clamp_keep_nan(__fdiv_rn(v[e], s), 127.0f));
       packed[e >> 2] |= ((uint32_t)(int32_t)q & 0xffu) << (8 * (e & 3));
     }
     store8((uint8_t*)xq + r * k, i, k, packed[0], packed[1]);
@@ -148,9 +195,9 @@ act_quant_fp8_kernel(const uint16_t* __restrict__ x, int dtype, int64_t k, int64
                      uint8_t* __restrict__ xq, float* __restrict__ xscale) {
   __shared__ float red[16];
   const int64_t r = blockIdx.x;
-  float v[NCH][8];
-  load_row_regs<NCH>(x + r * ldx, k, dtype, vec_ok, v);
-  const uint32_t abits = block_max_u32(row_abs_bits<NCH>(v), (uint32_t*)red);
+  u32x4 raw[NCH];
+  load_row_raw<NCH>(x + r * ldx, k, vec_ok, raw);
+  const uint32_t abits = block_max_u32(row_abs_bits_raw<NCH>(raw, dtype), (uint32_t*)red);
   bool fast = abits < 0x7f800000u;
   float s;
   if (scale_mode == 0) {
@@ -164,19 +211,21 @@ act_quant_fp8_kernel(const uint16_t* __restrict__ x, int dtype, int64_t k, int64
   for (int c = 0; c < NCH; ++c) {
     const int64_t i = ((int64_t)threadIdx.x + (int64_t)blockDim.x * c) * 8;
     if (i >= k) break;
+    float v[8];
+    widen8(raw[c], dtype, v);
     uint32_t packed[2] = {0u, 0u};
     if (fast) {
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         float q[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) q[e] = fminf(fmaxf(div_by_recip(v[c][4 * h + e], s, rs), -448.0f), 448.0f);
+        for (int e = 0; e < 4; ++e) q[e] = fminf(fmaxf(div_by_recip(v[4 * h + e], s, rs), -448.0f), 448.0f);
         packed[h] = pack4_e4m3(q[0], q[1], q[2], q[3]);
       }
     } else {
 #pragma unroll
       for (int e = 0; e < 8; ++e)
-        packed[e >> 2] |= f32_to_e4m3(clamp_keep_nan(__fdiv_rn(v[c][e], s), 448.0f)) << (8 * (e & 3));
+        packed[e >> 2] |= f32_to_e4m3(clamp_keep_nan(__fdiv_rn(v[e], s), 448.0f)) << (8 * (e & 3));
     }
     store8(xq + r * k, i, k, packed[0], packed[1]);
   }
