@@ -55,6 +55,7 @@ constexpr int kTgThreads = 512;
 constexpr int kTgMaxKB = 128;     // K <= 16384 for block scaling (weight scale rows in LDS)
 constexpr int32_t kTgOob = (int32_t)0x80000000u;  // buffer offset past every resource: reads 0
 constexpr int kTgGroupM = 8;  // dense tile order: row tiles per group
+constexpr int kTgLag = 2;     // block scaling: MFMAs between a result and its scale FMA
 
 enum { kTgFp8 = 0, kTgI8 = 1 };
 enum { kTgEpiStore = 0, kTgEpiSwiGluQuant = 1 };
@@ -391,7 +392,7 @@ tile_gemm_kernel(TileGemmArgs a) {
       auto kstep = [&](auto nrb_c) {
         constexpr int NRB = decltype(nrb_c)::value;
         TgFrag xf[NRB];
-        f32x4 blk[2];
+        f32x4 blk[kTgLag + 1];
 #pragma unroll
         for (int mb = 0; mb < NRB; ++mb) xf[mb] = tg_load(sX + mb * 16 * kTgBK, o_lo, o_hi);
 #pragma unroll
@@ -407,20 +408,26 @@ tile_gemm_kernel(TileGemmArgs a) {
               const i32x8 B = i32x8{xf[mb].lo[0], xf[mb].lo[1], xf[mb].lo[2], xf[mb].lo[3],
                                     xf[mb].hi[0], xf[mb].hi[1], xf[mb].hi[2], xf[mb].hi[3]};
               if constexpr (BLOCK) {
-                // scale-accumulate one MFMA behind, from alternating temporaries,
-                // so no MFMA waits on its own result before the next is issued
+                // scale-accumulate kTgLag MFMAs behind, from rotating
+                // temporaries: with one MFMA of lag the FMAs read a result
+                // the matrix core is still producing and the next MFMA into
+                // that temporary waits for them (two MFMAs in flight at most)
                 const int idx = j * NRB + mb;
-                blk[idx & 1] = mfma_fp8(A, B, f32x4{0.f, 0.f, 0.f, 0.f});
-                if (idx > 0) {
-                  const int pj = (idx - 1) / NRB, pm = (idx - 1) % NRB;
+                constexpr int R = kTgLag + 1;
+                blk[idx % R] = mfma_fp8(A, B, f32x4{0.f, 0.f, 0.f, 0.f});
+                // keep the FMAs of result idx - kTgLag after this MFMA (the
+                // scheduler would otherwise hoist them next to their MFMA)
+                __builtin_amdgcn_sched_barrier(0);
+                auto fold = [&](int d) {
+                  const int pj = d / NRB, pm = d % NRB;
                   const float sc = prod[pj >> 2][pm];
 #pragma unroll
-                  for (int q = 0; q < 4; ++q) acc[pj][pm][q] = fmaf(blk[(idx - 1) & 1][q], sc, acc[pj][pm][q]);
-                }
+                  for (int q = 0; q < 4; ++q) acc[pj][pm][q] = fmaf(blk[d % R][q], sc, acc[pj][pm][q]);
+                };
+                if (idx >= kTgLag) fold(idx - kTgLag);
                 if (idx == 8 * NRB - 1) {
-                  const float sc = prod[1][NRB - 1];
 #pragma unroll
-                  for (int q = 0; q < 4; ++q) acc[7][NRB - 1][q] = fmaf(blk[idx & 1][q], sc, acc[7][NRB - 1][q]);
+                  for (int d = 8 * NRB - kTgLag; d < 8 * NRB; ++d) fold(d);
                 }
               } else {
                 acc[j][mb] = mfma_fp8(A, B, acc[j][mb]);
