@@ -26,6 +26,7 @@ KQ_DEV float reduce_epilogue(const ReduceArgs& a, int64_t idx, int m, int n, int
 
 // Thread = 4 consecutive outputs.  N % 4 == 0 (VEC): they share a row, so
 // the partials load as 16-byte vectors and the outputs store as 8 bytes.
+// (The W8A8 modes with N % 8 == 0 take splitk_reduce8_kernel below.)
 template <int MODE, bool VEC>
 __global__ void __launch_bounds__(256) splitk_reduce_kernel(ReduceArgs a) {
   const int64_t plane = (int64_t)a.M * a.N;
@@ -77,8 +78,82 @@ __global__ void __launch_bounds__(256) splitk_reduce_kernel(ReduceArgs a) {
   }
 }
 
+// W8A8, N % 8 == 0: thread = 8 consecutive outputs of one row; per split two
+// 16-byte partial loads (streamed: non-temporal), the weight scales as two
+// 16-byte loads, one 16-byte store.  Same sums and roundings as above.
+template <int MODE>
+__global__ void __launch_bounds__(256) splitk_reduce8_kernel(ReduceArgs a) {
+  const int64_t plane = (int64_t)a.M * a.N;
+  const int64_t base = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 8;
+  if (base >= plane) return;
+  const int m0 = (int)(base / a.N), n0 = (int)(base - (int64_t)m0 * a.N);
+  const float xs = a.xscale[m0];
+  float ws[8];
+  if (MODE == kReduceI8 || a.ws_per_channel) {
+    const f32x4 w0 = *(const f32x4*)(a.wscale + n0), w1 = *(const f32x4*)(a.wscale + n0 + 4);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      ws[q] = w0[q];
+      ws[4 + q] = w1[q];
+    }
+  } else {
+#pragma unroll
+    for (int q = 0; q < 8; ++q) ws[q] = a.wscale[0];
+  }
+  float v[8];
+  if constexpr (MODE == kReduceI8) {
+    i32x4 lo = i32x4{0, 0, 0, 0}, hi = i32x4{0, 0, 0, 0};
+    for (int s = 0; s < a.splits; ++s) {
+      const i32x4* p = (const i32x4*)((const int32_t*)a.partials + s * plane + base);
+      lo += __builtin_nontemporal_load(p);
+      hi += __builtin_nontemporal_load(p + 1);
+    }
+    if (a.acc_out) {
+      *(i32x4*)(a.acc_out + base) = lo;
+      *(i32x4*)(a.acc_out + base + 4) = hi;
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      v[q] = __fmul_rn(__fmul_rn((float)lo[q], xs), ws[q]);
+      v[4 + q] = __fmul_rn(__fmul_rn((float)hi[q], xs), ws[4 + q]);
+    }
+  } else {
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int s = 0; s < a.splits; ++s) {
+      const f32x4* p = (const f32x4*)((const float*)a.partials + s * plane + base);
+      const f32x4 lo = __builtin_nontemporal_load(p), hi = __builtin_nontemporal_load(p + 1);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        acc[q] = __fadd_rn(acc[q], lo[q]);
+        acc[4 + q] = __fadd_rn(acc[4 + q], hi[q]);
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < 8; ++q) v[q] = __fmul_rn(__fmul_rn(acc[q], xs), ws[q]);
+  }
+  uint32_t o[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    float a0 = v[2 * q], a1 = v[2 * q + 1];
+    if (a.bias_dtype != KQ_DTYPE_NONE) {
+      a0 = __fadd_rn(a0, load_as_f32(a.bias, a.bias_dtype, n0 + 2 * q));
+      a1 = __fadd_rn(a1, load_as_f32(a.bias, a.bias_dtype, n0 + 2 * q + 1));
+    }
+    o[q] = (uint32_t)f32_to_out(a0, a.out_dtype) | ((uint32_t)f32_to_out(a1, a.out_dtype) << 16);
+  }
+  *(u32x4*)((uint16_t*)a.out + base) = u32x4{o[0], o[1], o[2], o[3]};
+}
+
 void launch_splitk_reduce(int mode, const ReduceArgs& a, hipStream_t stream) {
   const int64_t total = (int64_t)a.M * a.N;
+  if (mode != kReduceW4 && (a.N & 7) == 0 && ((uintptr_t)a.partials & 15) == 0 &&
+      ((uintptr_t)a.out & 15) == 0 && ((uintptr_t)a.wscale & 15) == 0 &&
+      (!a.acc_out || ((uintptr_t)a.acc_out & 15) == 0)) {
+    const dim3 g((unsigned)((total + 2047) / 2048)), b(256);
+    if (mode == kReduceI8) hipLaunchKernelGGL(splitk_reduce8_kernel<kReduceI8>, g, b, 0, stream, a);
+    else hipLaunchKernelGGL(splitk_reduce8_kernel<kReduceFp8>, g, b, 0, stream, a);
+    return;
+  }
   const unsigned blocks = (unsigned)((total + 1023) / 1024);
   const bool vec = (a.N & 3) == 0 && ((uintptr_t)a.partials & 15) == 0 && ((uintptr_t)a.out & 7) == 0 &&
                    (!a.acc_out || ((uintptr_t)a.acc_out & 15) == 0);
