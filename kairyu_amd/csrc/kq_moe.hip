@@ -415,10 +415,51 @@ moe_count_quant_kernel(const int32_t* __restrict__ idx, int R, int E, int32_t* _
 
 // ------------------------------------------------------------------ combine
 // out[t] = sum over slots s (in order) of fp32(y[inv[t*k+s]]) * w[t*k+s].
+KQ_DEV void widen8_out(u32x4 raw, int dtype, float v[8]) {
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    v[2 * d] = dtype == KQ_DTYPE_BF16 ? bf16_to_f32(raw[d] & 0xffffu) : f16_to_f32(raw[d] & 0xffffu);
+    v[2 * d + 1] = dtype == KQ_DTYPE_BF16 ? bf16_to_f32(raw[d] >> 16) : f16_to_f32(raw[d] >> 16);
+  }
+}
+
 __global__ void __launch_bounds__(256)
 moe_combine_kernel(const uint16_t* __restrict__ y, int y_dtype, const int32_t* __restrict__ inv,
                    const float* __restrict__ w, int k, int H, uint16_t* __restrict__ out) {
   const int64_t t = blockIdx.x;
+  if (k == 8 && (H & 7) == 0 && (((uintptr_t)out | (uintptr_t)y) & 15) == 0) {
+    // the common top-8 case: all eight rows are requested before the first
+    // is summed (the generic loop below has one row in flight per thread)
+    for (int h = threadIdx.x * 8; h < H; h += 256 * 8) {
+      int pos[8];
+      float wv[8];
+      u32x4 raw[8];
+#pragma unroll
+      for (int s = 0; s < 8; ++s) {
+        pos[s] = inv[t * 8 + s];
+        wv[s] = w[t * 8 + s];
+      }
+#pragma unroll
+      for (int s = 0; s < 8; ++s) raw[s] = *(const u32x4*)(y + (int64_t)max(pos[s], 0) * H + h);
+      float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < 8; ++s) {
+        float yv[8];
+        widen8_out(raw[s], y_dtype, yv);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float sum = __fadd_rn(acc[e], __fmul_rn(yv[e], wv[s]));
+          acc[e] = pos[s] < 0 ? acc[e] : sum;  // an unrouted slot adds nothing
+        }
+      }
+      u32x4 o;
+#pragma unroll
+      for (int d = 0; d < 4; ++d)
+        o[d] = (uint32_t)f32_to_out(acc[2 * d], y_dtype) | ((uint32_t)f32_to_out(acc[2 * d + 1], y_dtype) << 16);
+      *(u32x4*)(out + t * H + h) = o;
+    }
+    return;
+  }
   for (int h = threadIdx.x * 8; h < H; h += 256 * 8) {
     float acc[8];
 #pragma unroll
