@@ -237,6 +237,34 @@ def test_int8_tile_engine_split_k_bit_exact(cuda, m, n, k):
     assert np.array_equal(np32(out), expected)
 
 
+# The split-K reduce writes 8 outputs per thread when N % 8 == 0 and 4 per
+# thread otherwise; both forms with fp16 output and with no bias.
+@pytest.mark.parametrize("m,n,k", SPLITK_SHAPES[:2])
+@pytest.mark.parametrize("bias", [True, False])
+def test_int8_split_k_fp16_output_bit_exact(cuda, m, n, k, bias):
+    banner(f"int8 split-k fp16 m={m} n={n} k={k} bias={bias}")
+    module = _int8_module(k, n, seed=m + n + 7, bias=bias).to(cuda)
+    x = torch.randn(m, k, generator=torch.Generator().manual_seed(k + 1)).to(torch.float16)
+    acc = torch.empty(m, n, dtype=torch.int32, device=cuda)
+    out = hip.int8_linear_forward(x.to(cuda), module, accumulators=acc)
+    assert out.dtype == torch.float16
+    expected, xq, xs, eacc = olinear.int8_forward(
+        np32(x), module.weight.cpu().numpy(), module.weight_scale.cpu().numpy(),
+        np32(module.bias) if bias else None, out_dtype="float16")
+    assert np.array_equal(acc.cpu().numpy().astype(np.int64), eacc)
+    assert np.array_equal(np32(out), expected)
+
+
+@pytest.mark.parametrize("m,n,k", SPLITK_SHAPES[:2])
+def test_fp8_split_k_fp16_output_no_bias(cuda, m, n, k):
+    banner(f"fp8 split-k fp16 m={m} n={n} k={k}")
+    module = _fp8_module(k, n, seed=m + n + 7, bias=False).to(cuda)
+    x = torch.randn(m, k, generator=torch.Generator().manual_seed(k + 1)).to(torch.float16)
+    out = module(x.to(cuda))
+    assert out.dtype == torch.float16
+    check_fp8(out, x, module, label=f"fp16 m={m} n={n} k={k}", add_bias=False)
+
+
 @pytest.mark.parametrize("m,n,k", SPLITK_SHAPES[:2])
 def test_fp8_tile_engine_split_k_matches_oracle(cuda, m, n, k):
     banner(f"fp8 split-k m={m} n={n} k={k}")
