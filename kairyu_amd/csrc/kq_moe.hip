@@ -22,11 +22,12 @@
 //   2. act_quant_fp8_blocks: each token quantized once (not once per slot).
 //   3. grouped GEMM 1 (gate_up), kq_tile_gemm.h: activation rows gathered
 //      through the sorted order, weights = the expert's stacked [gate; up].
-//      A 256 x 256 tile pairs gate columns [n0, n0+128) with up columns
-//      [I+n0, I+n0+128), so the epilogue forms the SwiGLU in the activation
-//      dtype and quantizes the finished 128-column block to e4m3 in registers
-//      (no bf16 intermediate in HBM).
-//   4. grouped GEMM 2 (down): 256 x 256 tiles -> expert outputs (bf16/fp16).
+//      A 320 x 256 tile (320 rows of one expert: at an even top-8 routing
+//      every expert's rows fit one row tile) pairs gate columns [n0, n0+128)
+//      with up columns [I+n0, I+n0+128), so the epilogue forms the SwiGLU in
+//      the activation dtype and quantizes the finished 128-column block to
+//      e4m3 in registers (no bf16 intermediate in HBM).
+//   4. grouped GEMM 2 (down): 320 x 256 tiles -> expert outputs (bf16/fp16).
 //   5. combine: fp32 slot-order weighted sum per token.
 // Both GEMMs use v_mfma_scale_f32_16x16x128_f8f6f4 (unit E8M0 scales): one
 // MFMA spans one 128-wide K block, and its fp32 result is scaled by
@@ -145,7 +146,8 @@ moe_route_kernel(const void* __restrict__ logits, int dtype, int T, int E, int k
 
 // -------------------------------------------------------------- stable sort
 constexpr int kSortChunk = 256;   // rows per chunk = threads per sort workgroup
-constexpr int kBM = kTgBM;        // rows per GEMM row tile
+constexpr int kMoeNrb = 5;        // tile engine row blocks per wave for the expert GEMMs
+constexpr int kBM = 64 * kMoeNrb; // rows per expert row tile (320)
 
 // Per-chunk expert histogram: counts[c][e] for chunk c (hist: E ints of LDS).
 KQ_DEV void moe_count_chunk(const int32_t* __restrict__ idx, int R, int E, int32_t* __restrict__ counts,
@@ -294,9 +296,11 @@ moe_scan_kernel(const int32_t* __restrict__ counts, int C, int E, int BM, int ma
 // expert e in the chunk's earlier waves (per-wave counts in LDS, whist[w][e])
 // plus the earlier lanes of this wave with expert e: one ballot per bit of
 // the expert id leaves the mask of lanes whose id equals this lane's.
+// sorted_tok[pos] is the token of the routed row at sorted position pos (the
+// gate_up GEMM's row source), inv[r] the sorted position of routed row r.
 __global__ void __launch_bounds__(kSortChunk)
-moe_scatter_kernel(const int32_t* __restrict__ idx, int R, int E, const int32_t* __restrict__ base,
-                   int32_t* __restrict__ sorted_rows, int32_t* __restrict__ inv) {
+moe_scatter_kernel(const int32_t* __restrict__ idx, int R, int E, int top_k, const int32_t* __restrict__ base,
+                   int32_t* __restrict__ sorted_tok, int32_t* __restrict__ inv) {
   extern __shared__ int whist[];   // [kSortChunk / 64][E]
   const int c = blockIdx.x, t = threadIdx.x;
   const int w = t >> 6, lane = t & 63;
@@ -325,7 +329,7 @@ moe_scatter_kernel(const int32_t* __restrict__ idx, int R, int E, const int32_t*
   const int pos = base[(int64_t)c * E + e] + rank;
   // (pos < R always holds for a consistent base table; the check keeps a
   // position outside the buffer from ever being written or combined)
-  if (pos < R) sorted_rows[pos] = r;
+  if (pos < R) sorted_tok[pos] = r / top_k;
   inv[r] = pos < R ? pos : -1;
 }
 
@@ -594,7 +598,7 @@ extern "C" int kq_block_fp8_gemm(const uint8_t* xq, const float* xs, const uint8
   }
   if (m == 0) return KQ_OK;
   TileGemmArgs a{};
-  a.x = xq; a.xs = xs; a.x_rows = (int)m; a.gather = nullptr; a.topk = 1;
+  a.x = xq; a.xs = xs; a.x_rows = (int)m; a.gather = nullptr;
   a.w = w; a.ws = ws; a.mtile_table = nullptr; a.mtile_count = nullptr;
   a.M = (int)m; a.N = (int)n; a.K = (int)k; a.I = 0;
   a.mtiles = (int)((m + kTgBM - 1) / kTgBM);
@@ -676,23 +680,23 @@ extern "C" int kq_moe_block_fp8_experts(const void* hidden, int dtype, int64_t t
     hipLaunchKernelGGL(moe_scan_kernel<0>, dim3(1), dim3(1024), 0, st, counts, C, E, kBM, max_tiles,
                        offsets, base, tiles, tile_count);
   hipLaunchKernelGGL(moe_scatter_kernel, dim3(C), dim3(kSortChunk), (kSortChunk / 64) * E * sizeof(int), st,
-                     topk_idx, R, E, base, sorted, inv);
+                     topk_idx, R, E, top_k, base, sorted, inv);
 
   TileGemmArgs g{};
-  g.x = xq; g.xs = xs; g.x_rows = (int)tokens; g.gather = sorted; g.topk = top_k;
+  g.x = xq; g.xs = xs; g.x_rows = (int)tokens; g.gather = sorted; g.gather_rows = R;
   g.w = w13; g.ws = s13; g.mtile_table = tiles; g.mtile_count = tile_count;
   g.N = (int)(2 * inter); g.K = (int)hidden_size; g.I = (int)inter;
   g.mtiles = max_tiles; g.ntiles = (int)(inter / 128);
   g.actq = actq; g.acts = acts; g.out_dtype = dtype; g.bias_dtype = KQ_DTYPE_NONE;
-  tg_launch<kTgFp8, true, kTgEpiSwiGluQuant>(g, st);
+  tg_launch<kTgFp8, true, kTgEpiSwiGluQuant, kMoeNrb>(g, st);
 
   TileGemmArgs d{};
-  d.x = actq; d.xs = acts; d.x_rows = R; d.gather = nullptr; d.topk = 1;
+  d.x = actq; d.xs = acts; d.x_rows = R; d.gather = nullptr;
   d.w = w2; d.ws = s2; d.mtile_table = tiles; d.mtile_count = tile_count;
   d.N = (int)hidden_size; d.K = (int)inter; d.I = 0;
   d.mtiles = max_tiles; d.ntiles = (int)((hidden_size + kTgBN - 1) / kTgBN);
   d.out = y; d.out_dtype = dtype; d.bias = nullptr; d.bias_dtype = KQ_DTYPE_NONE;
-  tg_launch<kTgFp8, true, kTgEpiStore>(d, st);
+  tg_launch<kTgFp8, true, kTgEpiStore, kMoeNrb>(d, st);
 
   hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)tokens), dim3(256), 0, st, y, dtype, inv, topk_w,
                      top_k, (int)hidden_size, (uint16_t*)out);

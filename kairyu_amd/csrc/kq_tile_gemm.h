@@ -1,4 +1,4 @@
-// Persistent 256x256 fp8 / int8 MFMA tile engine for gfx950.
+// Persistent fp8 / int8 MFMA tile engine for gfx950.
 //
 //   D[m, n] = sum_k X[m, k] * W[n, k]        (X: activation rows, W: weight rows,
 //                                            both K-contiguous bytes)
@@ -7,7 +7,11 @@
 // and the W8A8 (FP8 / INT8) prefill GEMMs.
 //
 // Work decomposition
-//   * Tiles of 256 activation rows x 256 weight rows.  The grid is persistent
+//   * Tiles of BM = 64 * NRB activation rows x 256 weight rows: NRB = 4
+//     (256 rows) for the dense GEMMs, NRB = 5 (320 rows) for the MoE experts,
+//     where one 320-row tile holds every row of an expert at an even top-8
+//     routing (≈256 ± 50 rows) that 256-row tiles split into a full tile and
+//     a tail of a few rows streaming the same weights.  The grid is persistent
 //     (one 512-thread workgroup per CU).  Workgroup b runs on XCD b % 8; XCD x
 //     owns the contiguous slice [x*T/8, (x+1)*T/8) of the T tiles, walked by
 //     its workgroups in order, so the 32 tiles an XCD has in flight are
@@ -16,16 +20,17 @@
 //     in that XCD's L2.  T may come from device memory (MoE: the number of
 //     row tiles the routing produced), so the host launches no empty tiles.
 //   * Eight waves: wn = wave / 4 owns 128 weight rows (8 blocks of 16),
-//     wm = wave % 4 owns 64 activation rows (4 blocks of 16).  Weights are the
-//     MFMA A operand and activations the B operand, so a lane's four results
-//     are four consecutive output columns of one row: one activation scale and
-//     one weight scale cover all four (one multiply per 16x16 block and K
-//     block for block scaling), and stores are 8 bytes wide.
+//     wm = wave % 4 owns the NRB activation row blocks 4 * mb + wm (16 rows
+//     each; interleaved, so a ragged tile's rows spread over the four SIMDs).
+//     Weights are the MFMA A operand and activations the B operand, so a
+//     lane's four results are four consecutive output columns of one row: one
+//     activation scale and one weight scale cover all four (one multiply per
+//     16x16 block and K block for block scaling), and stores are 8 bytes wide.
 //
 // Memory pipeline
-//   K advances in 128-byte blocks.  W and X blocks (32 KB each) move global ->
-//   LDS with buffer_load ... lds (no registers), double-buffered: block kb+1
-//   is in flight while kb is multiplied.  Rows are 128 bytes in LDS, their
+//   K advances in 128-byte blocks.  W blocks (32 KB) and X blocks (BM x 128
+//   bytes) move global -> LDS with buffer_load ... lds (no registers),
+//   double-buffered: block kb+1 is in flight while kb is multiplied.  Rows are 128 bytes in LDS, their
 //   16-byte chunks permuted by an XOR of row bits chosen per operand pattern
 //   (measured with ds_read_b128 on gfx950: FP8 lanes read chunk pairs
 //   (2g, 2g+1) of 16 rows -> c ^ (r & 7) ^ ((r >> 3) & 1); INT8 lanes read
@@ -48,7 +53,7 @@
 
 namespace kq {
 
-constexpr int kTgBM = 256;        // activation rows per tile
+constexpr int kTgBM = 256;        // activation rows per tile of the dense GEMMs (NRB = 4)
 constexpr int kTgBN = 256;        // weight rows per tile
 constexpr int kTgBK = 128;        // K bytes per pipeline stage (one block-scale block)
 constexpr int kTgThreads = 512;
@@ -60,22 +65,28 @@ constexpr int kTgLag = 2;     // block scaling: MFMAs between a result and its s
 enum { kTgFp8 = 0, kTgI8 = 1 };
 enum { kTgEpiStore = 0, kTgEpiSwiGluQuant = 1 };
 
-// LDS map (bytes)
-constexpr int kTgLdsW = 0;                                // 2 stages x 256 weight rows x 128
-constexpr int kTgLdsX = kTgLdsW + 2 * kTgBN * kTgBK;      // 2 stages x 256 activation rows x 128
-constexpr int kTgLdsXs = kTgLdsX + 2 * kTgBM * kTgBK;     // 2 stages x 256 activation block scales
-constexpr int kTgLdsWs = kTgLdsXs + 2 * kTgBM * 4;        // 2 tiles x 2 weight-scale rows x kTgMaxKB
-constexpr int kTgLdsRed = kTgLdsWs + 4 * kTgMaxKB * 4;    // 2 x 256 row maxima (SwiGLU quant)
-constexpr int kTgLdsEpi = kTgLdsRed + 2 * kTgBM * 4;      // 2 tiles x {row scale, column scale, bias} x 256
-constexpr int kTgLdsBytes = kTgLdsEpi + 2 * 3 * 256 * 4;
+// LDS map (bytes) of a tile of 64 * NRB activation rows
+template <int NRB>
+struct TgLds {
+  static constexpr int BM = 64 * NRB;
+  static constexpr int W = 0;                           // 2 stages x 256 weight rows x 128
+  static constexpr int X = W + 2 * kTgBN * kTgBK;       // 2 stages x BM activation rows x 128
+  static constexpr int Xs = X + 2 * BM * kTgBK;         // 2 stages x BM activation block scales
+  static constexpr int Ws = Xs + 2 * BM * 4;            // 2 tiles x 2 weight-scale rows x kTgMaxKB
+  static constexpr int Red = Ws + 4 * kTgMaxKB * 4;     // 2 x BM row maxima (SwiGLU quant)
+  static constexpr int Epi = Red + 2 * BM * 4;          // 2 tiles x {row scale, column scale, bias} x 256
+  static constexpr int Gat = Epi + 2 * 3 * 256 * 4;     // the next tile's BM row sources (gathered rows)
+  static constexpr int Bytes = Gat + BM * 4;
+  static_assert(Bytes <= 160 * 1024, "the tile's LDS exceeds a CU's 160 KB");
+};
 
 struct TileGemmArgs {
   // activations (MFMA B operand)
   const uint8_t* x;          // [x_rows][K]
   int x_rows;                // rows addressable through x (buffer bound)
   const float* xs;           // block scaling: [x_rows][ceil(K/128)]; otherwise per-row scale [M]
-  const int32_t* gather;     // tile row -> flat routed row (source row = flat / topk); null: identity
-  int topk;
+  const int32_t* gather;     // tile row -> source row of x; null: identity
+  int gather_rows;           // entries of gather
   // weights (MFMA A operand)
   const uint8_t* w;          // [E][N][K]
   const float* ws;           // block scaling: [E][ceil(N/128)][K/128]; otherwise [N] or [1]
@@ -127,6 +138,11 @@ KQ_DEV uint16_t tg_to_out(float v, int dtype) {
   return __builtin_bit_cast(uint16_t, (_Float16)v);
 }
 
+KQ_DEV float tg_from_bits(uint16_t b, int dtype) {
+  if (dtype == KQ_DTYPE_BF16) return __uint_as_float((uint32_t)b << 16);
+  return (float)__builtin_bit_cast(_Float16, b);
+}
+
 
 template <int FMT> struct TgTraits;
 template <> struct TgTraits<kTgFp8> { using Acc = f32x4; };
@@ -152,11 +168,15 @@ struct TgTile {
   int split, kb0, kb1;  // K blocks [kb0, kb1) of this work unit
 };
 
-template <int FMT, bool BLOCK, int EPI>
+template <int FMT, bool BLOCK, int EPI, int NRB>
 __global__ void __launch_bounds__(kTgThreads)
 tile_gemm_kernel(TileGemmArgs a) {
+  // 320-row tiles only where no per-row epilogue constants are needed
+  static_assert(NRB == 4 || (NRB == 5 && BLOCK), "row blocks per wave: 4, or 5 with block scaling");
   using Acc = typename TgTraits<FMT>::Acc;
-  __shared__ __attribute__((aligned(16))) uint8_t smem[kTgLdsBytes];
+  using L = TgLds<NRB>;
+  constexpr int BM = L::BM;
+  __shared__ __attribute__((aligned(16))) uint8_t smem[L::Bytes];
   const int lane = lane_id();
   const int wave = __builtin_amdgcn_readfirstlane(wave_id());
   const int wn = wave >> 2, wm = wave & 3;
@@ -179,12 +199,19 @@ tile_gemm_kernel(TileGemmArgs a) {
   const i32x4 rx = make_rsrc(a.x, (uint32_t)((uint64_t)a.x_rows * K));
   const i32x4 rxs = make_rsrc(a.xs, BLOCK ? (uint32_t)((uint64_t)a.x_rows * KB * 4) : 0u);
   const i32x4 rtab = make_rsrc(a.mtile_table, a.mtile_table ? (uint32_t)a.mtiles * 16u : 0u);
+  const i32x4 rgat = make_rsrc(a.gather, a.gather ? (uint32_t)((uint64_t)a.gather_rows * 4) : 0u);
+  // block scales: every offset below addresses a weight-scale row of an
+  // expert in the tile table (the buffer bound is not the check)
+  const i32x4 rws = make_rsrc(a.ws, BLOCK ? 0x7fffffffu : 0u);
 
   // lane-constant parts of the operand reads: row lr of a 16-row block
   const int o_lo = lr * kTgBK + (tg_chunk<FMT>(lr, FMT == kTgFp8 ? 2 * lg : lg) << 4);
   const int o_hi = lr * kTgBK + (tg_chunk<FMT>(lr, FMT == kTgFp8 ? 2 * lg + 1 : 4 + lg) << 4);
 
-  float* sRed = (float*)(smem + kTgLdsRed);
+  // tile row of this lane's results in row block mb
+  auto trow = [&](int mb) { return 16 * (4 * mb + wm) + lr; };
+
+  float* sRed = (float*)(smem + L::Red);
 
   // ---- tile metadata.  A row tile's table entry is (expert, first row, end
   // row, 0); lane l < 3 of a table word holds entry word l.
@@ -213,8 +240,8 @@ tile_gemm_kernel(TileGemmArgs a) {
       const int gm = min(kTgGroupM, a.mtiles - g * kTgGroupM);
       r.ntile = rr / gm;
       r.e = 0;
-      r.row0 = (g * kTgGroupM + rr % gm) * kTgBM;
-      r.row_end = min(a.M, r.row0 + kTgBM);
+      r.row0 = (g * kTgGroupM + rr % gm) * BM;
+      r.row_end = min(a.M, r.row0 + BM);
     }
     return r;
   };
@@ -225,29 +252,23 @@ tile_gemm_kernel(TileGemmArgs a) {
     else return min(tl.ntile * 2 + half, NB - 1);
   };
 
-  // ---- per-tile loads (row sources, weight scales), issued one tile ahead
-  int pf_src[4], pf_xsrc = -1;
-  float pf_ws = 0.0f, pf_exs = 1.0f, pf_ews = 1.0f, pf_eb = 0.0f;
-  auto prefetch = [&](const TgTile& tl) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int r = tl.row0 + (((wave * 4 + i) * 64 + lane) >> 3);
-      pf_src[i] = r < tl.row_end ? (a.gather ? a.gather[r] : r) : -1;
+  // ---- per-tile loads, issued one tile ahead so that they land under the
+  // current tile's K loop.  Row sources (gathered rows) and block weight
+  // scales move global -> LDS by DMA (no registers held across the K loop);
+  // the store epilogue's constants load into registers.
+  float pf_exs = 1.0f, pf_ews = 1.0f, pf_eb = 0.0f;
+  auto prefetch = [&](const TgTile& tl, int wsbuf) {
+    if (a.gather && wave < NRB) {
+      // LDS int t of the Gat region holds tile row t's flat routed row
+      const int r = tl.row0 + 64 * wave + lane;
+      tg_dma4(rgat, lds0 + L::Gat + wave * 256, r < tl.row_end ? r * 4 : kTgOob, 0);
     }
-    if (BLOCK && wave < 4) {
-      // LDS scale float p = 16 * lr + 4 * c + i (lr = p / 16) holds tile row
-      // 64 * wm + 16 * i + lr of slab wm = c ^ ((lr >> 1) & 3): a lane's four
-      // row scales are one 16-byte chunk, and the chunk XOR spreads the 16
-      // lanes of a read over eight bank groups (2-way instead of 8-way)
-      const int p = wave * 64 + lane;
-      const int lr_ = p >> 4, c_ = (p >> 2) & 3, i_ = p & 3;
-      const int r = tl.row0 + 64 * (c_ ^ ((lr_ >> 1) & 3)) + 16 * i_ + lr_;
-      pf_xsrc = r < tl.row_end ? (a.gather ? a.gather[r] : r) : -1;
-    }
-    if (BLOCK && (int)threadIdx.x < 2 * KB) {
-      const int half = (int)threadIdx.x >= KB;
-      const int kb = (int)threadIdx.x - half * KB;
-      pf_ws = a.ws[((int64_t)tl.e * NB + scale_block(tl, half)) * KB + kb];
+    if (BLOCK && 64 * wave < 2 * KB) {
+      // LDS float t of weight-scale buffer wsbuf: t < KB the first 128-row
+      // block's scale of K block t, then the second block's
+      const int tt = (int)threadIdx.x, half = tt >= KB, kb = tt - half * KB;
+      const int off = tt < 2 * KB ? ((tl.e * NB + scale_block(tl, half)) * KB + kb) * 4 : kTgOob;
+      tg_dma4(rws, lds0 + L::Ws + wsbuf * (2 * kTgMaxKB * 4) + wave * 256, off, 0);
     }
     if (EPI == kTgEpiStore && threadIdx.x < 256) {
       // epilogue constants of tile row / column t: loaded here, one tile
@@ -262,16 +283,31 @@ tile_gemm_kernel(TileGemmArgs a) {
     }
   };
 
-  // ---- DMA state of the tile being loaded
+  // ---- DMA state of the tile being loaded (after its prefetch has landed)
   i32x4 rw;
-  int32_t w_off[4], x_off[4], xs_off = kTgOob;
+  int32_t w_off[4], x_off[NRB], xs_off = kTgOob;
+  const int32_t* sGat = (const int32_t*)(smem + L::Gat);
+  auto row_src = [&](const TgTile& tl, int row) -> int {
+    const int r = tl.row0 + row;
+    return r < tl.row_end ? (a.gather ? sGat[row] : r) : -1;
+  };
   auto set_offsets = [&](const TgTile& tl) {
     rw = make_rsrc(a.w + (int64_t)tl.e * a.N * K, (uint32_t)((uint64_t)a.N * K));
-    // this wave fills 1 KB blocks 4*wave+i of each 32 KB stage; slot
-    // p = block*64 + lane is row p/8, physical chunk p%8
+    // lane terms formed per tile (see the epilogue)
+    int ln = lane;
+    asm volatile("" : "+v"(ln));
+    // this wave fills 1 KB blocks 4*wave+i of each 32 KB weight stage and
+    // NRB*wave+i of each activation stage; slot p = block*64 + lane is row
+    // p/8, physical chunk p%8
+#pragma unroll
+    for (int i = 0; i < NRB; ++i) {
+      const int p = (wave * NRB + i) * 64 + ln, row = p >> 3;
+      const int src = row_src(tl, row);
+      x_off[i] = src >= 0 ? src * K + tg_chunk<FMT>(row, p & 7) * 16 : kTgOob;
+    }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int p = (wave * 4 + i) * 64 + lane, row = p >> 3;
+      const int p = (wave * 4 + i) * 64 + ln, row = p >> 3;
       const int c = tg_chunk<FMT>(row, p & 7);
       int n;
       if constexpr (EPI == kTgEpiSwiGluQuant) {
@@ -284,48 +320,56 @@ tile_gemm_kernel(TileGemmArgs a) {
         n = tl.ntile * kTgBN + row;
       }
       w_off[i] = n < a.N ? n * K + c * 16 : kTgOob;
-      x_off[i] = pf_src[i] >= 0 ? (pf_src[i] / a.topk) * K + c * 16 : kTgOob;
     }
-    if (BLOCK && wave < 4) xs_off = pf_xsrc >= 0 ? (pf_xsrc / a.topk) * KB * 4 : kTgOob;
+    if (BLOCK && wave < NRB) {
+      // LDS scale float r of a stage holds tile row r (64 rows per wave)
+      const int src = row_src(tl, 64 * wave + ln);
+      xs_off = src >= 0 ? src * KB * 4 : kTgOob;
+    }
   };
   auto stage_ws = [&](int buf) {
-    if (BLOCK && (int)threadIdx.x < 2 * KB)
-      ((float*)(smem + kTgLdsWs))[buf * 2 * kTgMaxKB + (int)threadIdx.x] = pf_ws;
     if (EPI == kTgEpiStore && threadIdx.x < 256) {
-      float* e = (float*)(smem + kTgLdsEpi) + buf * 3 * 256 + (int)threadIdx.x;
+      float* e = (float*)(smem + L::Epi) + buf * 3 * 256 + (int)threadIdx.x;
       e[0] = pf_exs;
       e[256] = pf_ews;
       e[512] = pf_eb;
     }
   };
   auto issue = [&](int kb, int st) {
-    const uint32_t lw = lds0 + kTgLdsW + st * (kTgBN * kTgBK) + wave * 4096;
-    const uint32_t lx = lds0 + kTgLdsX + st * (kTgBM * kTgBK) + wave * 4096;
+    const uint32_t lw = lds0 + L::W + st * (kTgBN * kTgBK) + wave * 4096;
+    const uint32_t lx = lds0 + L::X + st * (BM * kTgBK) + wave * (NRB * 1024);
     const int soff = kb * kTgBK;
-    if (kb == KB - 1 && ktail < kTgBK) {
-      // ragged last block: chunks past K read zeros (K % 16 == 0)
+    if (!BLOCK && kb == KB - 1 && ktail < kTgBK) {
+      // ragged last block: chunks past K read zeros (K % 16 == 0; block
+      // scaling takes K % 128 == 0)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int row = (wave * 4 + i) * 8 + (lane >> 3);
+      for (int i = 0; i < NRB; ++i) {
+        if (i < 4) {
+          const int row = (wave * 4 + i) * 8 + (lane >> 3);
+          const bool ok = tg_chunk<FMT>(row, lane & 7) * 16 < ktail;
+          tg_dma16(rw, lw + i * 1024, ok ? w_off[i] : kTgOob, soff);
+        }
+        const int row = (wave * NRB + i) * 8 + (lane >> 3);
         const bool ok = tg_chunk<FMT>(row, lane & 7) * 16 < ktail;
-        tg_dma16(rw, lw + i * 1024, ok ? w_off[i] : kTgOob, soff);
         tg_dma16(rx, lx + i * 1024, ok ? x_off[i] : kTgOob, soff);
       }
     } else {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        tg_dma16(rw, lw + i * 1024, w_off[i], soff);
+      for (int i = 0; i < NRB; ++i) {
+        if (i < 4) tg_dma16(rw, lw + i * 1024, w_off[i], soff);
         tg_dma16(rx, lx + i * 1024, x_off[i], soff);
       }
     }
-    if (BLOCK && wave < 4) tg_dma4(rxs, lds0 + kTgLdsXs + st * (kTgBM * 4) + wave * 256, xs_off, kb * 4);
+    if (BLOCK && wave < NRB) tg_dma4(rxs, lds0 + L::Xs + st * (BM * 4) + wave * 256, xs_off, kb * 4);
   };
 
   // ---- first tile: synchronous set-up
   TgTile cur = tile_of(t, load_tab(t));
-  prefetch(cur);
-  set_offsets(cur);
   int buf = 0, st = 0;
+  prefetch(cur, buf);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();  // the first tile's row sources are in LDS
+  set_offsets(cur);
   stage_ws(buf);
   issue(cur.kb0, st);
   int tn = t + per;
@@ -340,18 +384,18 @@ tile_gemm_kernel(TileGemmArgs a) {
       // the next tile's row sources and weight scales load under this tile's
       // K loop; the table word of the tile after it as well
       nxt = tile_of(tn, pf_tab);
-      prefetch(nxt);
+      prefetch(nxt, buf ^ 1);
       if (tn + per < t_hi) pf_tab = load_tab(tn + per);
     }
     int wslot = 0;  // block scaling: staged weight-scale row of this wave's blocks j < 4
     if (BLOCK && EPI != kTgEpiSwiGluQuant) wslot = wn;
-    const float* sWs = (const float*)(smem + kTgLdsWs) + buf * 2 * kTgMaxKB;
+    const float* sWs = (const float*)(smem + L::Ws) + buf * 2 * kTgMaxKB;
 
-    Acc acc[8][4];
+    Acc acc[8][NRB];
 #pragma unroll
     for (int j = 0; j < 8; ++j)
 #pragma unroll
-      for (int mb = 0; mb < 4; ++mb) acc[j][mb] = Acc{0, 0, 0, 0};
+      for (int mb = 0; mb < NRB; ++mb) acc[j][mb] = Acc{0, 0, 0, 0};
 
     // The next tile's prefetch loads are still in flight here.  Where the
     // register allocator reuses one of their destination registers inside the
@@ -359,42 +403,55 @@ tile_gemm_kernel(TileGemmArgs a) {
     // for all vector-memory operations (the next block's copies included) in
     // every K step; one wait per tile here lets it drop that.
     if constexpr (EPI == kTgEpiStore) __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
-    // Block scaling (MoE experts, block-FP8 linear): a ragged row tile (an
-    // expert's last one holds a few rows at C5-like routing, about a third of
-    // the row tiles) can leave this wave's 64-row slab without rows; the wave
-    // then skips its fragment reads and MFMAs (its accumulators stay 0 and are
-    // never stored) and only takes part in the copies and barriers.  (The
-    // W8A8 prefill instantiations keep the unbranched loop: same speed
+    // Block scaling (MoE experts, block-FP8 linear): row block 4 * mb + wm of
+    // a ragged row tile holds rows while 16 * (4 * mb + wm) < rows, so the
+    // first `live` of this wave's row blocks hold rows.  A wave without any
+    // skips its fragment reads and MFMAs (its accumulators stay 0 and are
+    // never stored) and takes part in every copy and barrier; the SwiGLU
+    // epilogue skips the blocks past `live`.  (Skipping single row blocks in
+    // the K loop takes one loop body per live count, and the compiler's
+    // register copies between those bodies cost more than the MFMAs saved;
+    // the W8A8 prefill instantiations keep the unbranched loop: same speed
     // without the branch, measured.)
-    const bool slab_live = !BLOCK || __builtin_amdgcn_readfirstlane(cur.row_end - cur.row0 - 64 * wm) > 0;
+    const int live = BLOCK ? __builtin_amdgcn_readfirstlane(
+                                 min(NRB, max(0, (cur.row_end - cur.row0 - 16 * wm + 63) >> 6)))
+                           : NRB;
     for (int kb = cur.kb0; kb < cur.kb1; ++kb) {
       if (kb + 1 < cur.kb1) issue(kb + 1, st ^ 1);
-      const uint8_t* sW = smem + kTgLdsW + st * (kTgBN * kTgBK) + (128 * wn) * kTgBK;
-      const uint8_t* sX = smem + kTgLdsX + st * (kTgBM * kTgBK) + (64 * wm) * kTgBK;
-      float prod[2][4];
+      const uint8_t* sW = smem + L::W + st * (kTgBN * kTgBK) + (128 * wn) * kTgBK;
+      // row block mb of this wave: tile rows 16 * (4 * mb + wm) ...
+      const uint8_t* sX = smem + L::X + st * (BM * kTgBK) + (16 * wm) * kTgBK;
+      // block scaling: the scale of row block mb and W rows j * 16 is
+      // sx[mb] * sw[j >> 2]; 256-row tiles form the products once per K
+      // block, 320-row tiles (160 accumulators: registers are short) form
+      // each at its use
+      float sx[NRB], sw[2] = {0.f, 0.f}, prod[2][NRB];
       if constexpr (BLOCK) {
-        const f32x4 sx =
-            *(const f32x4*)(smem + kTgLdsXs + st * (kTgBM * 4) + (lr * 16 + 4 * (wm ^ ((lr >> 1) & 3))) * 4);
+        // 16 lanes read 16 consecutive floats (the other lane groups the same
+        // ones): conflict-free
+        const float* sxs = (const float*)(smem + L::Xs + st * (BM * 4)) + 16 * wm + lr;
+#pragma unroll
+        for (int mb = 0; mb < NRB; ++mb) sx[mb] = sxs[64 * mb];
         if constexpr (EPI == kTgEpiSwiGluQuant) {
-          const float s0 = sWs[kb], s1 = sWs[KB + kb];
-#pragma unroll
-          for (int mb = 0; mb < 4; ++mb) {
-            prod[0][mb] = sx[mb] * s0;
-            prod[1][mb] = sx[mb] * s1;
-          }
+          sw[0] = sWs[kb];
+          sw[1] = sWs[KB + kb];
         } else {
-          const float s0 = sWs[wslot * KB + kb];
+          sw[0] = sw[1] = sWs[wslot * KB + kb];
+        }
+        if constexpr (NRB == 4) {
 #pragma unroll
-          for (int mb = 0; mb < 4; ++mb) prod[0][mb] = prod[1][mb] = sx[mb] * s0;
+          for (int mb = 0; mb < NRB; ++mb) {
+            prod[0][mb] = sx[mb] * sw[0];
+            prod[1][mb] = sx[mb] * sw[1];
+          }
         }
       }
-      // fragment reads and MFMAs of row blocks mb < NRB
-      auto kstep = [&](auto nrb_c) {
-        constexpr int NRB = decltype(nrb_c)::value;
+      // fragment reads and MFMAs of the wave's NRB row blocks
+      auto kstep = [&]() {
         TgFrag xf[NRB];
         f32x4 blk[kTgLag + 1];
 #pragma unroll
-        for (int mb = 0; mb < NRB; ++mb) xf[mb] = tg_load(sX + mb * 16 * kTgBK, o_lo, o_hi);
+        for (int mb = 0; mb < NRB; ++mb) xf[mb] = tg_load(sX + mb * 64 * kTgBK, o_lo, o_hi);
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
           const TgFrag wf = tg_load(sW + j * 16 * kTgBK, o_lo, o_hi);
@@ -420,7 +477,7 @@ tile_gemm_kernel(TileGemmArgs a) {
                 __builtin_amdgcn_sched_barrier(0);
                 auto fold = [&](int d) {
                   const int pj = d / NRB, pm = d % NRB;
-                  const float sc = prod[pj >> 2][pm];
+                  const float sc = NRB == 4 ? prod[pj >> 2][pm] : sx[pm] * sw[pj >> 2];
 #pragma unroll
                   for (int q = 0; q < 4; ++q) acc[pj][pm][q] = fmaf(blk[d % R][q], sc, acc[pj][pm][q]);
                 };
@@ -436,11 +493,7 @@ tile_gemm_kernel(TileGemmArgs a) {
           }
         }
       };
-      if constexpr (BLOCK) {
-        if (slab_live) kstep(std::integral_constant<int, 4>{});
-      } else {
-        kstep(std::integral_constant<int, 4>{});
-      }
+      if (live > 0) kstep();
       __builtin_amdgcn_s_waitcnt(0);  // this wave's copies of the next block have landed
       __syncthreads();                 // ... and everyone's; stage st is free again
       st ^= 1;
@@ -458,49 +511,75 @@ tile_gemm_kernel(TileGemmArgs a) {
     // rounding and conversion below is a single fixed instruction sequence.
     auto epilogue = [&](auto odt) {
       constexpr int ODT = decltype(odt)::value;
-      // lane holds rows m = 64*wm + 16*mb + lr, columns 128*wn + 16*j + 4*lg + q
+      // The epilogue's lane-derived addresses are formed here, once per tile:
+      // an opaque copy of the lane id keeps the compiler from computing them
+      // before the tile loop and holding them in registers across the K loop.
+      int ln = lane;
+      asm volatile("" : "+v"(ln));
+      const int lr = ln & 15, lg = ln >> 4, tid = 64 * wave + ln;
+      auto trow = [&](int mb) { return 16 * (4 * mb + wm) + lr; };
+      // lane holds tile rows trow(mb) = 16*(4*mb + wm) + lr, columns 128*wn + 16*j + 4*lg + q
       const int row0 = cur.row0, row_end = cur.row_end, ntile = cur.ntile;
       if constexpr (EPI == kTgEpiSwiGluQuant) {
         // SwiGLU rounded to the activation dtype at each step (as torch does for
         // bf16 / fp16 tensors), then 1x128 e4m3 quantization of the tile's 128
         // activation columns: s = max(amax, 1e-12) / 448, q = e4m3(clamp(v / s)).
-        float amax[4] = {0.f, 0.f, 0.f, 0.f};
+        // Row blocks without rows keep their zero accumulators.
+        // The products are held as 16-bit pairs of the activation dtype (the
+        // value each rounds to), so the 80 gate and 80 up accumulators of a
+        // 320-row tile give way to 40 registers.
+        float amax[NRB];
+        uint32_t pv[4][NRB][2];
   #pragma unroll
-        for (int j = 0; j < 4; ++j)
+        for (int mb = 0; mb < NRB; ++mb) {
+          amax[mb] = 0.f;
   #pragma unroll
-          for (int mb = 0; mb < 4; ++mb)
+          for (int j = 0; j < 4; ++j) pv[j][mb][0] = pv[j][mb][1] = 0u;
+          if (mb >= live) continue;
   #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-              const float g = tg_round_act(acc[j][mb][q], ODT);
-              const float u = tg_round_act(acc[j + 4][mb][q], ODT);
-              const float sl = tg_round_act(g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)), ODT);
-              const float v = tg_round_act(sl * u, ODT);
-              acc[j][mb][q] = v;
-              amax[mb] = fmaxf(amax[mb], fabsf(v));
+          for (int j = 0; j < 4; ++j) {
+  #pragma unroll
+            for (int h = 0; h < 2; ++h) {
+              uint16_t bits[2];
+  #pragma unroll
+              for (int e = 0; e < 2; ++e) {
+                const int q = 2 * h + e;
+                const float g = tg_round_act(acc[j][mb][q], ODT);
+                const float u = tg_round_act(acc[j + 4][mb][q], ODT);
+                const float sl = tg_round_act(g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)), ODT);
+                const float v = tg_round_act(sl * u, ODT);
+                amax[mb] = fmaxf(amax[mb], fabsf(v));
+                bits[e] = tg_to_out(v, ODT);
+              }
+              pv[j][mb][h] = (uint32_t)bits[0] | ((uint32_t)bits[1] << 16);
             }
+          }
+        }
   #pragma unroll
-        for (int mb = 0; mb < 4; ++mb) {
+        for (int mb = 0; mb < NRB; ++mb) {
           amax[mb] = fmaxf(amax[mb], __shfl_xor(amax[mb], 16, 64));
           amax[mb] = fmaxf(amax[mb], __shfl_xor(amax[mb], 32, 64));
-          if (lg == 0) sRed[wn * kTgBM + 64 * wm + 16 * mb + lr] = amax[mb];
+          if (lg == 0) sRed[wn * BM + trow(mb)] = amax[mb];
         }
         __syncthreads();
         const int IB = a.I / 128;
-        // the tile's 256 x 128 e4m3 block goes through the idle pipeline stage
+        // the tile's BM x 128 e4m3 block goes through the idle pipeline stage
         // (row r at r*128, 16-byte chunk c at c ^ (r & 7)) so that the global
         // stores below write whole 128-byte rows
-        uint8_t* stg = smem + kTgLdsX + (st ^ 1) * (kTgBM * kTgBK);
+        uint8_t* stg = smem + L::X + (st ^ 1) * (BM * kTgBK);
   #pragma unroll
-        for (int mb = 0; mb < 4; ++mb) {
-          const int lrow = 64 * wm + 16 * mb + lr;
-          const float am = fmaxf(sRed[lrow], sRed[kTgBM + lrow]);
+        for (int mb = 0; mb < NRB; ++mb) {
+          const int lrow = trow(mb);
+          const float am = fmaxf(sRed[lrow], sRed[BM + lrow]);
           const float s = __fdiv_rn(fmaxf(am, 1e-12f), 448.0f);
           const float rs = __fdiv_rn(1.0f, s);
   #pragma unroll
           for (int j = 0; j < 4; ++j) {
             float v[4];
   #pragma unroll
-            for (int q = 0; q < 4; ++q) v[q] = fminf(fmaxf(div_by_recip(acc[j][mb][q], s, rs), -448.0f), 448.0f);
+            for (int q = 0; q < 4; ++q)
+              v[q] = fminf(fmaxf(div_by_recip(tg_from_bits((uint16_t)(pv[j][mb][q >> 1] >> (16 * (q & 1))), ODT), s, rs),
+                                 -448.0f), 448.0f);
             const int col = 64 * wn + 16 * j + 4 * lg;
             *(uint32_t*)(stg + lrow * 128 + (((col >> 4) ^ (lrow & 7)) << 4) + (col & 15)) =
                 pack4_e4m3(v[0], v[1], v[2], v[3]);
@@ -509,8 +588,8 @@ tile_gemm_kernel(TileGemmArgs a) {
         }
         __syncthreads();
   #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int r = 64 * i + ((int)threadIdx.x >> 3), c = (int)threadIdx.x & 7;
+        for (int i = 0; i < NRB; ++i) {
+          const int r = 64 * i + (tid >> 3), c = tid & 7;
           if (row0 + r < row_end)
             *(i32x4*)(a.actq + (int64_t)(row0 + r) * a.I + ntile * 128 + c * 16) =
                 *(const i32x4*)(stg + r * 128 + ((c ^ (r & 7)) << 4));
@@ -524,8 +603,8 @@ tile_gemm_kernel(TileGemmArgs a) {
         for (int j = 0; j < 8; ++j) {
           const int n = ntile * kTgBN + 128 * wn + 16 * j + 4 * lg;
   #pragma unroll
-          for (int mb = 0; mb < 4; ++mb) {
-            const int grow = row0 + 64 * wm + 16 * mb + lr;
+          for (int mb = 0; mb < NRB; ++mb) {
+            const int grow = row0 + trow(mb);
             if (grow >= row_end) continue;
             uint32_t v[4];
   #pragma unroll
@@ -544,63 +623,71 @@ tile_gemm_kernel(TileGemmArgs a) {
           }
         }
       } else {
-        const float* eX = (const float*)(smem + kTgLdsEpi) + buf * 3 * 256;
-        // each wave's 128 x 64 output block goes through its 8 KB of the idle
-        // pipeline stage in two column halves ([m][64 columns], 16-byte chunk c of
-        // row m at c ^ (m & 7)), so every global store writes whole 128-byte
-        // row segments; rows of 8-aligned N only (others store directly)
-        uint8_t* stg = smem + (wave < 4 ? kTgLdsW : kTgLdsX) + (st ^ 1) * (kTgBN * kTgBK) + (wave & 3) * 8192;
+        const float* eX = (const float*)(smem + L::Epi) + buf * 3 * 256;
+        // each wave's output rows go through its 8 KB of the idle pipeline
+        // stage in passes of up to four row blocks by 64 columns ([m][64
+        // columns], 16-byte chunk c of row m at c ^ (m & 7)), so every global
+        // store writes whole 128-byte row segments; rows of 8-aligned N only
+        // (others store directly)
+        uint8_t* stg = smem + (wave < 4 ? L::W : L::X) + (st ^ 1) * (wave < 4 ? kTgBN * kTgBK : BM * kTgBK) +
+                       (wave & 3) * 8192;
         const bool staged = (a.N & 7) == 0;
   #pragma unroll
         for (int half = 0; half < 2; ++half) {
   #pragma unroll
-          for (int jj = 0; jj < 4; ++jj) {
-            const int j = 4 * half + jj;
-            const int nl = 128 * wn + 16 * j + 4 * lg;  // tile column of q = 0
-            const int n = ntile * kTgBN + nl;
-            const f32x4 wsc = *(const f32x4*)(eX + 256 + nl);
-            const f32x4 bv = *(const f32x4*)(eX + 512 + nl);
+          for (int mg = 0; mg < NRB; mg += 4) {
+            constexpr int kPass = 4;
   #pragma unroll
-            for (int mb = 0; mb < 4; ++mb) {
-              const int ml = 16 * mb + lr;  // row within the wave's block
-              const int grow = row0 + 64 * wm + ml;
-              const float xsc = BLOCK ? 1.0f : eX[64 * wm + ml];
-              uint16_t o[4];
+            for (int jj = 0; jj < 4; ++jj) {
+              const int j = 4 * half + jj;
+              const int nl = 128 * wn + 16 * j + 4 * lg;  // tile column of q = 0
+              const int n = ntile * kTgBN + nl;
+              const f32x4 wsc = *(const f32x4*)(eX + 256 + nl);
+              const f32x4 bv = *(const f32x4*)(eX + 512 + nl);
   #pragma unroll
-              for (int q = 0; q < 4; ++q) {
-                float v = (float)acc[j][mb][q];
-                if (!BLOCK) v = __fmul_rn(__fmul_rn(v, xsc), wsc[q]);
-                if (a.bias_dtype != KQ_DTYPE_NONE) v = __fadd_rn(v, bv[q]);
-                o[q] = tg_to_out(v, ODT);
-              }
-              const u32x2 word = u32x2{(uint32_t)o[0] | ((uint32_t)o[1] << 16), (uint32_t)o[2] | ((uint32_t)o[3] << 16)};
-              if (staged) {
-                const int cb = 32 * jj + 8 * lg;  // byte column within the 128-byte row
-                *(u32x2*)(stg + ml * 128 + (((cb >> 4) ^ (ml & 7)) << 4) + (cb & 15)) = word;
-              } else if (grow < row_end) {
-                uint16_t* dst = (uint16_t*)a.out + (int64_t)grow * a.N + n;
+              for (int mb = mg; mb < NRB && mb < mg + kPass; ++mb) {
+                const int ml = 16 * (mb - mg) + lr;  // staging row
+                const int grow = row0 + trow(mb);
+                const float xsc = BLOCK ? 1.0f : eX[trow(mb)];
+                uint16_t o[4];
   #pragma unroll
-                for (int q = 0; q < 4; ++q)
-                  if (n + q < a.N) dst[q] = o[q];
-              }
-              if constexpr (FMT == kTgI8) {
-                if (a.acc_out && grow < row_end) {
-                  int32_t* ad = a.acc_out + (int64_t)grow * a.N + n;
+                for (int q = 0; q < 4; ++q) {
+                  float v = (float)acc[j][mb][q];
+                  if (!BLOCK) v = __fmul_rn(__fmul_rn(v, xsc), wsc[q]);
+                  if (a.bias_dtype != KQ_DTYPE_NONE) v = __fadd_rn(v, bv[q]);
+                  o[q] = tg_to_out(v, ODT);
+                }
+                const u32x2 word = u32x2{(uint32_t)o[0] | ((uint32_t)o[1] << 16), (uint32_t)o[2] | ((uint32_t)o[3] << 16)};
+                if (staged) {
+                  const int cb = 32 * jj + 8 * lg;  // byte column within the 128-byte row
+                  *(u32x2*)(stg + ml * 128 + (((cb >> 4) ^ (ml & 7)) << 4) + (cb & 15)) = word;
+                } else if (grow < row_end) {
+                  uint16_t* dst = (uint16_t*)a.out + (int64_t)grow * a.N + n;
   #pragma unroll
                   for (int q = 0; q < 4; ++q)
-                    if (n + q < a.N) ad[q] = acc[j][mb][q];
+                    if (n + q < a.N) dst[q] = o[q];
+                }
+                if constexpr (FMT == kTgI8) {
+                  if (a.acc_out && grow < row_end) {
+                    int32_t* ad = a.acc_out + (int64_t)grow * a.N + n;
+  #pragma unroll
+                    for (int q = 0; q < 4; ++q)
+                      if (n + q < a.N) ad[q] = acc[j][mb][q];
+                  }
                 }
               }
             }
-          }
-          if (staged) {
+            if (staged) {
+              // 8 rows of 8 chunks per instruction over the pass's rows
+              const int prow = 16 * (NRB - mg < kPass ? NRB - mg : kPass);
   #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-              const int ml = 8 * i + (lane >> 3), c = lane & 7;
-              const int grow = row0 + 64 * wm + ml;
-              const int n = ntile * kTgBN + 128 * wn + 64 * half + 8 * c;
-              const i32x4 v = *(const i32x4*)(stg + ml * 128 + ((c ^ (ml & 7)) << 4));
-              if (grow < row_end && n < a.N) *(i32x4*)((uint16_t*)a.out + (int64_t)grow * a.N + n) = v;
+              for (int i = 0; i < prow / 8; ++i) {
+                const int ml = 8 * i + (ln >> 3), c = ln & 7;
+                const int grow = row0 + 16 * (4 * (mg + (ml >> 4)) + wm) + (ml & 15);
+                const int n = ntile * kTgBN + 128 * wn + 64 * half + 8 * c;
+                const i32x4 v = *(const i32x4*)(stg + ml * 128 + ((c ^ (ml & 7)) << 4));
+                if (grow < row_end && n < a.N) *(i32x4*)((uint16_t*)a.out + (int64_t)grow * a.N + n) = v;
+              }
             }
           }
         }
@@ -633,13 +720,14 @@ static inline int tg_device_cus() {
 }
 
 // Persistent launch: one workgroup per CU (never more than the tiles), a
-// multiple of 8 so every XCD gets the same number of workgroups.
-template <int FMT, bool BLOCK, int EPI>
+// multiple of 8 so every XCD gets the same number of workgroups.  NRB = 5:
+// row tiles of 320 rows (a.mtiles counts them).
+template <int FMT, bool BLOCK, int EPI, int NRB = 4>
 static void tg_launch(const TileGemmArgs& a, hipStream_t stream) {
   const int64_t max_total = (int64_t)a.mtiles * a.ntiles * (a.ksplit > 1 ? a.ksplit : 1);
   int64_t grid = max_total < tg_device_cus() ? max_total : tg_device_cus();
   grid = (grid + 7) / 8 * 8;
-  hipLaunchKernelGGL((tile_gemm_kernel<FMT, BLOCK, EPI>), dim3((unsigned)grid), dim3(kTgThreads), 0,
+  hipLaunchKernelGGL((tile_gemm_kernel<FMT, BLOCK, EPI, NRB>), dim3((unsigned)grid), dim3(kTgThreads), 0,
                      stream, a);
 }
 

@@ -801,7 +801,7 @@ static int run_w8a8(const char* what, const uint8_t* xq, const uint8_t* w, int64
     // with fewer tiles than CUs each tile's K range is split over `splits`
     // work units whose raw accumulators the split-K reduce sums in order
     TileGemmArgs a{};
-    a.x = xq; a.x_rows = (int)m; a.xs = ep.xscale; a.gather = nullptr; a.topk = 1;
+    a.x = xq; a.x_rows = (int)m; a.xs = ep.xscale; a.gather = nullptr;
     a.w = w; a.ws = ep.wscale; a.ws_per_channel = ep.ws_per_channel;
     a.mtile_table = nullptr; a.mtile_count = nullptr;
     a.M = (int)m; a.N = (int)n; a.K = K; a.I = 0;

@@ -121,6 +121,10 @@ def _oracle_moe(pack, x, idx, w, tokens=None):
     (100, 384, 128, 16, 4, torch.float16, 7),     # most experts empty
     (7, 128, 384, 4, 4, torch.bfloat16, 4),       # top_k == experts
     (300, 512, 256, 32, 8, torch.bfloat16, 32),
+    # experts with more rows than one row tile: 1000 rows each (row tiles of
+    # 320, 320, 320 and 40) and ≈470 rows each
+    (1000, 256, 128, 4, 4, torch.bfloat16, 4),
+    (700, 256, 256, 8, 2, torch.float16, 3),
 ])
 def test_routed_block_fp8_experts_match_oracle(cuda, cfg):
     tokens, hidden, inter, experts, top_k, dtype, used = cfg
