@@ -22,12 +22,13 @@
 //   2. act_quant_fp8_blocks: each token quantized once (not once per slot).
 //   3. grouped GEMM 1 (gate_up), kq_tile_gemm.h: activation rows gathered
 //      through the sorted order, weights = the expert's stacked [gate; up].
-//      A 320 x 256 tile (320 rows of one expert: at an even top-8 routing
-//      every expert's rows fit one row tile) pairs gate columns [n0, n0+128)
-//      with up columns [I+n0, I+n0+128), so the epilogue forms the SwiGLU in
-//      the activation dtype and quantizes the finished 128-column block to
-//      e4m3 in registers (no bf16 intermediate in HBM).
-//   4. grouped GEMM 2 (down): 320 x 256 tiles -> expert outputs (bf16/fp16).
+//      A 320 x 256 or 256 x 256 tile (rows of one expert; moe_nrb picks the
+//      height) pairs gate columns [n0, n0+128) with up columns
+//      [I+n0, I+n0+128), so the epilogue forms the SwiGLU in the activation
+//      dtype and quantizes the finished 128-column block to e4m3 in registers
+//      (no bf16 intermediate in HBM).
+//   4. grouped GEMM 2 (down): the same row tiles x 256 -> expert outputs
+//      (bf16/fp16).
 //   5. combine: fp32 slot-order weighted sum per token.
 // Both GEMMs use v_mfma_scale_f32_16x16x128_f8f6f4 (unit E8M0 scales): one
 // MFMA spans one 128-wide K block, and its fp32 result is scaled by
@@ -146,8 +147,16 @@ moe_route_kernel(const void* __restrict__ logits, int dtype, int T, int E, int k
 
 // -------------------------------------------------------------- stable sort
 constexpr int kSortChunk = 256;   // rows per chunk = threads per sort workgroup
-constexpr int kMoeNrb = 5;        // tile engine row blocks per wave for the expert GEMMs
-constexpr int kBM = 64 * kMoeNrb; // rows per expert row tile (320)
+// Row tiles of the expert GEMMs: 64 * moe_nrb rows.  320-row tiles (NRB 5)
+// when the routing averages more than 192 rows per expert: an even top-k
+// routing then spreads the experts' rows over ~256 +- 50, which 256-row tiles
+// split into a full tile and a tail of a few rows that streams the same
+// weights and unbalances the persistent schedule (C5: 368 -> 295 us).  With
+// fewer rows every expert fits one 256-row tile, which costs less than a
+// 320-row one (measured 3-6% at 16 to 1024 tokens of the C5 layer).
+static inline int moe_nrb(int64_t routed_rows, int64_t experts) {
+  return routed_rows > 192 * experts ? 5 : 4;
+}
 
 // Per-chunk expert histogram: counts[c][e] for chunk c (hist: E ints of LDS).
 KQ_DEV void moe_count_chunk(const int32_t* __restrict__ idx, int R, int E, int32_t* __restrict__ counts,
@@ -505,7 +514,8 @@ static size_t align256(size_t v) { return (v + 255) / 256 * 256; }
 static MoeWorkspace moe_layout(int64_t T, int64_t H, int64_t I, int64_t E, int64_t k) {
   const int64_t R = T * k;
   const int64_t C = (R + kSortChunk - 1) / kSortChunk;
-  const int64_t max_tiles = (R + kBM - 1) / kBM + E;
+  const int64_t BM = 64 * moe_nrb(R, E);
+  const int64_t max_tiles = (R + BM - 1) / BM + E;
   MoeWorkspace w{};
   size_t p = 0;
   auto take = [&](size_t bytes) { const size_t at = p; p += align256(bytes); return at; };
@@ -658,7 +668,8 @@ extern "C" int kq_moe_block_fp8_experts(const void* hidden, int dtype, int64_t t
   const int R = (int)(tokens * top_k);
   const int C = (R + kSortChunk - 1) / kSortChunk;
   const int E = (int)experts;
-  const int max_tiles = (R + kBM - 1) / kBM + E;
+  const int nrb = moe_nrb(R, E), BM = 64 * nrb;
+  const int max_tiles = (R + BM - 1) / BM + E;
 
   // chunk histograms and the token quantization share one launch
   {
@@ -671,13 +682,13 @@ extern "C" int kq_moe_block_fp8_experts(const void* hidden, int dtype, int64_t t
   }
   const int scan_per = (C + moe_scan_slices(E) - 1) / moe_scan_slices(E);
   if (scan_per <= 16)
-    hipLaunchKernelGGL(moe_scan_kernel<16>, dim3(1), dim3(1024), 0, st, counts, C, E, kBM, max_tiles,
+    hipLaunchKernelGGL(moe_scan_kernel<16>, dim3(1), dim3(1024), 0, st, counts, C, E, BM, max_tiles,
                        offsets, base, tiles, tile_count);
   else if (scan_per <= 64)
-    hipLaunchKernelGGL(moe_scan_kernel<64>, dim3(1), dim3(1024), 0, st, counts, C, E, kBM, max_tiles,
+    hipLaunchKernelGGL(moe_scan_kernel<64>, dim3(1), dim3(1024), 0, st, counts, C, E, BM, max_tiles,
                        offsets, base, tiles, tile_count);
   else
-    hipLaunchKernelGGL(moe_scan_kernel<0>, dim3(1), dim3(1024), 0, st, counts, C, E, kBM, max_tiles,
+    hipLaunchKernelGGL(moe_scan_kernel<0>, dim3(1), dim3(1024), 0, st, counts, C, E, BM, max_tiles,
                        offsets, base, tiles, tile_count);
   hipLaunchKernelGGL(moe_scatter_kernel, dim3(C), dim3(kSortChunk), (kSortChunk / 64) * E * sizeof(int), st,
                      topk_idx, R, E, top_k, base, sorted, inv);
@@ -688,7 +699,8 @@ extern "C" int kq_moe_block_fp8_experts(const void* hidden, int dtype, int64_t t
   g.N = (int)(2 * inter); g.K = (int)hidden_size; g.I = (int)inter;
   g.mtiles = max_tiles; g.ntiles = (int)(inter / 128);
   g.actq = actq; g.acts = acts; g.out_dtype = dtype; g.bias_dtype = KQ_DTYPE_NONE;
-  tg_launch<kTgFp8, true, kTgEpiSwiGluQuant, kMoeNrb>(g, st);
+  if (nrb == 5) tg_launch<kTgFp8, true, kTgEpiSwiGluQuant, 5>(g, st);
+  else tg_launch<kTgFp8, true, kTgEpiSwiGluQuant, 4>(g, st);
 
   TileGemmArgs d{};
   d.x = actq; d.xs = acts; d.x_rows = R; d.gather = nullptr;
@@ -696,7 +708,8 @@ extern "C" int kq_moe_block_fp8_experts(const void* hidden, int dtype, int64_t t
   d.N = (int)hidden_size; d.K = (int)inter; d.I = 0;
   d.mtiles = max_tiles; d.ntiles = (int)((hidden_size + kTgBN - 1) / kTgBN);
   d.out = y; d.out_dtype = dtype; d.bias = nullptr; d.bias_dtype = KQ_DTYPE_NONE;
-  tg_launch<kTgFp8, true, kTgEpiStore, kMoeNrb>(d, st);
+  if (nrb == 5) tg_launch<kTgFp8, true, kTgEpiStore, 5>(d, st);
+  else tg_launch<kTgFp8, true, kTgEpiStore, 4>(d, st);
 
   hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)tokens), dim3(256), 0, st, y, dtype, inv, topk_w,
                      top_k, (int)hidden_size, (uint16_t*)out);

@@ -8,10 +8,11 @@
 //
 // Work decomposition
 //   * Tiles of BM = 64 * NRB activation rows x 256 weight rows: NRB = 4
-//     (256 rows) for the dense GEMMs, NRB = 5 (320 rows) for the MoE experts,
-//     where one 320-row tile holds every row of an expert at an even top-8
-//     routing (≈256 ± 50 rows) that 256-row tiles split into a full tile and
-//     a tail of a few rows streaming the same weights.  The grid is persistent
+//     (256 rows) for the dense GEMMs, NRB = 5 (320 rows) for MoE experts of
+//     many rows, where one 320-row tile holds every row of an expert at an
+//     even top-8 routing (≈256 ± 50 rows) that 256-row tiles split into a
+//     full tile and a tail of a few rows streaming the same weights (MoE
+//     experts of fewer rows take NRB = 4).  The grid is persistent
 //     (one 512-thread workgroup per CU).  Workgroup b runs on XCD b % 8; XCD x
 //     owns the contiguous slice [x*T/8, (x+1)*T/8) of the T tiles, walked by
 //     its workgroups in order, so the 32 tiles an XCD has in flight are

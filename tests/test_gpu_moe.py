@@ -121,8 +121,9 @@ def _oracle_moe(pack, x, idx, w, tokens=None):
     (100, 384, 128, 16, 4, torch.float16, 7),     # most experts empty
     (7, 128, 384, 4, 4, torch.bfloat16, 4),       # top_k == experts
     (300, 512, 256, 32, 8, torch.bfloat16, 32),
-    # experts with more rows than one row tile: 1000 rows each (row tiles of
-    # 320, 320, 320 and 40) and ≈470 rows each
+    # experts with more rows than one row tile: 1000 rows each (320-row tiles:
+    # 320, 320, 320 and 40) and ≈470 rows each (the routing averages 175 rows
+    # over the 8 experts: 256-row tiles of 256 and ≈210)
     (1000, 256, 128, 4, 4, torch.bfloat16, 4),
     (700, 256, 256, 8, 2, torch.float16, 3),
 ])
@@ -169,6 +170,29 @@ def test_sort_scan_forms_match_oracle(cuda, tokens, top_k, experts):
     sample = np.random.default_rng(tokens).choice(tokens, size=24, replace=False)
     expected = _oracle_moe(pack, x, idx.numpy(), w.numpy(), tokens=sample)
     assert_moe_close(np32(out)[sample], expected, "bfloat16", label=f"sort {tokens}x{top_k} E={experts}")
+
+
+def test_row_tile_heights_agree_bit_for_bit(cuda):
+    """1500 tokens x top-4 over 16 experts average 375 rows per expert, so the
+    whole call runs 320-row tiles (several per expert, with tails); 128-token
+    calls average 32 rows and run 256-row tiles.  A token's result does not
+    depend on the tile it lands in, so both must agree bit for bit; a token
+    sample is checked against the oracle."""
+    tokens, top_k, experts = 1500, 4, 16
+    banner(f"moe tile heights tokens={tokens} top_k={top_k} experts={experts}")
+    pack = _pack(experts, 256, 256, seed=11, device=cuda)
+    g = torch.Generator().manual_seed(12)
+    x = torch.randn(tokens, 256, generator=g).to(torch.bfloat16)
+    idx = torch.argsort(torch.rand(tokens, experts, generator=g), dim=1)[:, :top_k].to(torch.int32)
+    w = torch.softmax(torch.randn(tokens, top_k, generator=g), dim=1)
+    xd, idxd, wd = x.to(cuda), idx.to(cuda), w.to(cuda)
+    out = pack.forward(xd, idxd, wd)
+    parts = torch.cat([pack.forward(xd[i:i + 128], idxd[i:i + 128], wd[i:i + 128])
+                       for i in range(0, tokens, 128)])
+    assert torch.equal(out, parts)
+    sample = np.random.default_rng(13).choice(tokens, size=24, replace=False)
+    expected = _oracle_moe(pack, x, idx.numpy(), w.numpy(), tokens=sample)
+    assert_moe_close(np32(out)[sample], expected, "bfloat16", label="tile heights")
 
 
 def test_block_module_uses_grouped_path_and_matches_cpu(cuda):
