@@ -161,3 +161,79 @@ def test_swiglu_bound_accepts_fp32_accumulation_and_rejects_mistakes():
         to_dtype((to_dtype(dev[:, :half].astype(np.float32), "float16") *
                   to_dtype(dev[:, half:].astype(np.float32), "float16")).astype(np.float32), "float16")
     assert not swiglu_check(no_silu, gp, up_, "float16", gs, us)["ok"]
+
+
+def _device_block_gemm(xq, xs, wq, ws, drop_k=None, twice_block=None):
+    """Block-FP8 GEMM as the tile engine computes it: per 128-K block the
+    emulated e4m3 MFMA, then acc = fma(blk, fp32(xs * ws), acc) in fp32."""
+    xv = e4m3_decode(xq).astype(np.float32)
+    if drop_k is not None:
+        xv[:, drop_k] = 0.0
+    wv = e4m3_decode(wq).astype(np.float32)
+    wsn = np.repeat(np.asarray(ws, np.float32), 128, axis=0)[:wv.shape[0]]
+    acc = np.zeros((xv.shape[0], wv.shape[0]), np.float32)
+    for b in range(xv.shape[1] // 128):
+        sl = slice(128 * b, 128 * (b + 1))
+        blk = _e4m3_mfma(xv[:, sl], wv[:, sl])
+        sc = (np.asarray(xs, np.float32)[:, b:b + 1] * wsn[None, :, b]).astype(np.float32)
+        for _ in range(2 if b == twice_block else 1):
+            acc = (blk.astype(np.float64) * sc + acc).astype(np.float32)
+    return acc
+
+
+def _device_moe(x, idx, w, w13, s13, w2, s2, dtype, mistake=None):
+    """The routed experts as the HIP path rounds them (gate / up, silu and the
+    product to the activation dtype; silu as g * (1 / (1 + exp(-g))) in fp32;
+    e4m3 1x128 re-quantization; slot-order fp32 combine), with one planted
+    mistake when asked."""
+    from oracle import moe as omoe
+    tokens, top_k = idx.shape
+    inter = w13.shape[1] // 2
+    y = np.zeros((tokens, top_k, x.shape[1]), np.float32)
+    for e in np.unique(idx):
+        t, s = np.nonzero(idx == e)
+        rows = x[t]
+        if mistake == "row one off":
+            rows = x[(t + 1) % tokens]
+        xq, xs = formats.block_fp8_quantize_rows(rows)
+        gu = _device_block_gemm(xq, xs, w13[e], s13[e], drop_k=300 if mistake == "dropped k term" else None,
+                                twice_block=1 if mistake == "K block twice" else None)
+        g, u = to_dtype(gu[:, :inter], dtype), to_dtype(gu[:, inter:], dtype)
+        sl = to_dtype((g * (np.float32(1.0) / (np.float32(1.0) + np.exp(-g)))).astype(np.float32), dtype)
+        act = to_dtype((sl * u).astype(np.float32), dtype)
+        aq, as_ = formats.block_fp8_quantize_rows(act)
+        y[t, s] = to_dtype(_device_block_gemm(aq, as_, w2[e], s2[e]), dtype)
+    if mistake == "slot dropped":
+        w = w.copy()
+        w[:, -1] = 0.0
+    return to_dtype(omoe.combine(y, w), dtype)
+
+
+@pytest.mark.parametrize("dtype,ulps", [("bfloat16", 8.0), ("float16", 64.0)])
+def test_moe_criterion_accepts_the_device_rounding_and_rejects_mistakes(dtype, ulps):
+    """``oracle.parity.moe_check`` (the routed-expert criterion of the GPU
+    tests; fp16 outputs take 64 ulps, the same relative width as bf16's 8,
+    since the deviations come from e4m3 re-quantization flips whose size does
+    not depend on the output dtype) accepts the emulated device and rejects a
+    dropped K term, a K block counted twice, a row gathered one token off and
+    a dropped combine slot."""
+    from oracle import moe as omoe
+    from oracle.parity import moe_check
+    rng = np.random.default_rng(5)
+    tokens, hidden, inter, experts, top_k = 48, 512, 256, 4, 2
+    w13 = np.empty((experts, 2 * inter, hidden), np.uint8)
+    s13 = np.empty((experts, 2 * inter // 128, hidden // 128), np.float32)
+    w2 = np.empty((experts, hidden, inter), np.uint8)
+    s2 = np.empty((experts, hidden // 128, inter // 128), np.float32)
+    for e in range(experts):
+        w13[e], s13[e] = formats.block_fp8_quantize_weight(rng.standard_normal((2 * inter, hidden)) * 0.05)
+        w2[e], s2[e] = formats.block_fp8_quantize_weight(rng.standard_normal((hidden, inter)) * 0.05)
+    x = to_dtype(rng.standard_normal((tokens, hidden)).astype(np.float32), dtype)
+    idx = np.argsort(rng.random((tokens, experts)), axis=1)[:, :top_k]
+    w = rng.random((tokens, top_k)).astype(np.float32)
+    w /= w.sum(axis=1, keepdims=True)
+    expected = omoe.moe_forward(x, idx, w, w13, s13, w2, s2, dtype)
+    assert moe_check(_device_moe(x, idx, w, w13, s13, w2, s2, dtype), expected, dtype, ulps=ulps)["ok"]
+    for mistake in ("dropped k term", "K block twice", "row one off", "slot dropped"):
+        got = _device_moe(x, idx, w, w13, s13, w2, s2, dtype, mistake=mistake)
+        assert not moe_check(got, expected, dtype, ulps=ulps)["ok"], mistake
