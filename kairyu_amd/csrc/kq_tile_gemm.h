@@ -129,19 +129,24 @@ KQ_DEV void tg_dma4(i32x4 rsrc, uint32_t lds, int32_t voff, int32_t soff) {
   kq_rbl_lds(rsrc, (tg_lds_ptr)(uintptr_t)lds, 4, voff, soff, 0, 0);
 }
 
-KQ_DEV float tg_round_act(float v, int dtype) {
-  if (dtype == KQ_DTYPE_BF16) return (float)(__bf16)v;
-  return (float)(_Float16)v;
+// Two values rounded (to nearest even) to the 16-bit dtype and packed, low
+// half first: one v_cvt_pk_bf16_f32 / v_cvt_pk_f16_f32.
+typedef __bf16 tg_bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 tg_f16x2 __attribute__((ext_vector_type(2)));
+typedef float tg_f32x2 __attribute__((ext_vector_type(2)));
+KQ_DEV uint32_t tg_pack2(float lo, float hi, int dtype) {
+  const tg_f32x2 v = {lo, hi};
+  if (dtype == KQ_DTYPE_BF16) return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, tg_bf16x2));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, tg_f16x2));
 }
-
-KQ_DEV uint16_t tg_to_out(float v, int dtype) {
-  if (dtype == KQ_DTYPE_BF16) return __builtin_bit_cast(uint16_t, (__bf16)v);
-  return __builtin_bit_cast(uint16_t, (_Float16)v);
+// The two values of a packed pair, widened to fp32.
+KQ_DEV float tg_lo(uint32_t p, int dtype) {
+  if (dtype == KQ_DTYPE_BF16) return __uint_as_float(p << 16);
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)p);
 }
-
-KQ_DEV float tg_from_bits(uint16_t b, int dtype) {
-  if (dtype == KQ_DTYPE_BF16) return __uint_as_float((uint32_t)b << 16);
-  return (float)__builtin_bit_cast(_Float16, b);
+KQ_DEV float tg_hi(uint32_t p, int dtype) {
+  if (dtype == KQ_DTYPE_BF16) return __uint_as_float(p & 0xffff0000u);
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)(p >> 16));
 }
 
 
@@ -257,7 +262,7 @@ tile_gemm_kernel(TileGemmArgs a) {
   // current tile's K loop.  Row sources (gathered rows) and block weight
   // scales move global -> LDS by DMA (no registers held across the K loop);
   // the store epilogue's constants load into registers.
-  float pf_exs = 1.0f, pf_ews = 1.0f, pf_eb = 0.0f;
+  float pf_exs = 1.0f, pf_ews = 1.0f, pf_eb = -0.0f;  // (no bias: adds -0.0, the identity)
   auto prefetch = [&](const TgTile& tl, int wsbuf) {
     if (a.gather && wave < NRB) {
       // LDS int t of the Gat region holds tile row t's flat routed row
@@ -541,18 +546,15 @@ tile_gemm_kernel(TileGemmArgs a) {
           for (int j = 0; j < 4; ++j) {
   #pragma unroll
             for (int h = 0; h < 2; ++h) {
-              uint16_t bits[2];
-  #pragma unroll
-              for (int e = 0; e < 2; ++e) {
-                const int q = 2 * h + e;
-                const float g = tg_round_act(acc[j][mb][q], ODT);
-                const float u = tg_round_act(acc[j + 4][mb][q], ODT);
-                const float sl = tg_round_act(g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)), ODT);
-                const float v = tg_round_act(sl * u, ODT);
-                amax[mb] = fmaxf(amax[mb], fabsf(v));
-                bits[e] = tg_to_out(v, ODT);
-              }
-              pv[j][mb][h] = (uint32_t)bits[0] | ((uint32_t)bits[1] << 16);
+              // the pair q = 2h, 2h + 1, each rounding a packed conversion
+              const uint32_t gp = tg_pack2(acc[j][mb][2 * h], acc[j][mb][2 * h + 1], ODT);
+              const uint32_t up = tg_pack2(acc[j + 4][mb][2 * h], acc[j + 4][mb][2 * h + 1], ODT);
+              const float g0 = tg_lo(gp, ODT), g1 = tg_hi(gp, ODT);
+              const uint32_t sp = tg_pack2(g0 * __builtin_amdgcn_rcpf(1.0f + __expf(-g0)),
+                                           g1 * __builtin_amdgcn_rcpf(1.0f + __expf(-g1)), ODT);
+              const uint32_t vp = tg_pack2(tg_lo(sp, ODT) * tg_lo(up, ODT), tg_hi(sp, ODT) * tg_hi(up, ODT), ODT);
+              amax[mb] = fmaxf(amax[mb], fmaxf(fabsf(tg_lo(vp, ODT)), fabsf(tg_hi(vp, ODT))));
+              pv[j][mb][h] = vp;
             }
           }
         }
@@ -579,7 +581,7 @@ tile_gemm_kernel(TileGemmArgs a) {
             float v[4];
   #pragma unroll
             for (int q = 0; q < 4; ++q)
-              v[q] = fminf(fmaxf(div_by_recip(tg_from_bits((uint16_t)(pv[j][mb][q >> 1] >> (16 * (q & 1))), ODT), s, rs),
+              v[q] = fminf(fmaxf(div_by_recip((q & 1) ? tg_hi(pv[j][mb][q >> 1], ODT) : tg_lo(pv[j][mb][q >> 1], ODT), s, rs),
                                  -448.0f), 448.0f);
             const int col = 64 * wn + 16 * j + 4 * lg;
             *(uint32_t*)(stg + lrow * 128 + (((col >> 4) ^ (lrow & 7)) << 4) + (col & 15)) =
@@ -650,15 +652,18 @@ tile_gemm_kernel(TileGemmArgs a) {
                 const int ml = 16 * (mb - mg) + lr;  // staging row
                 const int grow = row0 + trow(mb);
                 const float xsc = BLOCK ? 1.0f : eX[trow(mb)];
-                uint16_t o[4];
+                // bias: -0.0 when the call has none (v + -0 == v for every v,
+                // signed zeros and NaNs included), so no branch or select
+                float v[4];
   #pragma unroll
                 for (int q = 0; q < 4; ++q) {
-                  float v = (float)acc[j][mb][q];
-                  if (!BLOCK) v = __fmul_rn(__fmul_rn(v, xsc), wsc[q]);
-                  if (a.bias_dtype != KQ_DTYPE_NONE) v = __fadd_rn(v, bv[q]);
-                  o[q] = tg_to_out(v, ODT);
+                  v[q] = (float)acc[j][mb][q];
+                  if (!BLOCK) v[q] = __fmul_rn(__fmul_rn(v[q], xsc), wsc[q]);
+                  v[q] = __fadd_rn(v[q], bv[q]);
                 }
-                const u32x2 word = u32x2{(uint32_t)o[0] | ((uint32_t)o[1] << 16), (uint32_t)o[2] | ((uint32_t)o[3] << 16)};
+                const u32x2 word = u32x2{tg_pack2(v[0], v[1], ODT), tg_pack2(v[2], v[3], ODT)};
+                const uint16_t o[4] = {(uint16_t)word[0], (uint16_t)(word[0] >> 16), (uint16_t)word[1],
+                                       (uint16_t)(word[1] >> 16)};
                 if (staged) {
                   const int cb = 32 * jj + 8 * lg;  // byte column within the 128-byte row
                   *(u32x2*)(stg + ml * 128 + (((cb >> 4) ^ (ml & 7)) << 4) + (cb & 15)) = word;
