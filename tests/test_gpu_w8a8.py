@@ -101,7 +101,7 @@ def test_int8_accumulators_and_output_bit_exact_all_paths(cuda, m, out_dtype):
 DECODE_N = 4104
 
 
-@pytest.mark.parametrize("k,m", [(1536, 1), (1536, 16), (4096, 8), (4096, 9), (8320, 5), (8320, 16)])
+@pytest.mark.parametrize("k,m", [(1536, 1), (1536, 8), (1536, 9), (1536, 16), (4096, 8), (4096, 9), (8320, 5), (8320, 16)])
 def test_int8_decode_path_bit_exact(cuda, k, m):
     banner(f"int8 decode k={k} m={m}")
     module = _int8_module(k, DECODE_N, seed=k + m).to(cuda)
