@@ -126,14 +126,16 @@ def check_block_fp8(out: torch.Tensor, x: torch.Tensor, module, label: str = "",
 
 
 def assert_moe_close(actual, expected, dtype: str, label: str = "", **criteria) -> dict:
-    """``oracle.parity.moe_check`` as an assertion (statistical criterion for
-    the routed experts, whose intermediate roundings rule out a per-element
-    bound)."""
+    """``oracle.parity.moe_check`` as an assertion: the reference's per-element
+    tolerance, the normwise maximum, per-row and per-column relative RMSE and
+    the whole-tensor statistics of the routed experts."""
 
     metrics = moe_check(actual, expected, dtype, **criteria)
-    print(f"[parity] {label} ulp bins {metrics['ulp_bins']}: {metrics['ulp_hist']} within "
-          f"{metrics['within']:.5f} normwise {metrics['normwise_max']:.3e} "
-          f"rel_rmse {metrics['rel_rmse']:.3e}", flush=True)
+    print(f"[parity] {label} ulp bins {metrics.get('ulp_bins')}: {metrics.get('ulp_hist')} within "
+          f"{metrics.get('within', 0.0):.5f} normwise {metrics.get('normwise_max', 0.0):.3e} "
+          f"rel_rmse {metrics.get('rel_rmse', 0.0):.3e} tol ratio {metrics.get('max_tol_ratio', 0.0):.3f} "
+          f"row rmse {metrics.get('max_row_rmse', 0.0):.3e} col rmse {metrics.get('max_col_rmse')}",
+          flush=True)
     assert metrics["ok"], f"{label} {metrics}"
     return metrics
 

@@ -5,8 +5,9 @@ through the same ``module(x)`` call, against the CPU oracle.
 * C1 AWQ N=K=4096 g128, M=16: every output.
 * C2 GPTQ act-order N=28672 K=4096 g128, M in {1, 4, 16, 64, 512} (the
   decode GEMV's one-round share mode, the 64x128 and 128x256 prefill tiles):
-  three 1024-column slices (first, middle, last) of every row; the oracle's
-  dequantization is per column, so a slice is exact.
+  every column of every row for M <= 16 (every workgroup share of the decode
+  GEMV), three 1024-column slices (first, middle, last) of every row above;
+  the oracle's dequantization is per column, so a slice is exact.
 * C3 FP8 N=4096 K=14336 with 1% x20 outliers, M in {1, 16, 2048, 8192} (decode
   kernel, 2-way split-K tile engine, whole-tile engine): every row for M <= 16,
   else 96 rows (the first and last 32 -- first and last row tile -- and 32
@@ -59,12 +60,14 @@ def test_c2_gptq_act_order(cuda, m):
     qweight, qzeros = module.qweight.cpu().numpy(), module.qzeros.cpu().numpy()
     scales, g_idx = np32(module.scales), module.g_idx.cpu().numpy()
     n = module.out_features
-    for c0 in (0, n // 2 - 512, n - 1024):
-        cols = slice(c0, c0 + 1024)
-        pre, terms = olinear.gptq_reference(x, qweight[:, cols], qzeros[:, c0 // 8:(c0 + 1024) // 8],
+    width = 4096 if m <= 16 else 1024
+    starts = range(0, n, width) if m <= 16 else (0, n // 2 - 512, n - 1024)
+    for c0 in starts:
+        cols = slice(c0, c0 + width)
+        pre, terms = olinear.gptq_reference(x, qweight[:, cols], qzeros[:, c0 // 8:(c0 + width) // 8],
                                             scales[:, cols], g_idx, "float16")
         assert_ulp_close(out[:, cols], pre, "float16", fp16_mfma_slack(terms, module.in_features),
-                         label=f"C2 M={m} cols {c0}:{c0 + 1024}")
+                         label=f"C2 M={m} cols {c0}:{c0 + width}")
 
 
 @pytest.mark.parametrize("m", [1, 16, 2048, 8192])

@@ -4,11 +4,15 @@ Routing: expert indices exact (stable, ties to the smaller id), weights within
 2e-6 relative (fp32 softmax; exp may differ from numpy's by an ulp).
 Activation quantization (1x128 blocks): bytes and scales bit-exact.
 Dense block-FP8 linear: every output within one ulp (plus an fp32
-accumulation slack) of the fp64-accumulated oracle.  Routed experts: at least
-95% of the outputs within eight ulps (fp16 at C5's widths: 64, the same
-relative width) and relative RMSE <= 5e-3 of the oracle
-(``gpu_helpers.assert_moe_close`` says why no per-element bound holds there;
-``tests/test_parity_bounds.py`` pins the criterion with planted mistakes).
+accumulation slack) of the fp64-accumulated oracle.  Routed experts
+(``oracle.parity.moe_check``): every output within the reference's grouped-MoE
+tolerance (atol 2e-2 + rtol 1e-2), the normwise maximum within 1e-2 at C5's
+widths (2e-2 for the narrower synthetic layers, where one e4m3
+re-quantization flip of the SwiGLU product moves an output by up to 1.4e-2 of
+the largest output on the emulated device), every token row's and output
+column's relative RMSE bounded, at least 95% of the outputs within eight ulps
+(fp16 at C5's widths: 64, the same relative width) and relative RMSE <= 5e-3
+(``tests/test_parity_bounds.py`` pins the criterion with planted mistakes).
 Parity of the block-FP8 expert arithmetic is unpinned at the reference boundary (its hub kernel is not
 vendored); every piece is pinned by the oracle's own tests.
 """
@@ -32,6 +36,30 @@ pytestmark = pytest.mark.gpu
 
 
 _DT = {torch.bfloat16: "bfloat16", torch.float16: "float16"}
+# normwise bound of the layers whose reductions are narrower than C5's (module docstring)
+_NARROW = {"normwise": 2e-2}
+
+
+def _covering_sample(idx: np.ndarray, experts: int, size: int, seed: int) -> np.ndarray:
+    """Tokens that reach every routed expert's first row and the last row
+    block (16 rows) of each of its row tiles, topped up with seeded others to
+    ``size``.  Rows of an expert are its tokens in ascending order, tiles are
+    320 rows when the routing averages more than 192 rows per expert, else
+    256 (kq_moe.hip)."""
+    tokens, top_k = idx.shape
+    bm = 320 if tokens * top_k > 192 * experts else 256
+    chosen = set()
+    for e in range(experts):
+        rows = np.nonzero((idx == e).any(axis=1))[0]
+        if rows.size == 0:
+            continue
+        chosen.add(int(rows[0]))
+        for start in range(0, rows.size, bm):
+            chosen.add(int(rows[min(rows.size, start + bm) - 1]))
+    rest = np.setdiff1d(np.arange(tokens), np.fromiter(chosen, np.int64))
+    fill = max(0, size - len(chosen))
+    extra = np.random.default_rng(seed).choice(rest, size=min(fill, rest.size), replace=False)
+    return np.sort(np.concatenate([np.fromiter(chosen, np.int64), extra]))
 
 
 def _bits(t: torch.Tensor) -> np.ndarray:
@@ -103,10 +131,10 @@ def test_dense_block_fp8_linear_matches_oracle(cuda, m, n, dtype):
     check_block_fp8(out, x, module, label=f"dense m={m} n={n}")
 
 
-def _pack(experts, hidden, inter, seed, device):
+def _pack(experts, hidden, inter, seed, device, std=0.05):
     g = torch.Generator().manual_seed(seed)
-    q13, s13 = quantize_block_fp8(torch.randn(experts, 2 * inter, hidden, generator=g) * 0.05)
-    q2, s2 = quantize_block_fp8(torch.randn(experts, hidden, inter, generator=g) * 0.05)
+    q13, s13 = quantize_block_fp8(torch.randn(experts, 2 * inter, hidden, generator=g) * std)
+    q2, s2 = quantize_block_fp8(torch.randn(experts, hidden, inter, generator=g) * std)
     return hmoe.GroupedBlockFp8Experts.from_tensors(q13.to(device), s13.to(device), q2.to(device), s2.to(device))
 
 
@@ -141,7 +169,7 @@ def test_routed_block_fp8_experts_match_oracle(cuda, cfg):
     out = pack.forward(x.to(cuda), idx, w)
     assert out.dtype == dtype
     expected = _oracle_moe(pack, x, idx.cpu().numpy(), w.cpu().numpy())
-    assert_moe_close(np32(out), expected, _DT[dtype], label=str(cfg))
+    assert_moe_close(np32(out), expected, _DT[dtype], label=str(cfg), **_NARROW)
 
 
 @pytest.mark.parametrize("tokens,top_k,experts", [
@@ -169,9 +197,10 @@ def test_sort_scan_forms_match_oracle(cuda, tokens, top_k, experts):
     parts = torch.cat([pack.forward(xd[i:i + 256], idxd[i:i + 256], wd[i:i + 256])
                        for i in range(0, tokens, 256)])
     assert torch.equal(out, parts)
-    sample = np.random.default_rng(tokens).choice(tokens, size=24, replace=False)
+    sample = np.random.default_rng(tokens).choice(tokens, size=64, replace=False)
     expected = _oracle_moe(pack, x, idx.numpy(), w.numpy(), tokens=sample)
-    assert_moe_close(np32(out)[sample], expected, "bfloat16", label=f"sort {tokens}x{top_k} E={experts}")
+    assert_moe_close(np32(out)[sample], expected, "bfloat16", label=f"sort {tokens}x{top_k} E={experts}",
+                     **_NARROW)
 
 
 def test_row_tile_heights_agree_bit_for_bit(cuda):
@@ -192,15 +221,17 @@ def test_row_tile_heights_agree_bit_for_bit(cuda):
     parts = torch.cat([pack.forward(xd[i:i + 128], idxd[i:i + 128], wd[i:i + 128])
                        for i in range(0, tokens, 128)])
     assert torch.equal(out, parts)
-    sample = np.random.default_rng(13).choice(tokens, size=24, replace=False)
+    sample = _covering_sample(idx.numpy(), experts, 96, seed=13)
     expected = _oracle_moe(pack, x, idx.numpy(), w.numpy(), tokens=sample)
-    assert_moe_close(np32(out)[sample], expected, "bfloat16", label="tile heights")
+    assert_moe_close(np32(out)[sample], expected, "bfloat16", label="tile heights", **_NARROW)
 
 
 def test_fp16_experts_at_c5_widths_sampled_tokens(cuda):
     """fp16 activations through the 320-row tiles at C5's hidden / intermediate
-    widths (K = 2048 for gate_up, 768 for down): 1024 tokens x top-8 over 32
-    experts average 256 rows per expert; 24 sampled tokens against the oracle.
+    widths (K = 2048 for gate_up, 768 for down) and weight distribution
+    (N(0, 0.02) before block quantization): 1024 tokens x top-8 over 32
+    experts average 256 rows per expert; 160 tokens against the oracle, among
+    them every expert's first row and the last row block of each row tile.
     fp16 outputs take 64 ulps (the relative width of bf16's 8): the e4m3
     re-quantization flips of the SwiGLU product move outputs by the same
     relative amount in either dtype, which at these widths is 8 or more fp16
@@ -208,19 +239,19 @@ def test_fp16_experts_at_c5_widths_sampled_tokens(cuda):
     bound (5e-3) is unchanged."""
     tokens, hidden, inter, experts, top_k = 1024, 2048, 768, 32, 8
     banner("moe fp16 C5 widths")
-    pack = _pack(experts, hidden, inter, seed=21, device=cuda)
+    pack = _pack(experts, hidden, inter, seed=21, device=cuda, std=0.02)  # C5's weight distribution
     g = torch.Generator().manual_seed(22)
     x = torch.randn(tokens, hidden, generator=g).to(torch.float16)
     logits = torch.randn(tokens, experts, generator=g)
     idx, w = hmoe.route_logits(logits.to(cuda), top_k)
     out = pack.forward(x.to(cuda), idx, w)
     assert out.dtype == torch.float16
-    sample = np.random.default_rng(23).choice(tokens, size=24, replace=False)
+    sample = _covering_sample(idx.cpu().numpy(), experts, 160, seed=23)
     expected = _oracle_moe(pack, x, idx.cpu().numpy(), w.cpu().numpy(), tokens=sample)
     assert_moe_close(np32(out)[sample], expected, "float16", label="fp16 C5 widths", ulps=64.0)
 
 
-def test_block_module_uses_grouped_path_and_matches_cpu(cuda):
+def test_block_module_uses_grouped_path_and_matches_oracle(cuda):
     torch.manual_seed(2)
     block = hmoe.Qwen3BlockFp8MoeBlock(256, 128, 8, 2)
     hmoe.quantize_experts(block, torch.randn(8, 256, 256) * 0.05, torch.randn(8, 256, 128) * 0.05)
@@ -229,13 +260,14 @@ def test_block_module_uses_grouped_path_and_matches_cpu(cuda):
     block.gate.to(torch.bfloat16)
     x = torch.randn(2, 9, 256).to(torch.bfloat16)
     with torch.no_grad():
-        cpu_out = block(x)
         block = block.to(cuda)
-        assert block._grouped_experts is not None and block._grouped_experts.w13.is_cuda
+        pack = block._grouped_experts
+        assert pack is not None and pack.w13.is_cuda
         gpu_out = block(x.to(cuda))
+        idx, w = hmoe.route_logits(block.gate(x.to(cuda).reshape(-1, 256)), 2)
     assert gpu_out.shape == x.shape
-    err = (gpu_out.float().cpu() - cpu_out.float()).abs().max() / cpu_out.float().abs().max()
-    assert err < 1e-2
+    expected = _oracle_moe(pack, x.reshape(-1, 256), idx.cpu().numpy(), w.cpu().numpy())
+    assert_moe_close(np32(gpu_out).reshape(-1, 256), expected, "bfloat16", label="block module", **_NARROW)
 
 
 def test_c5_shape_sampled_tokens_and_determinism(cuda):
@@ -249,10 +281,14 @@ def test_c5_shape_sampled_tokens_and_determinism(cuda):
     idx, w = hmoe.route_logits(mod.logits, mod.top_k)
     counts = torch.bincount(idx.reshape(-1), minlength=128)
     assert int(counts.sum()) == 4096 * 8
-    sample = np.random.default_rng(0).choice(4096, size=24, replace=False)
+    # every expert's first row and the last row block of its row tile, 320 tokens in all
+    sample = _covering_sample(idx.cpu().numpy(), 128, 320, seed=0)
+    assert len(sample) >= 256
+    reached = np.unique(idx.cpu().numpy()[sample])
+    assert reached.size == 128
     pack = hmoe.GroupedBlockFp8Experts.from_tensors(mod.w13, mod.s13, mod.w2, mod.s2)
     expected = _oracle_moe(pack, wl.x.cpu(), idx.cpu().numpy(), w.cpu().numpy(), tokens=sample)
-    assert_moe_close(np32(out1)[sample], expected, "bfloat16", label="C5 sample")
+    assert_moe_close(np32(out1)[sample], expected, "bfloat16", label=f"C5 {len(sample)} tokens")
 
 
 def test_graph_replays_match_eager(cuda):
@@ -331,7 +367,7 @@ def test_factory_built_block_packs_its_experts_and_matches_oracle(cuda):
         out = block(x)
         idx, w = hmoe.route_logits(block.gate(x), 2)
     expected = _oracle_moe(pack, x.cpu(), idx.cpu().numpy(), w.cpu().numpy())
-    assert_moe_close(np32(out), expected, "bfloat16", label="factory block")
+    assert_moe_close(np32(out), expected, "bfloat16", label="factory block", **_NARROW)
     # an expert projection on its own runs the bound dense block-FP8 kernel
     single = block.experts[3].up_proj(x)
     check_block_fp8(single, x, block.experts[3].up_proj, label="factory expert up_proj")
@@ -346,7 +382,7 @@ def test_single_route_with_empty_trailing_experts(cuda):
     w = torch.ones(1, 1, dtype=torch.float32, device=cuda)
     out = pack.forward(x, idx, w)
     expected = _oracle_moe(pack, x.cpu(), idx.cpu().numpy(), w.cpu().numpy())
-    assert_moe_close(np32(out), expected, "bfloat16", label="single route")
+    assert_moe_close(np32(out), expected, "bfloat16", label="single route", **_NARROW)
     # weight 1 on one slot: the combine is the expert's own output
     alone = moe.expert_forward(np32(x), _bits(pack.w13)[0], pack.s13[0].cpu().numpy(),
                                _bits(pack.w2)[0], pack.s2[0].cpu().numpy())

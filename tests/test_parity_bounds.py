@@ -237,3 +237,44 @@ def test_moe_criterion_accepts_the_device_rounding_and_rejects_mistakes(dtype, u
     for mistake in ("dropped k term", "K block twice", "row one off", "slot dropped"):
         got = _device_moe(x, idx, w, w13, s13, w2, s2, dtype, mistake=mistake)
         assert not moe_check(got, expected, dtype, ulps=ulps)["ok"], mistake
+
+
+@pytest.mark.parametrize("dtype,ulps", [("bfloat16", 8.0), ("float16", 64.0)])
+def test_moe_criterion_rejects_mistakes_confined_to_one_tile_or_column(dtype, ulps):
+    """Mistakes that touch too few outputs for the whole-tensor statistics
+    (at this size the ulp fraction and the relative RMSE alone accept both):
+    one expert's 16 x 16 output tile 10% off (a wrong scale for one MFMA
+    block) and one output column 5% off across every token.  The normwise
+    maximum and the per-column RMSE reject them; the emulated device passes.
+    Weights ~ N(0, 0.02) as in C5; reductions 4-8x narrower than C5's, so the
+    normwise bound is the narrow-width one (2e-2)."""
+    from oracle import moe as omoe
+    from oracle.parity import moe_check
+    rng = np.random.default_rng(12)
+    tokens, hidden, inter, experts, top_k = 192, 1024, 256, 16, 4
+    w13 = np.empty((experts, 2 * inter, hidden), np.uint8)
+    s13 = np.empty((experts, 2 * inter // 128, hidden // 128), np.float32)
+    w2 = np.empty((experts, hidden, inter), np.uint8)
+    s2 = np.empty((experts, hidden // 128, inter // 128), np.float32)
+    for e in range(experts):
+        w13[e], s13[e] = formats.block_fp8_quantize_weight(rng.standard_normal((2 * inter, hidden)) * 0.02)
+        w2[e], s2[e] = formats.block_fp8_quantize_weight(rng.standard_normal((hidden, inter)) * 0.02)
+    x = to_dtype(rng.standard_normal((tokens, hidden)).astype(np.float32), dtype)
+    idx = np.argsort(rng.random((tokens, experts)), axis=1)[:, :top_k]
+    w = rng.random((tokens, top_k)).astype(np.float32)
+    w /= w.sum(axis=1, keepdims=True)
+    expected = omoe.moe_forward(x, idx, w, w13, s13, w2, s2, dtype).astype(np.float64)
+    device = _device_moe(x, idx, w, w13, s13, w2, s2, dtype).astype(np.float64)
+    criterion = dict(ulps=ulps, normwise=2e-2)
+    whole_tensor_only = dict(ulps=ulps, atol=np.inf, normwise=np.inf, row_rmse=np.inf, col_rmse=np.inf)
+    assert moe_check(device, expected, dtype, **criterion)["ok"]
+    tile = device.copy()
+    rows = np.nonzero((idx == 3).any(axis=1))[0][:16]
+    cols = np.arange(32, 48)
+    tile[np.ix_(rows, cols)] *= 1.1
+    column = device.copy()
+    column[:, 37] *= 1.05
+    for name, got in (("one expert's 16x16 tile", tile), ("one column", column)):
+        assert moe_check(got, expected, dtype, **whole_tensor_only)["ok"], name
+        assert not moe_check(got, expected, dtype, **criterion)["ok"], name
+    assert "column 37" in moe_check(column, expected, dtype, **criterion)["why"]
