@@ -247,8 +247,10 @@ int kq_swiglu(const void* src, int64_t ld_src, int interleaved, int dtype, void*
  * allocating library routine), for callers that cannot allocate: code under
  * HIP graph capture, tight serving loops, harnesses that forbid allocation.
  * Calls on one GPU share its array: calls that overlap on one GPU (two
- * streams, or two threads) race; order them on one stream.  No counterpart in
- * the reference. */
+ * streams, or two threads) race; order them on one stream.  The first call on
+ * each GPU resolves the array's device address (hipGetSymbolAddress), so make
+ * one eager call per GPU before capturing this entry in a HIP graph; captured
+ * launches then replay with no host work.  No counterpart in the reference. */
 #define KQ_W4A16_NOALLOC_SCRATCH_BYTES (16u << 20)
 int kq_w4a16_tiled_gemm_noalloc(const void* x, int x_dtype, const int32_t* tiles,
                                 const int32_t* qzeros, int zero_offset, const void* scales,
@@ -316,6 +318,29 @@ int kq_moe_block_fp8_experts(const void* hidden, int dtype, int64_t tokens, int6
                              const float* topk_w, const uint8_t* w13, const float* s13,
                              const uint8_t* w2, const float* s2, void* out, void* workspace,
                              size_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------- ceilings
+ * Measurement aids, no counterpart in the reference: the box's own ceilings
+ * that bench.py --peaks reports next to the vendor peaks.  `sink` is device
+ * memory of workgroups * 256 uint32 (written only if a fold of the data hits
+ * a fixed value, which keeps the work live). */
+
+/* Streaming read of `bytes` (a positive multiple of 16, 16-byte aligned) from
+ * `src`: 256-thread workgroups, grid-strided 16-byte loads, 8 in flight per
+ * thread.  Bytes moved per launch = `bytes`. */
+int kq_peak_stream_read(const void* src, int64_t bytes, int workgroups, void* sink, void* stream);
+
+/* Register-only MFMA loop: every wave of `workgroups` 256-thread workgroups
+ * runs `iterations` x KQ_PEAK_MFMA_CHAINS independent MFMAs of `kind`:
+ *   KQ_PEAK_FP16  v_mfma_f32_16x16x32_f16            16384 FLOP each
+ *   KQ_PEAK_FP8   v_mfma_scale_f32_16x16x128_f8f6f4  65536 FLOP each (e4m3)
+ *   KQ_PEAK_INT8  v_mfma_i32_16x16x64_i8             32768 OP each
+ * (the instructions the W4A16, FP8 and INT8 GEMMs issue). */
+#define KQ_PEAK_FP16 0
+#define KQ_PEAK_FP8 1
+#define KQ_PEAK_INT8 2
+#define KQ_PEAK_MFMA_CHAINS 8
+int kq_peak_mfma(int kind, int64_t iterations, int workgroups, void* sink, void* stream);
 
 #ifdef __cplusplus
 }

@@ -77,6 +77,8 @@ _SIGNATURES: dict[str, list] = {
     "kq_act_quant_fp8_blocks": [_P, _I, _I64, _I64, _I64, _P, _P, _P],
     "kq_block_fp8_gemm": [_P, _P, _P, _P, _P, _I, _P, _I, _I64, _I64, _I64, _P],
     "kq_moe_workspace_size": [_I64, _I64, _I64, _I64, _I],
+    "kq_peak_stream_read": [_P, _I64, _I, _P, _P],
+    "kq_peak_mfma": [_I, _I64, _I, _P, _P],
     "kq_moe_block_fp8_experts": [
         _P, _I, _I64, _I64, _I64, _I64, _I, _P, _P, _P, _P, _P, _P, _P, _P, _SZ, _P,
     ],

@@ -37,6 +37,12 @@ HIPCC_FLAGS = [
 ]
 
 
+# Per-source additions.  kq_peaks.hip: MFMA results in VGPRs, so the
+# register-only MFMA loop carries its accumulators without AGPR copies (the
+# default form moves them between AGPRs and VGPRs every iteration there).
+EXTRA_FLAGS = {"kq_peaks.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+
+
 def hipcc() -> str:
     candidates = [os.environ.get("HIPCC"), shutil.which("hipcc"), "/opt/rocm/bin/hipcc"]
     for candidate in candidates:
@@ -47,7 +53,7 @@ def hipcc() -> str:
 
 def _compile(source: Path, compiler: str) -> Path:
     obj = BUILD_DIR / (source.stem + ".o")
-    cmd = [compiler, *HIPCC_FLAGS, "-c", str(source), "-o", str(obj)]
+    cmd = [compiler, *HIPCC_FLAGS, *EXTRA_FLAGS.get(source.name, []), "-c", str(source), "-o", str(obj)]
     result = subprocess.run(cmd, capture_output=True, text=True)
     if result.returncode != 0:
         raise RuntimeError(f"hipcc failed for {source.name}:\n{result.stderr}")

@@ -415,23 +415,32 @@ def _gptq_operands(module, device: torch.device):
         return cached[1]
     _refuse_under_capture("GPTQ")
     k, n, group = module.in_features, module.out_features, module.group_size
-    natural = torch.arange(k, device=device, dtype=torch.int64) // group
-    gi = g_idx.to(torch.int64)
+    mode, perm32 = gptq_group_mode(g_idx, k, group, device)
     result = (GIDX_PER_K, qweight, None)
-    if group % 8 == 0:
-        if torch.equal(gi, natural):
-            tiled = tile_operand(qweight, 1, None, qzeros, 1, scales, n, k, group, device)
-            if tiled is not None:
-                result = (GIDX_UNIFORM, tiled, None)
-        else:
-            perm = torch.argsort(gi, stable=True)
-            if torch.equal(gi[perm], natural):
-                perm32 = perm.to(torch.int32).contiguous()
-                tiled = tile_operand(qweight, 1, perm32, qzeros, 1, scales, n, k, group, device)
-                if tiled is not None:
-                    result = (GIDX_PERMUTED, tiled, perm32)
+    if mode != GIDX_PER_K:
+        tiled = tile_operand(qweight, 1, perm32, qzeros, 1, scales, n, k, group, device)
+        if tiled is not None:
+            result = (mode, tiled, perm32)
     object.__setattr__(module, "_kq_gptq_operands", (key, result))
     return result
+
+
+def gptq_group_mode(g_idx: torch.Tensor, k: int, group: int, device: torch.device):
+    """(gidx_mode, perm int32 or None) of a GPTQ ``g_idx`` without building
+    any operand: ``GIDX_UNIFORM`` when ``g_idx == k // group``,
+    ``GIDX_PERMUTED`` with the stable argsort when that sort groups every
+    ``group`` rows together (act-order), else ``GIDX_PER_K``."""
+
+    if group % 8 != 0:
+        return GIDX_PER_K, None
+    natural = torch.arange(k, device=device, dtype=torch.int64) // group
+    gi = g_idx.to(device=device, dtype=torch.int64)
+    if torch.equal(gi, natural):
+        return GIDX_UNIFORM, None
+    perm = torch.argsort(gi, stable=True)
+    if torch.equal(gi[perm], natural):
+        return GIDX_PERMUTED, perm.to(torch.int32).contiguous()
+    return GIDX_PER_K, None
 
 
 def gptq_linear_forward(x: torch.Tensor, module, *, add_bias: bool = True) -> torch.Tensor:

@@ -136,9 +136,10 @@ class QuantLinearPack:
             if scheme == "gptq":
                 if any(not torch.equal(m.g_idx, first.g_idx) for m in mods):
                     return None
-                from kairyu_amd.kernels.quant_gemm_hip import GIDX_PER_K, _gptq_operands
+                from kairyu_amd.kernels.quant_gemm_hip import GIDX_PER_K, gptq_group_mode
 
-                if device.type == "cuda" and _gptq_operands(first, device)[0] == GIDX_PER_K:
+                if device.type == "cuda" and gptq_group_mode(
+                        first.g_idx, first.in_features, first.group_size, device)[0] == GIDX_PER_K:
                     return None
         return cls(mods, scheme, weight)
 
@@ -336,7 +337,12 @@ class QuantLinearPack:
                             hip.awq_natural_zeros(up.qzeros, up.out_features, device), 2)
                 qweight, fmt, zoff, d["perm"], d["mode"] = mix(gate.qweight, up.qweight, 2), 0, 0, None, hip.GIDX_UNIFORM
             else:
-                mode, _, perm = hip._gptq_operands(gate, device)
+                if not torch.equal(up.g_idx, gate.g_idx):
+                    # one activation gather serves both halves
+                    raise RuntimeError("packed GPTQ projections need one g_idx")
+                # the group mode and permutation alone: tiling gate on its own
+                # here would cache a second tiled copy of its weights
+                mode, perm = hip.gptq_group_mode(gate.g_idx, gate.in_features, gate.group_size, device)
                 if mode == hip.GIDX_PER_K:
                     raise RuntimeError("GPTQ swiglu pack requires uniform or act-order groups")
                 zeros = mix(gate.qzeros, up.qzeros, 2)
@@ -345,6 +351,9 @@ class QuantLinearPack:
                                           2 * gate.out_features, gate.in_features, gate.group_size, device)
             if d["tiled"] is None:
                 raise RuntimeError("swiglu pack requires tileable projections")
+            for m in (gate, up):  # the pack holds the only tiled copies
+                m.__dict__.pop("_kq_gptq_operands", None)
+                m.__dict__.pop("_kq_awq_operands", None)
         self._swiglu, self._swiglu_key = d, key
         return d
 

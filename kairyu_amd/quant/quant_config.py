@@ -257,3 +257,18 @@ def load_checkpoint_quantization(model_dir: str | Path, hf_config: dict) -> Chec
         producer_name=name,
         producer_version=version,
     )
+
+
+def validate_model_quantization(quant: QuantConfig, *, is_mla: bool, architecture: str) -> None:
+    """Reject quantization combinations before the model is built
+    (kairyu/engine/core/quant_config.py:308-321, called by the reference's
+    loader at kairyu/models/loader.py:186): an MLA architecture's absorbed KV
+    projection needs an unquantized ``kv_b_proj`` weight, so any quantized
+    checkpoint is refused for it, with the reference's message."""
+
+    if is_mla and quant.method is not QuantMethod.NONE:
+        raise ValueError(
+            f"{architecture} MLA does not support {quant.method.value} "
+            "checkpoints: its absorbed KV projection requires an unquantized "
+            "kv_b_proj weight"
+        )

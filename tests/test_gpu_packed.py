@@ -147,6 +147,13 @@ _SWIGLU_CASES = [
     ("gptq", 100, 1024, 1024, torch.bfloat16, False),      # prefill: GEMM + elementwise pass
     ("gptq-sym-ao", 7, 4128, 512, torch.float16, False),   # skinny shape: two passes
     ("awq", 64, 2048, 1024, torch.float16, False),
+    # real MLP widths: 2-4 gate/up pairs per workgroup, uneven shares, K = 2048 (S = 4)
+    ("gptq-sym-ao", 1, 4096, 14336, torch.float16, False),
+    ("gptq", 16, 4096, 14336, torch.bfloat16, False),
+    ("gptq-sym", 1, 4096, 11008, torch.float16, False),
+    ("awq", 16, 4096, 11008, torch.float16, False),
+    ("gptq-sym-ao", 16, 2048, 14336, torch.float16, False),
+    ("gptq", 1, 2048, 11008, torch.bfloat16, True),
     ("fp8", 1, 2048, 2048, torch.bfloat16, True),
     ("fp8", 300, 1024, 1024, torch.float16, False),
     ("int8", 16, 2048, 1024, torch.bfloat16, True),
@@ -217,3 +224,36 @@ def test_swiglu_pack_in_a_graph(cuda):
         graph.replay()
         torch.cuda.synchronize()
         assert torch.equal(out, eager)
+
+
+@pytest.mark.parametrize("scheme", ["gptq-ao", "awq"])
+def test_swiglu_pack_holds_the_only_tiled_copy(cuda, scheme):
+    """After ``pack.swiglu`` neither projection keeps a tiled operand of its
+    own: the interleaved (gate, up) operand is the only derived copy of the
+    4-bit weights (a second per-module copy would add half of gate/up's
+    weight bytes per layer)."""
+
+    gate, up = (mod.to(cuda) for mod in _swiglu_pair(scheme, 2048, 2048, False, seed=8))
+    pack = QuantLinearPack.create([gate, up])
+    assert pack is not None
+    for mod in (gate, up):
+        assert "_kq_gptq_operands" not in mod.__dict__ and "_kq_awq_operands" not in mod.__dict__
+    x = torch.randn(4, 2048, generator=torch.Generator().manual_seed(9)).to(torch.float16).to(cuda)
+    pack.swiglu(x)
+    for mod in (gate, up):
+        assert "_kq_gptq_operands" not in mod.__dict__ and "_kq_awq_operands" not in mod.__dict__
+
+
+def test_swiglu_pack_rejects_diverged_g_idx(cuda):
+    """An act-order pack whose up projection's ``g_idx`` is changed in place to
+    another permutation cannot share one activation gather: the rebuilt
+    operand raises instead of applying gate's permutation to up."""
+
+    gate, up = (mod.to(cuda) for mod in _swiglu_pair("gptq-ao", 2048, 2048, False, seed=10))
+    pack = QuantLinearPack.create([gate, up])
+    x = torch.randn(4, 2048, generator=torch.Generator().manual_seed(11)).to(torch.float16).to(cuda)
+    pack.swiglu(x)
+    other = (torch.randperm(2048, generator=torch.Generator().manual_seed(12)) // 128).to(torch.int32)
+    up.g_idx.copy_(other.to(cuda))
+    with pytest.raises(RuntimeError, match="one g_idx"):
+        pack.swiglu(x)

@@ -302,3 +302,18 @@ def test_quantized_scales_normalize_to_the_kernel_dtype_at_bf16_compute_dtype():
     assert out["proj.bias"].dtype is torch.bfloat16 and out["norm.weight"].dtype is torch.bfloat16
     model.load_state_dict(out, strict=True, assign=True)
     assert model.proj.weight_scale.dtype is torch.float32
+
+
+def test_validate_model_quantization_rejects_quantized_mla():
+    """kairyu/engine/core/quant_config.py:308-321: a quantized checkpoint is
+    refused for an MLA architecture before the model is built; dense MLA and
+    quantized non-MLA models pass."""
+    from kairyu_amd.quant.quant_config import QuantConfig, QuantMethod, validate_model_quantization
+
+    fp8 = detect_quantization({"quantization_config": {"quant_method": "fp8"}})
+    with pytest.raises(ValueError, match="DeepseekV3ForCausalLM MLA does not support fp8 checkpoints: "
+                                         "its absorbed KV projection requires an unquantized kv_b_proj weight"):
+        validate_model_quantization(fp8, is_mla=True, architecture="DeepseekV3ForCausalLM")
+    validate_model_quantization(fp8, is_mla=False, architecture="LlamaForCausalLM")
+    validate_model_quantization(QuantConfig(method=QuantMethod.NONE), is_mla=True,
+                                architecture="DeepseekV3ForCausalLM")

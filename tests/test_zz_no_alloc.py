@@ -82,3 +82,36 @@ def test_noalloc_rejects_shapes_beyond_the_fixed_scratch(cuda):
     x = torch.randn(8, 4096, device=cuda, dtype=torch.float16)
     got = _run("kq_w4a16_tiled_gemm_noalloc", module, x, cuda)
     assert torch.equal(got, _run("kq_w4a16_tiled_gemm", module, x, cuda))
+
+
+@pytest.mark.parametrize("m", [16, 64])
+def test_noalloc_captured_in_a_graph_replays_the_eager_result(cuda, m):
+    """One eager call (it resolves the array's device address), then the
+    allocation-free call captured in a HIP graph: every replay, with other
+    calls of the entry between replays overwriting the shared array, is
+    bit-equal to the eager output (act-order gather and decode GEMV at
+    m = 16, staged prefill at m = 64)."""
+    k, n, group = 4096, 2048, 128
+    g = torch.Generator().manual_seed(43)
+    g_idx = (torch.randperm(k, generator=g) // group).to(torch.int32)
+    module = _gptq_module(k, n, group=group, seed=43, g_idx=g_idx, random_packed=True).to(cuda)
+    x = torch.randn(m, k, generator=g).to(torch.float16).to(cuda)
+    other = torch.randn(m + 7, k, generator=g).to(torch.float16).to(cuda)
+    banner(f"noalloc graph m={m}")
+    eager = _run("kq_w4a16_tiled_gemm_noalloc", module, x, cuda).clone()
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        _run("kq_w4a16_tiled_gemm_noalloc", module, x, cuda)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        captured = _run("kq_w4a16_tiled_gemm_noalloc", module, x, cuda)
+    for i in range(4):
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(captured.view(torch.int16), eager.view(torch.int16)), i
+        _run("kq_w4a16_tiled_gemm_noalloc", module, other, cuda)  # eager work on the same array
+        torch.cuda.synchronize()
