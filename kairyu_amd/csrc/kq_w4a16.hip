@@ -11,9 +11,10 @@
 // fp16((q-z)*s) as the reference's fp32 product rounded to fp16.
 //
 // Kernels:
-//   * decode GEMV (M <= 16, K in {1024, 2048, 4096}, load-time tiled weights):
-//     one 16-wave workgroup per CU, x held in registers, weights streamed
-//     through buffer loads with three 16-column blocks in flight (below);
+//   * decode GEMV (M <= 16, K % 128 == 0, load-time tiled weights): 16-wave
+//     workgroups, x held in registers, weights streamed through buffer loads
+//     with three 16-column blocks in flight; K beyond 4096 split across
+//     workgroups (below);
 //   * skinny kernel (every other shape, checkpoint or tiled layout), next.
 //
 // Skinny kernel (M <= 64 per row block): a workgroup owns 64 output columns; its
@@ -548,12 +549,16 @@ w4a16_skinny_kernel(W4Args a) {
 }
 
 // ---------------------------------------------------------------------------
-// Decode GEMV (M <= 16, K = 16 waves x S steps x 32 with S in {2, 4, 8},
-// group_size a multiple of 32 whose boundaries fall at fixed steps of every
-// wave's window).
+// Decode GEMV (M <= 16, K % 128 == 0 in windows of S steps x 32 with S in
+// {2, 4, 8}, group_size a multiple of 32 whose boundaries fall at fixed steps
+// of every wave's window).
 //
-// One 16-wave workgroup per CU owns a balanced run of 16-column blocks.  Wave
-// w owns steps [w*S, w*S + S): it loads those x chunks once as MFMA A
+// A 16-wave workgroup (one per CU) owns a balanced run of 16-column blocks
+// and one K chunk of at most 16 windows (all of K up to 4096 at S = 8; longer
+// K runs several chunks, grid y, whose fp32 partials a reduce pass adds in
+// chunk order).  Wave w owns steps [c0 + w*S, c0 + w*S + S) of the chunk
+// starting at step c0 (none when that lies past the chunk or past K: the
+// wave then loads nothing and adds zeros): it loads those x chunks once as MFMA A
 // operands and keeps them in registers while it streams the weights of every
 // column block of the workgroup with D blocks in flight, so x is read once
 // per wave rather than once per column block.  Lane (j = l%16, kb = l/16)
@@ -574,6 +579,7 @@ constexpr int kGvWaves = 16;
 
 struct GvPlan {
   int wgs, units;
+  int splits, sps;  // K splits (grid y) and steps of 32 per split
 };
 
 template <int S, int SPG>
@@ -585,6 +591,8 @@ struct GvShape {
   static constexpr int kDepth = (S + 2 * kGroups) > 16 ? 2
                                 : (S >= 8 || (S + 2 * kGroups) > 12) ? 3 : 4;
   static constexpr int kRound = kDepth;  // blocks per reduction round (several rounds)
+  // a share of at most kShort blocks has all of them in flight at once
+  static constexpr int kShort = kDepth + 1;
   // a workgroup's whole share in one round (at least 8 blocks: 7 on C2)
   static constexpr int kOneRound = 2 * kDepth < 8 ? 8 : 2 * kDepth;
 };
@@ -605,6 +613,7 @@ struct GvCtx {
   int pairs;             // tiles: group pairs per column tile
   int st0;               // first step of this wave
   int g0;                // group of the first step
+  bool wlive;            // the wave's window lies inside K (else it loads nothing)
 };
 
 // Loads of one block in the order its compute consumes them (the group's
@@ -624,6 +633,7 @@ KQ_DEV i32x4 select_rsrc(bool live, const i32x4& r, const i32x4& dead) {
 template <int S, int SPG, int LAYOUT>
 KQ_DEV void gv_load(const W4Args& a, const GvCtx& c, int unit, bool live, GvBlock<S, SPG>& b) {
   constexpr int NG = GvShape<S, SPG>::kGroups;
+  live = live && c.wlive;
   const i32x4 rw = select_rsrc(live, c.rw, c.rnull);
   if constexpr (LAYOUT == kLayoutTilesZu) {
     // scales alone: one 2-byte scale (a single group) or 4 bytes per group pair
@@ -724,7 +734,9 @@ KQ_DEV f32x4 gv_compute(const W4Args& a, const NibbleConsts& nc, uint32_t zsh,
 // MODE kGvOne: the launch guarantees ncb <= kOneRound blocks per workgroup,
 // so one round with the accumulators of all of them in registers (no outer
 // loop).
-// kGvShort: ncb <= D, one round of D blocks.  kGvSingle: every workgroup owns
+// kGvShort: ncb <= kShort (one more than the streaming depth), one round with
+// all of them in flight at once (Llama-3-8B gate, N = 14336, K = 4096: 9.0 ->
+// 8.3 us at M = 1; down, K = 14336 in 4 chunks: 12.0 -> 11.0 us).  kGvSingle: every workgroup owns
 // exactly one block (D = U = 1).  The modes keep the slots past a share few:
 // their out-of-range loads move no data but still cost address-unit issue
 // slots.  kGvRounds: several rounds of U blocks.
@@ -737,7 +749,7 @@ template <int XDT, int S, int SPG, int LAYOUT, int MODE, bool SWIGLU = false>
 __global__ void __launch_bounds__(64 * kGvWaves)
 w4a16_gemv_kernel(W4Args a, GvPlan p) {
   constexpr bool ONE = MODE != kGvRounds;
-  constexpr int D = MODE == kGvSingle ? 1 : GvShape<S, SPG>::kDepth;
+  constexpr int D = MODE == kGvSingle ? 1 : MODE == kGvShort ? GvShape<S, SPG>::kShort : GvShape<S, SPG>::kDepth;
   constexpr int U = MODE == kGvSingle ? 1
                     : MODE == kGvShort ? D
                     : (MODE == kGvOne ? GvShape<S, SPG>::kOneRound : GvShape<S, SPG>::kRound);
@@ -780,8 +792,17 @@ w4a16_gemv_kernel(W4Args a, GvPlan p) {
   c.zlane = LAYOUT == kLayoutTilesZu ? j * 4 : LAYOUT == kLayoutTiles ? j * 8 : (j >> 3) * 4;
   c.tbase = (int32_t)(w4_tile_words(a.N, a.K) * 4);
   c.pairs = w4_group_pairs(a.K, a.G);
-  c.st0 = wave * S;
-  c.g0 = __builtin_amdgcn_readfirstlane(group_of(a, c.st0 * 32));
+  // K split blockIdx.y covers steps [cs0, cs1) (one split: all of K); its
+  // windows start at multiples of S, and windows past cs1 belong to inactive
+  // waves, whose loads go through the zero-size resource and whose x is
+  // zeroed (gv_plan: K % (32 * S) == 0, steps per split a multiple of S)
+  const int split = blockIdx.y;
+  const int cs0 = split * a.steps_per_split;
+  const int cs1 = min(cs0 + a.steps_per_split, a.K / 32);
+  c.st0 = cs0 + wave * S;
+  c.wlive = c.st0 < cs1;
+  const int xst0 = c.wlive ? c.st0 : 0;
+  c.g0 = __builtin_amdgcn_readfirstlane(group_of(a, xst0 * 32));
   const uint32_t zsh = 4u * (uint32_t)(j & 7);
 
   // x chunks of this wave's steps, loaded once and kept for every block.
@@ -802,7 +823,7 @@ w4a16_gemv_kernel(W4Args a, GvPlan p) {
     for (int i = 0; i < S; ++i) {
       const int q = i * 8 + rsub;                 // row chunk: row q % 16, 128 B chunk q / 16
       const int row = q & 15, cc = q >> 4;
-      X[i] = *(const u32x4*)(a.x + (int64_t)min(row, a.M - 1) * a.ldx + c.st0 * 32 + cc * 64 + csub * 8);
+      X[i] = *(const u32x4*)(a.x + (int64_t)min(row, a.M - 1) * a.ldx + xst0 * 32 + cc * 64 + csub * 8);
     }
   }
 
@@ -831,7 +852,10 @@ w4a16_gemv_kernel(W4Args a, GvPlan p) {
 
   u32x4 A[S];
 #pragma unroll
-  for (int s = 0; s < S; ++s) A[s] = gptq_order(x_to_f16<XDT>(X[s]));
+  for (int s = 0; s < S; ++s) {
+    A[s] = gptq_order(x_to_f16<XDT>(X[s]));
+    if (!c.wlive) A[s] = u32x4{0u, 0u, 0u, 0u};  // (a non-finite x would turn 0 * x into NaN)
+  }
 
   for (int q0 = 0; q0 < (ONE ? 1 : ncb); q0 += U) {
     // U blocks per round (U a multiple of D, so block q0+q sits in buf[q % D])
@@ -883,8 +907,14 @@ w4a16_gemv_kernel(W4Args a, GvPlan p) {
       const int m = 4 * kb + r;
       const int n = (u0 + q0 + q) * 16 + j;
       if (m < a.M && n < a.N) {
-        if (a.bias_dtype != KQ_DTYPE_NONE) v = __fadd_rn(v, load_as_f32(a.bias, a.bias_dtype, n));
-        a.out[(int64_t)m * a.N + n] = f32_to_out(v, a.out_dtype);
+        if (a.splits > 1) {
+          // this split's fp32 partial; the reduce pass adds the splits in
+          // order and applies bias and the cast
+          a.partials[((int64_t)split * a.M + m) * a.N + n] = v;
+        } else {
+          if (a.bias_dtype != KQ_DTYPE_NONE) v = __fadd_rn(v, load_as_f32(a.bias, a.bias_dtype, n));
+          a.out[(int64_t)m * a.N + n] = f32_to_out(v, a.out_dtype);
+        }
       }
     }
     __syncthreads();
@@ -1384,15 +1414,26 @@ static int device_cus() {
   return cached[slot];
 }
 
-// The decode GEMV covers M <= 16 with K in {1024, 2048, 4096} (16 waves x S
-// steps of 32), 16-byte aligned x rows, and group boundaries at fixed steps
-// of every wave window, when there are enough 16-column blocks to give every
-// CU work.  *S and *SPG receive the kernel's template values.
+// The decode GEMV covers M <= 16 with K % 128 == 0: 16 waves, each a window
+// of S steps of 32 (S = 2, 4 or 8: half, one or two stages; 8 from 17 stages
+// up when K % 256 == 0, else 4), 16-byte aligned x rows, and group boundaries
+// at fixed steps of every window.  K beyond one pass of the 16 windows (4096
+// at S = 8, 2048 at S = 4) is split across workgroups in chunks of whole
+// windows (fp32 partials, then the W4 split-K reduce); waves whose window lies
+// past K or past their chunk stay inactive (K = 3584: 14 of 16).  Every unit
+// count works: with fewer 16-column units than CUs each workgroup owns one
+// unit, and with K splits the workgroups per split fill the CUs together.
+// *S and *SPG receive the kernel's template values.
 static bool gv_plan(const W4Args& a, int fmt, int gmode, GvPlan* p, int* S, int* SPG) {
   if (fmt != kGptq || a.M > 16 || gmode == kGroupsPerK) return false;
-  if (a.K % 512 != 0) return false;
-  const int s = a.K / 512;
-  if (s != 2 && s != 4 && s != 8) return false;
+  if (a.K % 128 != 0 || (a.K > 4096 && a.swiglu)) return false;
+  const int stages = a.K / 128;
+  const int s = stages > 16 ? (a.K % 256 == 0 ? 8 : 4) : (stages > 8 ? 4 : 2);
+  if (a.K % (32 * s) != 0) return false;
+  const int nsteps = a.K / 32;
+  p->splits = (nsteps + 16 * s - 1) / (16 * s);
+  p->sps = ((nsteps + p->splits - 1) / p->splits + s - 1) / s * s;
+  p->splits = (nsteps + p->sps - 1) / p->sps;
   if (a.G % 32 != 0) return false;
   const int spg = a.G / 32;
   int tspg;
@@ -1407,7 +1448,6 @@ static bool gv_plan(const W4Args& a, int fmt, int gmode, GvPlan* p, int* S, int*
   if ((uint64_t)w4_tiled_words(a.N, a.K, a.G, a.zu != 0) * 4u >= ((uint64_t)1 << 31)) return false;
   const int cus = device_cus();
   p->units = (a.N + 15) / 16;
-  if (p->units * 2 < cus) return false;
   if (a.swiglu) {
     // whole gate/up unit pairs per workgroup, one round (at most 8 units)
     if (a.layout != kLayoutTiles || (a.N % 32) != 0) return false;
@@ -1418,10 +1458,27 @@ static bool gv_plan(const W4Args& a, int fmt, int gmode, GvPlan* p, int* S, int*
     *SPG = tspg;
     return true;
   }
-  p->wgs = std::min(cus, p->units);
+  // with K splits, workgroups per split so that all splits together fill the CUs
+  p->wgs = std::min(p->units, std::max(1, cus / p->splits));
+  if (p->splits > 1 && (p->units + p->wgs - 1) / p->wgs > GvShape<8, 4>::kOneRound) {
+    p->wgs = (p->units + GvShape<8, 4>::kOneRound - 1) / GvShape<8, 4>::kOneRound;
+  }
   *S = s;
   *SPG = tspg;
   return true;
+}
+
+// fp32 partial bytes of a split-K decode GEMV call (0 without splits); an
+// upper bound the workspace sizing uses without the device's CU count.
+static size_t gv_split_bytes(int64_t m, int64_t n, int64_t k) {
+  if (m > 16 || k % 128 != 0 || k <= 2048) return 0;
+  const int64_t s = k % 256 == 0 ? 8 : 4;
+  const int64_t nsteps = k / 32;
+  int64_t splits = (nsteps + 16 * s - 1) / (16 * s);
+  if (splits <= 1) return 0;
+  const int64_t sps = ((nsteps + splits - 1) / splits + s - 1) / s * s;
+  splits = (nsteps + sps - 1) / sps;
+  return ((size_t)splits * (size_t)m * (size_t)n * 4 + 255) / 256 * 256;
 }
 
 // Prefill GEMM conditions: tiled weights, M above the GEMV's range, whole
@@ -1456,10 +1513,10 @@ template <int XDT, int S, int SPG>
 static void launch_gv_s(const W4Args& a, const GvPlan& p, int layout, hipStream_t st) {
   const int per = (p.units + p.wgs - 1) / p.wgs;
   const int mode = per <= 1                         ? kGvSingle
-                   : per <= GvShape<S, SPG>::kDepth    ? kGvShort
+                   : per <= GvShape<S, SPG>::kShort    ? kGvShort
                    : per <= GvShape<S, SPG>::kOneRound ? kGvOne
                                                        : kGvRounds;
-  const dim3 g(p.wgs), b(64 * kGvWaves);
+  const dim3 g(p.wgs, p.splits), b(64 * kGvWaves);
 #define KQ_GV_LAUNCH(L, M) hipLaunchKernelGGL((w4a16_gemv_kernel<XDT, S, SPG, L, M>), g, b, 0, st, a, p)
   if (a.swiglu) {
     // (gv_plan: tiled operand, at most kOneRound units per workgroup)
@@ -1540,16 +1597,21 @@ static int run_w4(const char* what, int fmt, W4Args a, int gmode, void* workspac
   int gv_s = 0, gv_spg = 0;
   if (gv_plan(a, fmt, gmode, &gp, &gv_s, &gv_spg)) {
     int xdt = a.x_dtype == KQ_DTYPE_F16 ? kXF16 : kXBF16;
+    // act-order x gather first, then the split partials
+    const size_t x16_bytes = needs_x16 ? ((size_t)a.M * a.K * 2 + 255) / 256 * 256 : 0;
+    const size_t part_bytes = gp.splits > 1 ? (size_t)gp.splits * a.M * a.N * 4 : 0;
+    if (x16_bytes + part_bytes > 0 && (workspace == nullptr || ws_bytes < x16_bytes + part_bytes)) {
+      set_error("%s: workspace of %zu bytes is smaller than the %zu bytes this call needs", what,
+                workspace ? ws_bytes : (size_t)0, x16_bytes + part_bytes);
+      return KQ_EWORKSPACE;
+    }
+    a.splits = gp.splits;
+    a.steps_per_split = gp.sps;
+    a.partials = gp.splits > 1 ? (float*)((uint8_t*)workspace + x16_bytes) : nullptr;
     if (needs_x16) {
       // act-order: gather x through the permutation once per call
-      const size_t x16_bytes = (size_t)a.M * a.K * 2;
-      if (workspace == nullptr || ws_bytes < x16_bytes) {
-        set_error("%s: workspace of %zu bytes is smaller than the %zu bytes this call needs", what,
-                  workspace ? ws_bytes : (size_t)0, x16_bytes);
-        return KQ_EWORKSPACE;
-      }
       uint16_t* x16 = (uint16_t*)workspace;
-      // (gv_plan: M <= 16, K <= 4096, K % 512 == 0, 16-byte aligned x rows)
+      // (gv_plan: M <= 16, K % 128 == 0, 16-byte aligned x rows)
       hipLaunchKernelGGL(w4a16_prep_x_row_kernel, dim3((unsigned)((a.K + 1023) / 1024), (unsigned)a.M),
                          dim3(128), (size_t)a.K * 2, stream, a.x, a.x_dtype, a.ldx, a.perm, a.K, x16);
       a.x = x16;
@@ -1557,6 +1619,11 @@ static int run_w4(const char* what, int fmt, W4Args a, int gmode, void* workspac
       xdt = kXF16;
     }
     launch_gv(a, gp, xdt, gv_s, gv_spg, a.layout, stream);
+    if (gp.splits > 1) {
+      ReduceArgs r{a.partials, gp.splits, a.M, a.N, nullptr, nullptr, 0, a.bias, a.bias_dtype,
+                   a.out, a.out_dtype, nullptr};
+      launch_splitk_reduce(kReduceW4, r, stream);
+    }
     return check_launch(what);
   }
   if (prefill_applies(a, gmode)) {
@@ -1625,9 +1692,12 @@ extern "C" size_t kq_w4a16_workspace_size(int64_t m, int64_t n, int64_t k, int g
   // a generous workspace lets the planner choose split-K freely
   const W4Plan p = plan_w4((int)m, (int)n, (int)k, gidx_mode == kGroupsPermuted,
                            (size_t)1 << 40, true);
-  // the prefill GEMM (M > 16, tiled weights) stages fp16 x in the workspace
+  // the prefill GEMM (M > 16, tiled weights) stages fp16 x in the workspace;
+  // the decode GEMV keeps the act-order gather and its split partials there
   const size_t x16 = m > 16 ? ((size_t)m * (size_t)k * 2 + 255) / 256 * 256 : 0;
-  return std::max(p.x16_bytes + p.partial_bytes, x16);
+  const size_t gv = (gidx_mode == kGroupsPermuted ? ((size_t)m * (size_t)k * 2 + 255) / 256 * 256 : 0) +
+                    gv_split_bytes(m, n, k);
+  return std::max({p.x16_bytes + p.partial_bytes, x16, gv});
 }
 
 // Offset of the SwiGLU two-pass intermediate: after the GEMM's own scratch.

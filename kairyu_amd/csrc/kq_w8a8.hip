@@ -335,18 +335,43 @@ static void launch_decode_nw(const uint8_t* xq, const uint8_t* w, int K, const E
     hipLaunchKernelGGL((w8a8_decode_kernel<FMT, R, NW, 2>), grid, block, 0, stream, xq, w, K, ep);
 }
 
-// Waves per workgroup from the stage count (each wave keeps >= ~4 stages in
-// its range); rings of 4 stages.  The 2-wave form's short ranges take 3
+// Waves and ring depth of the decode kernels.  With at least one workgroup
+// per CU (N >= 16 * CUs) by the stage count, each wave keeping >= ~4 stages
+// in its range, rings of 4 stages; the 2-wave form's short ranges take 3
 // stages with 16-row activation stages (M > 8) and 2 otherwise: measured on
 // C4's shape (N = 18944, K = 3584) M = 16 15.5 -> 15.2 us with 3, M = 4 and 8
-// 3% slower with 3, and slower still with 4 or 6 stages or 4 waves.
+// 3% slower with 3, and slower still with 4 or 6 stages or 4 waves; N = K =
+// 4096 (one tile per CU) runs 4 waves 10% faster than 8.  With fewer tiles
+// than CUs, 8 waves with 4-stage rings (Qwen2-7B q_proj, N = K = 3584: every
+// stage of a tile in flight at once; 4.9 -> 4.6 us at M = 1 against the
+// skinny kernel), and with at most half a tile per CU and K <= 4096, 16 waves
+// of two stages with 2-stage rings (Llama-3-8B k_proj, N = 1024: every stage
+// of the 64 tiles in flight at once; 6.0 -> 3.7 us at M = 1).
+struct DecForm {
+  int nw, r;
+};
+
+static DecForm decode_form(int64_t n, int K, int M) {
+  const int64_t tiles = (n + kSkinnyCols - 1) / kSkinnyCols;
+  const int cus = tg_device_cus();
+  const int nst = K / 128;
+  if (tiles >= (int64_t)cus) {
+    if (nst >= 64) return {8, 4};
+    if (nst >= 32) return {4, 4};
+    return {2, M > 8 ? 3 : 2};
+  }
+  if (2 * tiles <= cus && nst <= 32) return {16, 2};
+  return {8, 4};
+}
+
 template <int FMT>
 static void launch_decode(const uint8_t* xq, const uint8_t* w, int K, const Epi& ep,
                           hipStream_t stream) {
-  const int nst = K / 128;
-  if (nst >= 64) launch_decode_nw<FMT, 4, 8>(xq, w, K, ep, stream);
-  else if (nst >= 32) launch_decode_nw<FMT, 4, 4>(xq, w, K, ep, stream);
-  else if (ep.M > 8) launch_decode_nw<FMT, 3, 2>(xq, w, K, ep, stream);
+  const DecForm f = decode_form(ep.N, K, ep.M);
+  if (f.nw == 16) launch_decode_nw<FMT, 2, 16>(xq, w, K, ep, stream);
+  else if (f.nw == 8) launch_decode_nw<FMT, 4, 8>(xq, w, K, ep, stream);
+  else if (f.nw == 4) launch_decode_nw<FMT, 4, 4>(xq, w, K, ep, stream);
+  else if (f.r == 3) launch_decode_nw<FMT, 3, 2>(xq, w, K, ep, stream);
   else launch_decode_nw<FMT, 2, 2>(xq, w, K, ep, stream);
 }
 
@@ -569,12 +594,15 @@ template <int FMT, int MR>
 static void launch_decode_quant_mr(const uint16_t* x, int x_dtype, int ldx, int scale_mode,
                                    const float* scale_in, const uint8_t* w, int K, const Epi& ep,
                                    hipStream_t stream) {
-  const int nst = K / 128;
+  const DecForm f = decode_form(ep.N, K, ep.M);
   const dim3 grid((ep.N + kSkinnyCols - 1) / kSkinnyCols);
-  if (nst >= 64)
+  if (f.nw == 16)
+    hipLaunchKernelGGL((w8a8_decode_quant_kernel<FMT, 2, 16, MR>), grid, dim3(1024), 0, stream, x,
+                       x_dtype, ldx, scale_mode, scale_in, w, K, ep);
+  else if (f.nw == 8)
     hipLaunchKernelGGL((w8a8_decode_quant_kernel<FMT, 4, 8, MR>), grid, dim3(512), 0, stream, x,
                        x_dtype, ldx, scale_mode, scale_in, w, K, ep);
-  else if (nst >= 32)
+  else if (f.nw == 4)
     hipLaunchKernelGGL((w8a8_decode_quant_kernel<FMT, 4, 4, MR>), grid, dim3(256), 0, stream, x,
                        x_dtype, ldx, scale_mode, scale_in, w, K, ep);
   else
@@ -794,7 +822,7 @@ static int run_w8a8(const char* what, const uint8_t* xq, const uint8_t* w, int64
     set_error("%s: weight or activation exceeds the 4 GiB addressing of the skinny kernel", what);
     return KQ_EINVAL;
   }
-  if (m <= 16 && K % 128 == 0 && (n + kSkinnyCols - 1) / kSkinnyCols >= tg_device_cus())
+  if (m <= 16 && K % 128 == 0)
     launch_decode<FMT>(xq, w, K, ep, stream);
   else if (m <= 16) launch_skinny<FMT, 1>(xq, w, K, ep, workspace, ws_bytes, stream);
   else if (m <= 32) launch_skinny<FMT, 2>(xq, w, K, ep, workspace, ws_bytes, stream);
@@ -865,7 +893,7 @@ static int run_linear(const char* what, const void* x, int x_dtype, int64_t ldx,
     return KQ_EINVAL;
   }
   const int K = (int)k;
-  if (m <= kFusedMaxRows && K % 128 == 0 && (n + kSkinnyCols - 1) / kSkinnyCols >= tg_device_cus() &&
+  if (m <= kFusedMaxRows && K % 128 == 0 &&
       ((uintptr_t)x % 16) == 0 && (ldx % 8) == 0 && ((uintptr_t)w % 16) == 0 &&
       ((m - 1) * ldx + k) * 2 < ((int64_t)1 << 31) && n * k < ((int64_t)1 << 32)) {
     ep.xscale = nullptr;
