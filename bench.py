@@ -15,7 +15,8 @@ GEMV's algorithmic bytes per launch over its per-launch time, timed live with
 HIP events on its own captured launches (x gathered once up front).
 
 ``sweep`` reports every BASELINE configuration (C1-C4 over their M values,
-C5), each row with
+C5) and decode (M = 1, 16) at the other projection shapes of Llama-3-8B and
+Qwen2-7B for AWQ, GPTQ act-order and FP8, each row with
   * ``op``: the whole module call (activation quantization / act-order gather
     included) -- GB/s, TFLOPS and both roofline fractions;
   * ``gemm``: the dominant GEMM entry alone on pre-processed activations
@@ -30,6 +31,9 @@ C5), each row with
     workload on this host's cores, and the device output on the same sample
     judged against the oracle with the test suite's criteria
     (``oracle.parity``).
+``context`` holds the reference microbenchmark's own setup (N = K = 4096, M
+in {1, 128}, bf16, seed 205, four formats) timed its way and this bench's
+way, next to its published numbers on its own GPU (``--no-context`` skips).
 The top-level ``cpu_baseline`` is the headline row's.  ``peaks`` holds the
 box's measured ceilings (streaming read, MFMA loop per dtype; see
 ``measure_peaks``), and every roofline entry gives its fraction of the
@@ -507,7 +511,98 @@ def sweep_entries():
     for m in (16, 4096):
         entries.append((f"C4 INT8 W8A8 N=18944 K=3584 M={m}", "int8", lambda m=m: W.int8_layer(m=m)))
     entries.append(("C5 block-FP8 MoE E=128 H=2048 I=768 T=4096 top8", "fp8", lambda: W.moe_layer()))
+    # decode at the other projection shapes of the models north_star names
+    # (kairyu/models/layers.py:212-241, attention.py:51-94)
+    for label, n, k in DECODE_SHAPES:
+        for m in (1, 16):
+            entries.append((f"{label} AWQ W4A16 N={n} K={k} M={m}", "fp16",
+                            lambda m=m, n=n, k=k: W.awq_layer(m=m, n=n, k=k)))
+            entries.append((f"{label} GPTQ act-order W4A16 N={n} K={k} M={m}", "fp16",
+                            lambda m=m, n=n, k=k: W.gptq_layer(m=m, n=n, k=k)))
+            entries.append((f"{label} FP8 W8A8 N={n} K={k} M={m}", "fp8",
+                            lambda m=m, n=n, k=k: W.fp8_layer(m=m, n=n, k=k)))
     return entries
+
+
+DECODE_SHAPES = [("Llama-3-8B down_proj", 4096, 14336), ("Llama-3-8B k_proj", 1024, 4096),
+                 ("Qwen2-7B q_proj", 3584, 3584), ("Qwen2-7B down_proj", 3584, 18944)]
+
+# The reference's published microbenchmark (RTX PRO 6000 Blackwell, N = K =
+# 4096, bf16 x, seed 205; bench/results/quant-gemm-rtxpro6000-2026-07-27.json
+# as quoted in BASELINE.md): median ms of module(x) per scheme and M.
+REFERENCE_MICROBENCH_MS = {("fp8", 1): 0.11891, ("fp8", 128): 0.11754, ("int8", 1): 0.10899,
+                           ("int8", 128): 0.11770, ("awq", 1): 0.08890, ("awq", 128): 0.29862,
+                           ("gptq", 1): 0.10749, ("gptq", 128): 0.26109}
+
+
+def _eager_median_ms(fn, warmup: int = 50, repeats: int = 200) -> float:
+    """The reference microbenchmark's timing (quant_gemm_bench.py:70-97):
+    events around each eager call, one synchronize after all samples, median."""
+
+    import statistics
+
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(repeats)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(repeats)]
+    for start, end in zip(starts, ends):
+        start.record()
+        fn()
+        end.record()
+    torch.cuda.synchronize()
+    return statistics.median(a.elapsed_time(b) for a, b in zip(starts, ends))
+
+
+def reference_microbench_rows() -> list[dict]:
+    """Context rows at the reference microbenchmark's own setup (N = K = 4096,
+    M in {1, 128}, bf16 x, seed 205, FP8 / INT8 / AWQ / GPTQ): the module call
+    timed the reference's way (eager events, median of 200 after 50 warm-ups,
+    the weights not rotated, so they may sit in the MALL as on the reference's
+    run) and this bench's way (graph samples, weights rotated past the MALL),
+    next to the reference's published time on its own hardware (context, not
+    a parity target), and the output against the oracle."""
+
+    import torch
+
+    from kairyu_amd import workloads as W
+    from oracle import linear as olinear
+
+    rows = []
+    for scheme in ("fp8", "int8", "awq", "gptq"):
+        for m in (1, 128):
+            wl = W.reference_microbench_layer(scheme, m)
+            eager = _eager_median_ms(lambda wl=wl: wl.module(wl.x))
+            graph = measure(wl, 20, 5)
+            out = wl.module(wl.x)
+            torch.cuda.synchronize()
+            mod = wl.module
+            x32 = _np(wl.x)
+            if scheme in ("awq", "gptq"):
+                args = (x32, mod.qweight.cpu().numpy(), mod.qzeros.cpu().numpy(), _np(mod.scales))
+                expected = (olinear.awq_forward(*args, mod.group_size, "bfloat16") if scheme == "awq"
+                            else olinear.gptq_forward(*args, mod.g_idx.cpu().numpy(), "bfloat16"))
+            elif scheme == "fp8":
+                expected, *_ = olinear.fp8_forward(x32, _bits_np(mod.weight), _np(mod.weight_scale))
+            else:
+                expected, *_ = olinear.int8_forward(x32, mod.weight.cpu().numpy(), _np(mod.weight_scale), None)
+            err = olinear.error_metrics(_np(out), expected)
+            ref_ms = REFERENCE_MICROBENCH_MS[(scheme, m)]
+            rows.append({
+                "scheme": scheme, "shape": {"m": m, "n": 4096, "k": 4096}, "x_dtype": "bfloat16", "seed": 205,
+                "eager_median_us": round(eager * 1e3, 2), "graph_us": round(graph["ms"] * 1e3, 2),
+                "reference_rtx_pro_6000_us": round(ref_ms * 1e3, 2),
+                "reference_us_over_eager_us": round(ref_ms / eager, 2),
+                "vs_oracle": {"rel_rmse": err["rel_rmse"], "normwise_max": err["normwise_max"]},
+            })
+            print(f"[bench] context {scheme} M={m}: eager {eager * 1e3:.2f} us, graph "
+                  f"{graph['ms'] * 1e3:.2f} us (reference on RTX PRO 6000: {ref_ms * 1e3:.2f} us); "
+                  f"rel_rmse {err['rel_rmse']:.2e}", file=sys.stderr, flush=True)
+            del wl
+            torch.cuda.empty_cache()
+    return rows
 
 
 # ---------------------------------------------------------- measured peaks
@@ -619,6 +714,8 @@ def main() -> int:
                         help="only measure the box's streaming-read and MFMA-loop ceilings")
     parser.add_argument("--no-peaks", action="store_true",
                         help="skip the measured ceilings in a full run")
+    parser.add_argument("--no-context", action="store_true",
+                        help="skip the reference microbenchmark's context rows")
     args = parser.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one MI355X; --gpus {args.gpus} is not supported "
@@ -699,15 +796,20 @@ def main() -> int:
             if not args.no_cpu:
                 out = wl.module(wl.x)
                 torch.cuda.synchronize()
-                row["cpu_baseline"], row["parity"] = cpu_row(name, wl, out)
+                shape_row = any(name.startswith(label) for label, _, _ in DECODE_SHAPES)
+                row["cpu_baseline"], row["parity"] = cpu_row(name, wl, out, target_s=0.5 if shape_row else 2.0)
                 print(f"[bench]   cpu {row['cpu_baseline']['value']} {row['cpu_baseline']['unit']}; "
                       f"parity {row['parity']['verdict']}", file=sys.stderr, flush=True)
             sweep.append(row)
             del wl
             torch.cuda.empty_cache()
 
+    context = None
+    if not args.no_context and not args.only:
+        context = reference_microbench_rows()
+
     if head is None:
-        print(json.dumps({"peaks": peaks, "sweep": sweep}), flush=True)
+        print(json.dumps({"peaks": peaks, "sweep": sweep, "context": context}), flush=True)
         return 0
 
     traffic = None
@@ -752,6 +854,7 @@ def main() -> int:
         "peaks": peaks,
         "cpu_baseline": cpu,
         "sweep": sweep,
+        "context": context,
     }
     print(json.dumps(line), flush=True)
     return 0

@@ -124,6 +124,49 @@ def int8_layer(m: int = 16, n: int = 18944, k: int = 3584, seed: int = 0, device
                     "hbm" if m <= 64 else "mfma")
 
 
+def reference_microbench_layer(scheme: str, m: int, n: int = 4096, k: int = 4096, seed: int = 205,
+                               device="cuda") -> Workload:
+    """The reference's own microbenchmark setup
+    (verification/l1/performance/quant_gemm_bench.py:184-196): torch seed 205,
+    weight ``randn(n, k)`` quantized by the format's quantizer (FP8 per
+    channel, INT8 per channel, AWQ / GPTQ groups of 128 along K), x
+    ``randn(m, k)`` in bf16 on the device (drawn after the weight, from the
+    global generator as the reference does)."""
+
+    from kairyu_amd.quant.awq import quantize_awq
+    from kairyu_amd.quant.gptq import quantize_gptq
+
+    torch.manual_seed(seed)
+    weight = torch.randn(n, k)
+    if scheme == "fp8":
+        module = Fp8Linear(k, n, bias=False)
+        qw, ws = quantize_fp8(weight)
+        module.weight.copy_(qw)
+        module.weight_scale.copy_(ws)
+    elif scheme == "int8":
+        module = Int8Linear(k, n, bias=False)
+        qw, ws = quantize_int8_weight(weight)
+        module.weight.copy_(qw)
+        module.weight_scale.copy_(ws)
+    elif scheme == "awq":
+        module = AwqLinear(k, n, bias=False, group_size=128)
+        for name, t in zip(("qweight", "qzeros", "scales"), quantize_awq(weight, group_size=128)):
+            getattr(module, name).copy_(t)
+    elif scheme == "gptq":
+        module = GptqLinear(k, n, bias=False, group_size=128)
+        for name, t in zip(("qweight", "qzeros", "scales", "g_idx"), quantize_gptq(weight, group_size=128)):
+            getattr(module, name).copy_(t)
+    else:
+        raise ValueError(f"unknown scheme {scheme!r}")
+    module = module.to(device)
+    x = torch.randn(m, k, device=device, dtype=torch.bfloat16)
+    w4 = scheme in ("awq", "gptq")
+    groups = k // 128
+    nbytes = (k * n // 2 + groups * (n // 8) * 4 + groups * n * 2 if w4 else n * k + 4 * n) + m * k * 2 + m * n * 2
+    return Workload(f"reference_microbench_{scheme}_m{m}_n{n}_k{k}", module, x, nbytes, 2 * m * n * k,
+                    "hbm" if m <= 64 else "mfma")
+
+
 def replicas(workload: Workload, copies: int) -> list[torch.nn.Module]:
     """Independent copies of a workload's module (distinct HBM allocations), used
     to rotate weights so repeated calls cannot be served from the 256 MB MALL."""
