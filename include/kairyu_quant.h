@@ -116,6 +116,29 @@ int kq_w8a8_fp8_linear(const void* x, int x_dtype, int64_t ldx, const float* sca
  * row scales, and every split-K form).  No counterpart in the reference. */
 size_t kq_w8a8_linear_workspace_size(int64_t m, int64_t n, int64_t k);
 
+/* Packed (gate, up) W8A8 projection with SwiGLU: w holds the gate rows then
+ * the up rows, [2 * i_width][k] (wscale and bias over the same 2 * i_width
+ * rows), and out [m][i_width] (activation dtype) = silu(g) * u for gate
+ * column c and up column i_width + c, with the roundings of
+ * kq_w8a8_*_linear followed by kq_swiglu (bit-identical to that pair).
+ * Prefill shapes apply SwiGLU in the tile engine's epilogue (the [m][2I]
+ * projection never reaches memory); other shapes run the pair through the
+ * workspace.  Replaces the reference MLP's act_fn(gate(x)) * up(x)
+ * (kairyu/models/layers.py:243-244) over its packed projections
+ * (kairyu/models/packed_linear.py:58-149) for FP8 / INT8 W8A8. */
+int kq_w8a8_i8_swiglu_linear(const void* x, int x_dtype, int64_t ldx, const int8_t* w,
+                             const float* wscale, const void* bias, int bias_dtype, void* out,
+                             int64_t m, int64_t i_width, int64_t k, void* workspace,
+                             size_t workspace_bytes, void* stream);
+int kq_w8a8_fp8_swiglu_linear(const void* x, int x_dtype, int64_t ldx, const float* scale_in,
+                              int scale_mode, const uint8_t* w, const float* wscale,
+                              int wscale_per_channel, const void* bias, int bias_dtype, void* out,
+                              int64_t m, int64_t i_width, int64_t k, void* workspace,
+                              size_t workspace_bytes, void* stream);
+/* Workspace bytes for kq_w8a8_*_swiglu_linear of this shape.  No counterpart
+ * in the reference. */
+size_t kq_w8a8_swiglu_workspace_size(int64_t m, int64_t i_width, int64_t k);
+
 /* Bytes of workspace with which every split-K form of the two W8A8 entry
  * points is available for this shape (0: none applies).  No counterpart in
  * the reference (its GPU path calls torch._scaled_mm / Triton, which allocate

@@ -53,6 +53,11 @@ _SIGNATURES: dict[str, list] = {
         _P, _I, _I64, _P, _I, _P, _P, _I, _P, _I, _P, _I, _I64, _I64, _I64, _P, _SZ, _P,
     ],
     "kq_w8a8_linear_workspace_size": [_I64, _I64, _I64],
+    "kq_w8a8_i8_swiglu_linear": [_P, _I, _I64, _P, _P, _P, _I, _P, _I64, _I64, _I64, _P, _SZ, _P],
+    "kq_w8a8_fp8_swiglu_linear": [
+        _P, _I, _I64, _P, _I, _P, _P, _I, _P, _I, _P, _I64, _I64, _I64, _P, _SZ, _P,
+    ],
+    "kq_w8a8_swiglu_workspace_size": [_I64, _I64, _I64],
     "kq_w4a16_awq_gemm": [_P, _I, _P, _P, _P, _P, _I, _P, _I64, _I64, _I64, _I, _P, _SZ, _P],
     "kq_w4a16_gptq_gemm": [
         _P, _I, _P, _P, _P, _P, _P, _I, _P, _I, _P, _I64, _I64, _I64, _I, _P, _SZ, _P,
@@ -112,6 +117,7 @@ def _load() -> ctypes.CDLL:
                           "kq_w4a16_tiled_words": ctypes.c_int64,
                           "kq_w8a8_workspace_size": ctypes.c_size_t,
                           "kq_w8a8_linear_workspace_size": ctypes.c_size_t,
+                          "kq_w8a8_swiglu_workspace_size": ctypes.c_size_t,
                           "kq_moe_workspace_size": ctypes.c_size_t}.get(name, ctypes.c_int)
         _lib = lib
         return lib

@@ -62,6 +62,21 @@ KQ_DEV uint16_t f32_to_out(float v, int dtype) {
   return dtype == KQ_DTYPE_BF16 ? f32_to_bf16(v) : f32_to_f16(v);
 }
 
+// fp32 -> the activation dtype and back (round to nearest even)
+KQ_DEV float round_act(float v, int dtype) {
+  if (dtype == KQ_DTYPE_BF16) return (float)(__bf16)v;
+  return (float)(_Float16)v;
+}
+
+// silu(gate) * up with torch's roundings on fp16 / bf16 tensors
+// (kairyu/models/layers.py:243-244): gate and up rounded to the activation
+// dtype, silu in fp32 (IEEE division) rounded, the product rounded.
+KQ_DEV uint16_t swiglu_bits(float gate, float up, int dtype) {
+  const float g = round_act(gate, dtype), u = round_act(up, dtype);
+  const float s = round_act(__fdiv_rn(g, __fadd_rn(1.0f, expf(-g))), dtype);
+  return f32_to_out(__fmul_rn(s, u), dtype);
+}
+
 // W4A16 activation operand: fp16 passes through, bf16 is widened and finite
 // values beyond fp16's range saturate to +-65504 while inf/nan stay non-finite
 // (reference contract, kairyu/kernels/quant_gemm_gpu.py:296-307).

@@ -64,7 +64,11 @@ constexpr int kTgGroupM = 8;  // dense tile order: row tiles per group
 constexpr int kTgLag = 2;     // block scaling: MFMAs between a result and its scale FMA
 
 enum { kTgFp8 = 0, kTgI8 = 1 };
-enum { kTgEpiStore = 0, kTgEpiSwiGluQuant = 1 };
+// Epilogues: store the outputs; SwiGLU of each gate / up column pair
+// quantized to e4m3 1x128 blocks (MoE gate_up); SwiGLU of each pair stored
+// in the activation dtype (a dense packed gate / up projection).  Both SwiGLU
+// forms pair weight rows [n0, n0 + 128) with [I + n0, I + n0 + 128).
+enum { kTgEpiStore = 0, kTgEpiSwiGluQuant = 1, kTgEpiSwiGluStore = 2 };
 
 // LDS map (bytes) of a tile of 64 * NRB activation rows
 template <int NRB>
@@ -103,7 +107,7 @@ struct TileGemmArgs {
   int out_dtype;
   const void* bias;          // [N] or null
   int bias_dtype;
-  int32_t* acc_out;          // INT8: raw int32 accumulators [M][N] or null
+  int32_t* acc_out;          // INT8: raw int32 accumulators [M][N] or null (store epilogue)
   int ksplit;                // dense, per-channel scales only: K split across this many
                              // work units per tile (0/1: none); each stores raw 32-bit
   uint32_t* partials;        // accumulators to partials[split][M][N], reduced afterwards
@@ -276,11 +280,15 @@ tile_gemm_kernel(TileGemmArgs a) {
       const int off = tt < 2 * KB ? ((tl.e * NB + scale_block(tl, half)) * KB + kb) * 4 : kTgOob;
       tg_dma4(rws, lds0 + L::Ws + wsbuf * (2 * kTgMaxKB * 4) + wave * 256, off, 0);
     }
-    if (EPI == kTgEpiStore && threadIdx.x < 256) {
+    if (EPI != kTgEpiSwiGluQuant && threadIdx.x < 256) {
       // epilogue constants of tile row / column t: loaded here, one tile
       // ahead, so the epilogue issues no global loads between its stores
-      // (loads and stores share vmcnt: a load would wait for every store)
-      const int t = (int)threadIdx.x, r = tl.row0 + t, n = min(tl.ntile * kTgBN + t, a.N - 1);
+      // (loads and stores share vmcnt: a load would wait for every store).
+      // SwiGLU store: column t < 128 is gate column ntile * 128 + t, the
+      // others the up columns I + ntile * 128 + t - 128.
+      const int t = (int)threadIdx.x, r = tl.row0 + t;
+      const int n = EPI == kTgEpiSwiGluStore ? min((t >> 7) * a.I + tl.ntile * 128 + (t & 127), a.N - 1)
+                                             : min(tl.ntile * kTgBN + t, a.N - 1);
       if (!BLOCK) {
         pf_exs = r < tl.row_end ? a.xs[r] : 0.0f;
         pf_ews = a.ws_per_channel ? a.ws[n] : a.ws[0];
@@ -316,7 +324,7 @@ tile_gemm_kernel(TileGemmArgs a) {
       const int p = (wave * 4 + i) * 64 + ln, row = p >> 3;
       const int c = tg_chunk<FMT>(row, p & 7);
       int n;
-      if constexpr (EPI == kTgEpiSwiGluQuant) {
+      if constexpr (EPI != kTgEpiStore) {
         // wave half wn: blocks j < 4 gate rows, j >= 4 up rows of activation
         // columns ntile*128 + 64*wn + 16*(j&3) + (row&15)
         const int j = (row >> 4) & 7;
@@ -334,7 +342,7 @@ tile_gemm_kernel(TileGemmArgs a) {
     }
   };
   auto stage_ws = [&](int buf) {
-    if (EPI == kTgEpiStore && threadIdx.x < 256) {
+    if (EPI != kTgEpiSwiGluQuant && threadIdx.x < 256) {
       float* e = (float*)(smem + L::Epi) + buf * 3 * 256 + (int)threadIdx.x;
       e[0] = pf_exs;
       e[256] = pf_ews;
@@ -408,7 +416,7 @@ tile_gemm_kernel(TileGemmArgs a) {
     // K loop (the store epilogue variants), the compiler would otherwise wait
     // for all vector-memory operations (the next block's copies included) in
     // every K step; one wait per tile here lets it drop that.
-    if constexpr (EPI == kTgEpiStore) __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    if constexpr (EPI != kTgEpiSwiGluQuant) __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
     // Block scaling (MoE experts, block-FP8 linear): row block 4 * mb + wm of
     // a ragged row tile holds rows while 16 * (4 * mb + wm) < rows, so the
     // first `live` of this wave's row blocks hold rows.  A wave without any
@@ -596,6 +604,36 @@ tile_gemm_kernel(TileGemmArgs a) {
           if (row0 + r < row_end)
             *(i32x4*)(a.actq + (int64_t)(row0 + r) * a.I + ntile * 128 + c * 16) =
                 *(const i32x4*)(stg + r * 128 + ((c ^ (r & 7)) << 4));
+        }
+      } else if constexpr (EPI == kTgEpiSwiGluStore) {
+        // gate and up of activation column 64 * wn + 16 * j + 4 * lg + q
+        // (j < 4: gate rows, j + 4 the up rows) with the store epilogue's
+        // arithmetic, ((acc * xs) * ws) + bias, then SwiGLU with the
+        // elementwise pass's roundings (swiglu_bits): the bits the packed
+        // GEMM followed by kq_swiglu produce, without the [M, 2I] round trip
+        const float* eX = (const float*)(smem + L::Epi) + buf * 3 * 256;
+        const int I = a.I;
+  #pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int cl = 64 * wn + 16 * j + 4 * lg;
+          const int col = ntile * 128 + cl;
+          const f32x4 wsg = *(const f32x4*)(eX + 256 + cl), wsu = *(const f32x4*)(eX + 256 + 128 + cl);
+          const f32x4 bg = *(const f32x4*)(eX + 512 + cl), bu = *(const f32x4*)(eX + 512 + 128 + cl);
+  #pragma unroll
+          for (int mb = 0; mb < NRB; ++mb) {
+            const int grow = row0 + trow(mb);
+            const float xsc = eX[trow(mb)];
+            uint16_t o[4];
+  #pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              const float g = __fadd_rn(__fmul_rn(__fmul_rn((float)acc[j][mb][q], xsc), wsg[q]), bg[q]);
+              const float u = __fadd_rn(__fmul_rn(__fmul_rn((float)acc[j + 4][mb][q], xsc), wsu[q]), bu[q]);
+              o[q] = swiglu_bits(g, u, ODT);
+            }
+            if (grow < row_end && col < I)
+              *(u32x2*)((uint16_t*)a.out + (int64_t)grow * I + col) =
+                  u32x2{(uint32_t)o[0] | ((uint32_t)o[1] << 16), (uint32_t)o[2] | ((uint32_t)o[3] << 16)};
+          }
         }
       } else if (ksplit > 1) {
         // raw 32-bit accumulators of this work unit's K range; a reduce pass

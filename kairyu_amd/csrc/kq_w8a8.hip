@@ -986,3 +986,107 @@ extern "C" int kq_w8a8_fp8_linear(const void* x, int x_dtype, int64_t ldx, const
   return run_linear<kFmtFp8>("kq_w8a8_fp8_linear", x, x_dtype, ldx, scale_mode, scale_in, w, m, n,
                              k, ep, workspace, workspace_bytes, (hipStream_t)stream);
 }
+
+// ------------------------------------------------------------------ SwiGLU
+// A packed (gate, up) projection with SwiGLU, out[m][c] = silu(g) * up for
+// gate column c and up column I + c of the packed weight w [2I][K] (the
+// reference MLP's act_fn(gate(x)) * up(x), kairyu/models/layers.py:243-244,
+// over its packed projections, kairyu/models/packed_linear.py:58-149).
+// Prefill shapes (M > 64, I % 128 == 0, enough 256 x 256 tiles for half the
+// CUs) run the tile engine with the SwiGLU store epilogue: each tile pairs
+// gate columns [n0, n0 + 128) with up columns [I + n0, I + n0 + 128), so the
+// [M, 2I] projection output never reaches memory.  Other shapes run the
+// packed linear into the workspace and the elementwise pass.  Both produce
+// the bits of the packed linear followed by kq_swiglu.
+static bool swiglu_fused_applies(int64_t m, int64_t i_width, int64_t k, const void* x, int64_t ldx,
+                                 const void* w) {
+  if (m <= 64 || i_width % 128 != 0 || k % 16 != 0 || ((uintptr_t)w % 16) != 0) return false;
+  if (m * k >= ((int64_t)1 << 31) || 2 * i_width * k >= ((int64_t)1 << 31)) return false;
+  const int64_t tiles = ((m + kTgBM - 1) / kTgBM) * (i_width / 128);
+  return 2 * tiles >= tg_device_cus();
+}
+
+template <int FMT>
+static int run_swiglu_linear(const char* what, const void* x, int x_dtype, int64_t ldx, int scale_mode,
+                             const float* scale_in, const uint8_t* w, const float* wscale,
+                             int ws_per_channel, const void* bias, int bias_dtype, void* out,
+                             int64_t m, int64_t i_width, int64_t k, void* workspace, size_t ws_bytes,
+                             hipStream_t stream) {
+  if (i_width < 1 || i_width > 0x3fffffff) {
+    set_error("%s: bad width %lld", what, (long long)i_width);
+    return KQ_EINVAL;
+  }
+  const int64_t n = 2 * i_width;
+  Epi ep{nullptr, wscale, ws_per_channel, bias, bias_dtype, out, x_dtype, nullptr, (int)m, (int)n};
+  if (m > 0 && m <= 0x7fffffff && k >= 1 && k <= 65536 && ldx >= k && x != nullptr &&
+      (x_dtype == KQ_DTYPE_F16 || x_dtype == KQ_DTYPE_BF16) &&
+      swiglu_fused_applies(m, i_width, k, x, ldx, w)) {
+    const size_t xq_bytes = ((size_t)m * (size_t)k + 255) / 256 * 256;
+    const size_t xs_bytes = ((size_t)m * 4 + 255) / 256 * 256;
+    if (workspace == nullptr || ws_bytes < xq_bytes + xs_bytes) {
+      set_error("%s: workspace of %zu bytes is smaller than the %zu bytes this call needs", what,
+                workspace ? ws_bytes : (size_t)0, xq_bytes + xs_bytes);
+      return KQ_EWORKSPACE;
+    }
+    uint8_t* xq = (uint8_t*)workspace;
+    float* xs = (float*)(xq + xq_bytes);
+    const int rc = FMT == kFmtI8
+                       ? kq_act_quant_i8(x, x_dtype, m, k, ldx, (int8_t*)xq, xs, stream)
+                       : kq_act_quant_fp8(x, x_dtype, m, k, ldx, scale_in, scale_mode, xq, xs, stream);
+    if (rc != KQ_OK) return rc;
+    TileGemmArgs a{};
+    a.x = xq; a.x_rows = (int)m; a.xs = xs; a.gather = nullptr;
+    a.w = w; a.ws = wscale; a.ws_per_channel = ws_per_channel;
+    a.mtile_table = nullptr; a.mtile_count = nullptr;
+    a.M = (int)m; a.N = (int)n; a.K = (int)k; a.I = (int)i_width;
+    a.mtiles = (int)((m + kTgBM - 1) / kTgBM);
+    a.ntiles = (int)(i_width / 128);
+    a.out = out; a.out_dtype = x_dtype; a.bias = bias; a.bias_dtype = bias_dtype;
+    a.acc_out = nullptr;
+    a.ksplit = 1;
+    tg_launch<FMT == kFmtI8 ? kTgI8 : kTgFp8, false, kTgEpiSwiGluStore>(a, stream);
+    return check_launch(what);
+  }
+  // two passes: the packed projection [m][2I] in the activation dtype, then SwiGLU
+  const size_t tmp_bytes = ((size_t)(m > 0 ? m : 0) * (size_t)n * 2 + 255) / 256 * 256;
+  if (m > 0 && (workspace == nullptr || ws_bytes < tmp_bytes)) {
+    set_error("%s: workspace of %zu bytes is smaller than the %zu bytes this call needs", what,
+              workspace ? ws_bytes : (size_t)0, tmp_bytes);
+    return KQ_EWORKSPACE;
+  }
+  ep.out = workspace;
+  const int rc = run_linear<FMT>(what, x, x_dtype, ldx, scale_mode, scale_in, w, m, n, k, ep,
+                                 (uint8_t*)workspace + tmp_bytes, ws_bytes - tmp_bytes, stream);
+  if (rc != KQ_OK || m == 0) return rc;
+  return kq_swiglu(workspace, n, 0, x_dtype, out, m, i_width, stream);
+}
+
+extern "C" size_t kq_w8a8_swiglu_workspace_size(int64_t m, int64_t i_width, int64_t k) {
+  if (m <= 0 || i_width <= 0 || k <= 0) return 0;
+  const size_t fused = ((size_t)m * (size_t)k + 255) / 256 * 256 + ((size_t)m * 4 + 255) / 256 * 256;
+  const size_t tmp = ((size_t)m * (size_t)(2 * i_width) * 2 + 255) / 256 * 256;
+  return std::max(fused, tmp + kq_w8a8_linear_workspace_size(m, 2 * i_width, k));
+}
+
+extern "C" int kq_w8a8_i8_swiglu_linear(const void* x, int x_dtype, int64_t ldx, const int8_t* w,
+                                        const float* wscale, const void* bias, int bias_dtype, void* out,
+                                        int64_t m, int64_t i_width, int64_t k, void* workspace,
+                                        size_t workspace_bytes, void* stream) {
+  return run_swiglu_linear<kFmtI8>("kq_w8a8_i8_swiglu_linear", x, x_dtype, ldx, 0, nullptr,
+                                   (const uint8_t*)w, wscale, 1, bias, bias_dtype, out, m, i_width, k,
+                                   workspace, workspace_bytes, (hipStream_t)stream);
+}
+
+extern "C" int kq_w8a8_fp8_swiglu_linear(const void* x, int x_dtype, int64_t ldx, const float* scale_in,
+                                         int scale_mode, const uint8_t* w, const float* wscale,
+                                         int wscale_per_channel, const void* bias, int bias_dtype,
+                                         void* out, int64_t m, int64_t i_width, int64_t k,
+                                         void* workspace, size_t workspace_bytes, void* stream) {
+  if (scale_mode < 0 || scale_mode > 2 || (scale_mode != 0 && scale_in == nullptr)) {
+    set_error("kq_w8a8_fp8_swiglu_linear: bad scale_mode %d", scale_mode);
+    return KQ_EINVAL;
+  }
+  return run_swiglu_linear<kFmtFp8>("kq_w8a8_fp8_swiglu_linear", x, x_dtype, ldx, scale_mode, scale_in,
+                                    w, wscale, wscale_per_channel, bias, bias_dtype, out, m, i_width, k,
+                                    workspace, workspace_bytes, (hipStream_t)stream);
+}

@@ -23,7 +23,9 @@ for this package's quantized formats:
 reference MLP's activation (``kairyu/models/layers.py:243-244``), with
 torch's fp16 / bf16 roundings; for W4A16 in one call whose decode GEMV applies
 SwiGLU in its epilogue (gate and up 16-column blocks interleaved in a derived
-tiled operand), for W8A8 as the packed GEMM plus one elementwise pass.
+tiled operand), for W8A8 in one call whose prefill tile engine applies it in
+its epilogue (gate rows [n0, n0 + 128) paired with up rows [I + n0, ...) of
+the packed weight, no second copy).
 
 ``create`` returns ``None`` for anything it cannot pack exactly (mixed
 formats, in-features, devices, biases, group sizes, static input scales,
@@ -270,8 +272,8 @@ class QuantLinearPack:
         roundings on fp16/bf16 tensors.  W4A16 packs run one call whose decode
         GEMV applies SwiGLU in its epilogue (gate and up columns interleaved
         by 16 in a derived tiled operand, ``kq_w4a16_tiled_swiglu_gemm``);
-        W8A8 packs run the packed GEMM and one elementwise pass
-        (``kq_swiglu``)."""
+        W8A8 packs run ``kq_w8a8_*_swiglu_linear`` (SwiGLU in the tile
+        engine's epilogue for prefill shapes)."""
 
         if len(self._projections) != 2 or self._out_features[0] != self._out_features[1]:
             raise ValueError("swiglu needs a (gate, up) pack of equal widths")
@@ -287,11 +289,7 @@ class QuantLinearPack:
         lead = hidden.shape[:-1]
         stream = _native.stream_handle(hidden.device)
         if self._scheme in ("fp8", "int8"):
-            both = self._packed(hidden)
-            act = torch.empty((both.shape[0], width), device=hidden.device, dtype=hidden.dtype)
-            _native.call("kq_swiglu", both.data_ptr(), both.stride(0), 0,
-                         _native.dtype_code(hidden.dtype), act.data_ptr(), both.shape[0], width, stream)
-            return act.reshape(*lead, width)
+            return self._w8a8_swiglu(hidden, width).reshape(*lead, width)
         flat, _ = hip._prepare(hidden, gate, self._scheme, allocate_output=False)
         hip._validate_layout(up, self._scheme)
         d = self._swiglu_operands(hidden.device)
@@ -308,6 +306,36 @@ class QuantLinearPack:
             k, gate.group_size, ws.data_ptr(), ws.numel(), stream,
         )
         return act.reshape(*lead, width)
+
+    def _w8a8_swiglu(self, hidden: torch.Tensor, width: int) -> torch.Tensor:
+        """One kq_w8a8_*_swiglu_linear call on the packed [gate; up] weight:
+        SwiGLU in the tile engine's epilogue for prefill shapes, the packed
+        GEMM and the elementwise pass otherwise (the same bits either way)."""
+
+        from kairyu_amd import _native
+        from kairyu_amd.kernels import quant_gemm_hip as hip
+
+        gate = self._projections[0]
+        flat, _ = hip._prepare(hidden, gate, self._scheme, allocate_output=False)
+        hip._validate_layout(self._projections[1], self._scheme)
+        d = self._operands(hidden.device)
+        m_rows, k = flat.shape
+        act = torch.empty((m_rows, width), device=hidden.device, dtype=hidden.dtype)
+        bias = d["bias"] if gate._add_local_bias() else None
+        bias_args = (_native.ptr(bias), _native.dtype_code(None if bias is None else bias.dtype))
+        ws = hip._workspace(hidden.device, int(_native.library().kq_w8a8_swiglu_workspace_size(m_rows, width, k)))
+        stream = _native.stream_handle(hidden.device)
+        if self._scheme == "fp8":
+            mode, source = (0, None) if gate.activation_dynamic else (1, hip._f32(gate.input_scale))
+            _native.call("kq_w8a8_fp8_swiglu_linear", flat.data_ptr(), _native.dtype_code(flat.dtype),
+                         flat.stride(0), _native.ptr(source), mode, self._weight.data_ptr(),
+                         d["weight_scale"].data_ptr(), 1, *bias_args, act.data_ptr(), m_rows, width, k,
+                         ws.data_ptr(), ws.numel(), stream)
+        else:
+            _native.call("kq_w8a8_i8_swiglu_linear", flat.data_ptr(), _native.dtype_code(flat.dtype),
+                         flat.stride(0), self._weight.data_ptr(), d["weight_scale"].data_ptr(), *bias_args,
+                         act.data_ptr(), m_rows, width, k, ws.data_ptr(), ws.numel(), stream)
+        return act
 
     def _swiglu_operands(self, device: torch.device) -> dict:
         """The (gate, up) pair tiled as one weight whose 16-column blocks of

@@ -135,7 +135,9 @@ def test_pack_graph_replays_match_eager(cuda):
 # silu(gate(x)) * up(x) of a (gate, up) pack (kairyu/models/layers.py:243-244).
 # W4A16: one kq_w4a16_tiled_swiglu_gemm call; decode shapes (here N = 2 x 4096
 # on K = 4096) apply SwiGLU in the GEMV epilogue, others run the tiled GEMM
-# and the elementwise pass.  W8A8: the packed GEMM and kq_swiglu.
+# and the elementwise pass.  W8A8: one kq_w8a8_*_swiglu_linear call; prefill
+# shapes apply SwiGLU in the tile engine's epilogue, others run the packed
+# GEMM and kq_swiglu.
 _SWIGLU_CASES = [
     # (scheme, m, k, width, dtype, bias)
     ("gptq", 1, 4096, 4096, torch.float16, False),
@@ -156,6 +158,9 @@ _SWIGLU_CASES = [
     ("gptq", 1, 2048, 11008, torch.bfloat16, True),
     ("fp8", 1, 2048, 2048, torch.bfloat16, True),
     ("fp8", 300, 1024, 1024, torch.float16, False),
+    # prefill shapes: SwiGLU in the tile engine's epilogue (>= 128 tiles of 256 x 256)
+    ("fp8", 1024, 1024, 4096, torch.bfloat16, True),
+    ("int8", 2048, 1024, 2048, torch.float16, False),
     ("int8", 16, 2048, 1024, torch.bfloat16, True),
 ]
 
@@ -257,3 +262,24 @@ def test_swiglu_pack_rejects_diverged_g_idx(cuda):
     up.g_idx.copy_(other.to(cuda))
     with pytest.raises(RuntimeError, match="one g_idx"):
         pack.swiglu(x)
+
+
+@pytest.mark.parametrize("scheme,m,k,width,dtype,bias", [
+    ("fp8", 1024, 1024, 4096, torch.bfloat16, True),
+    ("int8", 2048, 1024, 2048, torch.float16, False),
+])
+def test_w8a8_swiglu_epilogue_bit_identical_to_two_passes(cuda, scheme, m, k, width, dtype, bias):
+    """The tile engine's SwiGLU store epilogue gives the bits of the packed
+    GEMM followed by the elementwise pass (kq_swiglu) on the same call."""
+    from kairyu_amd import _native
+
+    gate, up = (mod.to(cuda) for mod in _swiglu_pair(scheme, k, width, bias, seed=m + width))
+    pack = QuantLinearPack.create([gate, up])
+    x = torch.randn(m, k, generator=torch.Generator().manual_seed(width)).to(dtype).to(cuda)
+    fused = pack.swiglu(x)
+    both = pack(x)
+    packed = torch.cat(both, dim=-1).contiguous()
+    two = torch.empty(m, width, device=cuda, dtype=dtype)
+    _native.call("kq_swiglu", packed.data_ptr(), packed.stride(0), 0, _native.dtype_code(dtype), two.data_ptr(),
+                 m, width, _native.stream_handle(torch.device(cuda)))
+    assert torch.equal(fused.view(torch.int16), two.view(torch.int16))
