@@ -978,10 +978,14 @@ struct W4pShape {
   static_assert(XOps >= 1 && WOps >= 1 && SOps + 1 <= 8, "tile shape");
 };
 
-template <int TM, int TN, int WM, int NS>
+// SWIGLU: the operand interleaves gate and up 16-column tiles (2p gate, 2p + 1
+// up), so each wave's pair of column tiles (TN = 2) holds both halves of its
+// 16 output columns and the epilogue writes silu(gate) * up into out [M][N/2].
+template <int TM, int TN, int WM, int NS, bool SWIGLU = false>
 __global__ void __launch_bounds__(512)
 w4a16_prefill_kernel(W4Args a, int mblocks, int tiles) {
   using S = W4pShape<TM, TN, WM>;
+  static_assert(!SWIGLU || TN == 2, "the SwiGLU epilogue pairs a wave's two column tiles");
   __shared__ __attribute__((aligned(16))) uint8_t smem[NS * S::Stage + 8 * 256];
   const int lane = lane_id();
   const int wave = __builtin_amdgcn_readfirstlane(wave_id());
@@ -1113,6 +1117,42 @@ w4a16_prefill_kernel(W4Args a, int mblocks, int tiles) {
 
   // epilogue: lane (c, g) of block (tn, i) holds rows m = .. + c, columns
   // n = .. + 4g .. 4g+3
+  if constexpr (SWIGLU) {
+    const int ng = n0 + wn * 32 + 4 * g;     // gate column of the interleaved operand (up: + 16)
+    const int width = a.N / 2;
+    const int oc = n0 / 2 + wn * 16 + 4 * g;  // output column
+    float bg[4] = {0.f, 0.f, 0.f, 0.f}, bu[4] = {0.f, 0.f, 0.f, 0.f};
+    if (a.bias_dtype != KQ_DTYPE_NONE)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        bg[q] = ng + q < a.N ? load_as_f32(a.bias, a.bias_dtype, ng + q) : 0.f;
+        bu[q] = ng + 16 + q < a.N ? load_as_f32(a.bias, a.bias_dtype, ng + 16 + q) : 0.f;
+      }
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      const int m = m0 + (wm * TM + i) * 16 + c;
+      if (m >= a.M) continue;
+      uint16_t o[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        float gv = acc[0][i][q], uv = acc[1][i][q];
+        if (a.bias_dtype != KQ_DTYPE_NONE) {
+          gv = __fadd_rn(gv, bg[q]);
+          uv = __fadd_rn(uv, bu[q]);
+        }
+        o[q] = swiglu_bits(gv, uv, a.out_dtype);
+      }
+      uint16_t* dst = a.out + (int64_t)m * width + oc;
+      if (oc + 3 < width) {
+        *(u32x2*)dst = u32x2{(uint32_t)o[0] | ((uint32_t)o[1] << 16), (uint32_t)o[2] | ((uint32_t)o[3] << 16)};
+      } else {
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          if (oc + q < width) dst[q] = o[q];
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int tn = 0; tn < TN; ++tn) {
     const int n = n0 + (wn * TN + tn) * 16 + 4 * g;
@@ -1490,14 +1530,14 @@ static bool prefill_applies(const W4Args& a, int gmode) {
          (uint64_t)w4_tile_words(a.N, a.K) * 4u < ((uint64_t)1 << 31);
 }
 
-template <int TM, int TN, int WM, int NS>
+template <int TM, int TN, int WM, int NS, bool SWIGLU = false>
 static void launch_prefill_shape(const W4Args& a, hipStream_t stream) {
   using S = W4pShape<TM, TN, WM>;
   const int mblocks = (a.M + S::BM - 1) / S::BM;
   const int tiles = mblocks * ((a.N + S::BN - 1) / S::BN);
   const int grid = 8 * ((tiles + 7) / 8);
-  hipLaunchKernelGGL((w4a16_prefill_kernel<TM, TN, WM, NS>), dim3(grid), dim3(512), 0, stream, a, mblocks,
-                     tiles);
+  hipLaunchKernelGGL((w4a16_prefill_kernel<TM, TN, WM, NS, SWIGLU>), dim3(grid), dim3(512), 0, stream, a,
+                     mblocks, tiles);
 }
 
 // 64 x 128 tiles up to M = 64 (twice the column tiles of 256-wide ones, no
@@ -1506,6 +1546,14 @@ static void launch_prefill_shape(const W4Args& a, hipStream_t stream) {
 // Measured on C2 (N = 28672, K = 4096): M = 64 34.4 -> 33.4 us against
 // 3 stages; M = 512 152 -> 140 us against 2 x 4 waves of 64 x 64.
 static void launch_prefill(const W4Args& a, hipStream_t stream) {
+  if (a.swiglu) {
+    // M > 64 (kq_w4a16_tiled_swiglu_gemm): each wave's two column tiles are a
+    // gate/up pair.  (A 64 x 256 form for M <= 64 halves the workgroups of the
+    // 64 x 128 tiles: C2's gate/up at M = 64 took 45.3 us fused against 41.8 us
+    // for the 64 x 128 GEMM and the elementwise pass.)
+    launch_prefill_shape<8, 2, 1, 3, true>(a, stream);
+    return;
+  }
   if (a.M <= 64) launch_prefill_shape<4, 1, 1, 4>(a, stream);
   else launch_prefill_shape<8, 2, 1, 3>(a, stream);
 }
@@ -1844,7 +1892,12 @@ extern "C" int kq_w4a16_tiled_swiglu_gemm(const void* x, int x_dtype, const int3
   GvPlan gp{};
   int s_ = 0, spg_ = 0;
   a.swiglu = 1;
-  if (a.M > 0 && gv_plan(a, kGptq, gmode, &gp, &s_, &spg_))
+  // decode GEMV or (M > 64) prefill GEMM with the SwiGLU epilogue: one launch
+  // (plus the activation staging pass), out written directly.  Llama-3-8B
+  // gate/up (K = 4096, I = 14336, act-order), graph replay: M = 512 169 ->
+  // 135 us, 2048 636 -> 495 us, 4096 1333 -> 1015 us against the GEMM and the
+  // elementwise pass
+  if (a.M > 0 && (gv_plan(a, kGptq, gmode, &gp, &s_, &spg_) || (a.M > 64 && prefill_applies(a, gmode))))
     return run_w4(what, kGptq, a, gmode, workspace, workspace_bytes, (hipStream_t)stream);
   // two passes: [m][2I] in the activation dtype after the GEMM's scratch
   a.swiglu = 0;

@@ -21,9 +21,10 @@ for this package's quantized formats:
 
 ``swiglu(x)`` of a (gate, up) pack returns ``silu(gate(x)) * up(x)``, the
 reference MLP's activation (``kairyu/models/layers.py:243-244``), with
-torch's fp16 / bf16 roundings; for W4A16 in one call whose decode GEMV applies
-SwiGLU in its epilogue (gate and up 16-column blocks interleaved in a derived
-tiled operand), for W8A8 in one call whose prefill tile engine applies it in
+torch's fp16 / bf16 roundings; for W4A16 in one call whose decode GEMV (M <=
+16) or prefill GEMM (M > 64) applies SwiGLU in its epilogue (gate and up
+16-column blocks interleaved in a derived tiled operand), for W8A8 in one
+call whose prefill tile engine applies it in
 its epilogue (gate rows [n0, n0 + 128) paired with up rows [I + n0, ...) of
 the packed weight, no second copy).
 
@@ -270,8 +271,9 @@ class QuantLinearPack:
         """``silu(gate(x)) * up(x)`` of a (gate, up) pack, as the reference's
         MLP computes it (``kairyu/models/layers.py:243-244``) with torch's
         roundings on fp16/bf16 tensors.  W4A16 packs run one call whose decode
-        GEMV applies SwiGLU in its epilogue (gate and up columns interleaved
-        by 16 in a derived tiled operand, ``kq_w4a16_tiled_swiglu_gemm``);
+        GEMV or prefill GEMM applies SwiGLU in its epilogue (gate and up
+        columns interleaved by 16 in a derived tiled operand,
+        ``kq_w4a16_tiled_swiglu_gemm``);
         W8A8 packs run ``kq_w8a8_*_swiglu_linear`` (SwiGLU in the tile
         engine's epilogue for prefill shapes)."""
 
