@@ -299,8 +299,8 @@ int kq_gptq_permute_qweight(const int32_t* qweight, const int32_t* perm, int32_t
  * (the finegrained_fp8_linear(..., block_size=[128, 128]) convention the
  * reference calls at kairyu/kernels/deepseek_v4_moe_gpu.py:60-74). */
 
-/* Per token, per 128-wide block quantization of x [rows, k] (fp16/bf16):
- * xq e4m3 [rows, k], xs fp32 [rows, ceil(k/128)].  Replaces the activation
+/* Per token, per 128-wide block quantization of x [rows, k] (fp16/bf16,
+ * k <= 65535 * 2048): xq e4m3 [rows, k], xs fp32 [rows, ceil(k/128)].  Replaces the activation
  * side of finegrained_fp8_linear (deepseek_v4_moe_gpu.py:60-74). */
 int kq_act_quant_fp8_blocks(const void* x, int x_dtype, int64_t rows, int64_t k, int64_t ldx,
                             uint8_t* xq, float* xs, void* stream);
@@ -321,7 +321,8 @@ int kq_block_fp8_gemm(const uint8_t* xq, const float* xs, const uint8_t* w, cons
 int kq_moe_route_topk(const void* logits, int dtype, int64_t tokens, int64_t experts, int top_k,
                       int norm_topk_prob, int32_t* topk_idx, float* topk_w, void* stream);
 
-/* Bytes of workspace kq_moe_block_fp8_experts needs for this shape. */
+/* Bytes of workspace kq_moe_block_fp8_experts and
+ * kq_moe_routed_block_fp8_experts need for this shape. */
 size_t kq_moe_workspace_size(int64_t tokens, int64_t hidden, int64_t inter, int64_t experts,
                              int top_k);
 
@@ -341,6 +342,21 @@ int kq_moe_block_fp8_experts(const void* hidden, int dtype, int64_t tokens, int6
                              const float* topk_w, const uint8_t* w13, const float* s13,
                              const uint8_t* w2, const float* s2, void* out, void* workspace,
                              size_t workspace_bytes, void* stream);
+
+/* The Qwen3 sparse block from its router logits: kq_moe_route_topk's routing
+ * (logits fp16/bf16/fp32 [tokens, experts], experts <= 512, top_k <= 32;
+ * topk_idx int32 and topk_w fp32 [tokens, top_k] are written as that call
+ * writes them) followed by kq_moe_block_fp8_experts, with the same outputs
+ * bit for bit.  The routing, the sort's expert histograms and the token
+ * quantization share one launch.  Replaces route_experts + _mix_experts of
+ * the sparse block's forward (kairyu/models/moe.py:255-273, 86-119,
+ * 324-332). */
+int kq_moe_routed_block_fp8_experts(const void* logits, int logits_dtype, int norm_topk_prob,
+                                    const void* hidden, int dtype, int64_t tokens,
+                                    int64_t hidden_size, int64_t inter, int64_t experts, int top_k,
+                                    const uint8_t* w13, const float* s13, const uint8_t* w2,
+                                    const float* s2, int32_t* topk_idx, float* topk_w, void* out,
+                                    void* workspace, size_t workspace_bytes, void* stream);
 
 /* ---------------------------------------------------------------- ceilings
  * Measurement aids, no counterpart in the reference: the box's own ceilings

@@ -87,6 +87,9 @@ _SIGNATURES: dict[str, list] = {
     "kq_moe_block_fp8_experts": [
         _P, _I, _I64, _I64, _I64, _I64, _I, _P, _P, _P, _P, _P, _P, _P, _P, _SZ, _P,
     ],
+    "kq_moe_routed_block_fp8_experts": [
+        _P, _I, _I, _P, _I, _I64, _I64, _I64, _I64, _I, _P, _P, _P, _P, _P, _P, _P, _P, _SZ, _P,
+    ],
 }
 
 _lock = threading.Lock()

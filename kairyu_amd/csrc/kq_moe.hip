@@ -83,70 +83,111 @@ KQ_DEV float key_float(uint32_t k) {
   return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
 }
 
-// One wave per token: k rounds of a wave-wide max of the value keys, ties
-// to the smallest expert (a ballot of the lanes holding the maximum); every
-// lane sees each round's winner, lane r keeps slot r's logit.
+// One wave routes TW tokens at once (their selection chains interleave):
+// per token, k rounds of a wave-wide max of the value keys, ties to the
+// smallest expert (a ballot of the lanes holding the maximum); every lane
+// sees each round's winner, lane r keeps slot r's logit.  v[j][i] holds token
+// t[j]'s logit of expert lane + 64 i; tokens j >= live are computed on a
+// repeated row and not written.  `sids`, when given, receives token j's k
+// experts in slot order at sids[j * sstride] (the sort chunk's row ids).
+template <int PL, int TW>
+KQ_DEV void route_tokens(const float (&v)[TW][PL], const int (&t)[TW], int live, int E, int k, int norm,
+                         int32_t* __restrict__ idx, float* __restrict__ w, int* sids, int sstride) {
+  const int lane = lane_id();
+  // value keys of the live experts; 0 marks a dead slot (no float maps to 0)
+  uint32_t key[TW][PL];
+  float my_sel[TW], first[TW], denom[TW];
+#pragma unroll
+  for (int j = 0; j < TW; ++j) {
+#pragma unroll
+    for (int i = 0; i < PL; ++i) key[j][i] = lane + 64 * i < E ? float_key(v[j][i]) : 0u;
+    my_sel[j] = first[j] = denom[j] = 0.0f;
+  }
+  for (int r = 0; r < k; ++r) {
+#pragma unroll
+    for (int j = 0; j < TW; ++j) {
+      // the largest key, then the smallest expert holding it: slot i covers
+      // experts 64i..64i+63, so the first slot with a match holds the smallest
+      uint32_t m = key[j][0];
+#pragma unroll
+      for (int i = 1; i < PL; ++i) m = max(m, key[j][i]);
+      m = wave_max_u32_dpp(m);
+      int e = -1;
+#pragma unroll
+      for (int i = PL - 1; i >= 0; --i) {
+        const uint64_t hit = __ballot(key[j][i] == m);
+        if (hit) e = 64 * i + (int)__builtin_ctzll(hit);
+      }
+      const float val = key_float(m);
+#pragma unroll
+      for (int i = 0; i < PL; ++i)
+        if (lane + 64 * i == e) key[j][i] = 0u;
+      if (lane == 0 && j < live) {
+        idx[(int64_t)t[j] * k + r] = e;
+        if (sids) sids[j * sstride + r] = e;
+      }
+      if (lane == r) my_sel[j] = val;
+      if (r == 0) first[j] = val;
+      if (norm) denom[j] = __fadd_rn(denom[j], expf(val - first[j]));  // slot order, uniform
+    }
+  }
+  // fp32 softmax over the selected logits, or over all logits gathered
+#pragma unroll
+  for (int j = 0; j < TW; ++j) {
+    float mx = first[j];
+    if (!norm) {
+      float m = -__builtin_inff();
+#pragma unroll
+      for (int i = 0; i < PL; ++i)
+        if (lane + 64 * i < E) m = fmaxf(m, v[j][i]);
+      mx = wave_max(m);
+      float sum = 0.0f;
+#pragma unroll
+      for (int i = 0; i < PL; ++i)
+        if (lane + 64 * i < E) sum += expf(v[j][i] - mx);
+      denom[j] = wave_sum(sum);
+    }
+    if (lane < k && j < live) w[(int64_t)t[j] * k + lane] = __fdiv_rn(expf(my_sel[j] - mx), denom[j]);
+  }
+}
+
+// The router logits of token t, widened; experts past E read as 0 (never
+// selected: their keys are dead).
+template <int PL>
+KQ_DEV void route_load(const void* __restrict__ logits, int dtype, int t, int E, float (&v)[PL]) {
+  const int lane = lane_id();
+#pragma unroll
+  for (int i = 0; i < PL; ++i) {
+    const int e = lane + 64 * i;
+    v[i] = e < E ? load_as_f32(logits, dtype, (int64_t)t * E + e) : 0.0f;
+  }
+}
+
 template <int PL>   // logits per lane: E <= 64 * PL
 __global__ void __launch_bounds__(256)
 moe_route_kernel(const void* __restrict__ logits, int dtype, int T, int E, int k, int norm,
                  int32_t* __restrict__ idx, float* __restrict__ w) {
-  const int lane = lane_id();
   const int t = blockIdx.x * 4 + wave_id();
   if (t >= T) return;
-  float v[PL];
-  bool live[PL];
-#pragma unroll
-  for (int i = 0; i < PL; ++i) {
-    const int e = lane + 64 * i;
-    live[i] = e < E;
-    v[i] = live[i] ? load_as_f32(logits, dtype, (int64_t)t * E + e) : 0.0f;
-  }
-  // value keys of the live experts; 0 marks a dead slot (no float maps to 0)
-  uint32_t key[PL];
-#pragma unroll
-  for (int i = 0; i < PL; ++i) key[i] = live[i] ? float_key(v[i]) : 0u;
-  float my_sel = 0.0f, first = 0.0f, denom = 0.0f;
-  for (int r = 0; r < k; ++r) {
-    // the largest key, then the smallest expert holding it: slot i covers
-    // experts 64i..64i+63, so the first slot with a match holds the smallest
-    uint32_t m = key[0];
-#pragma unroll
-    for (int i = 1; i < PL; ++i) m = max(m, key[i]);
-    m = wave_max_u32_dpp(m);
-    int e = -1;
-#pragma unroll
-    for (int i = PL - 1; i >= 0; --i) {
-      const uint64_t hit = __ballot(key[i] == m);
-      if (hit) e = 64 * i + (int)__builtin_ctzll(hit);
-    }
-    const float val = key_float(m);
-#pragma unroll
-    for (int i = 0; i < PL; ++i)
-      if (lane + 64 * i == e) key[i] = 0u;
-    if (lane == 0) idx[(int64_t)t * k + r] = e;
-    if (lane == r) my_sel = val;
-    if (r == 0) first = val;
-    if (norm) denom = __fadd_rn(denom, expf(val - first));  // slot order, uniform
-  }
-  // fp32 softmax over the selected logits, or over all logits gathered
-  float mx = first;
-  if (!norm) {
-    float m = -__builtin_inff();
-#pragma unroll
-    for (int i = 0; i < PL; ++i)
-      if (lane + 64 * i < E) m = fmaxf(m, v[i]);
-    mx = wave_max(m);
-    float sum = 0.0f;
-#pragma unroll
-    for (int i = 0; i < PL; ++i)
-      if (lane + 64 * i < E) sum += expf(v[i] - mx);
-    denom = wave_sum(sum);
-  }
-  if (lane < k) w[(int64_t)t * k + lane] = __fdiv_rn(expf(my_sel - mx), denom);
+  float v[1][PL];
+  route_load<PL>(logits, dtype, t, E, v[0]);
+  const int tt[1] = {t};
+  route_tokens<PL, 1>(v, tt, 1, E, k, norm, idx, w, nullptr, 0);
 }
 
 // -------------------------------------------------------------- stable sort
-constexpr int kSortChunk = 256;   // rows per chunk = threads per sort workgroup
+constexpr int kSortChunk = 256;   // threads per sort workgroup (>= rows per chunk)
+// Rows per sort chunk: whole tokens (kSortChunk / k of them, their rows
+// consecutive in the flat routed order r = token * k + slot), so one
+// workgroup can route a chunk's tokens and count its experts; 256 rows for
+// k > 256 (expert ids given by the caller).
+__host__ __device__ inline int moe_chunk_rows(int k) {
+  return k <= kSortChunk ? (kSortChunk / k) * k : kSortChunk;
+}
+// Chunks x experts up to which one launch both scans the chunk histograms and
+// scatters (every workgroup reads the whole histogram table: 128 KB at most).
+constexpr int kFusedScanMax = 32768;
+
 // Row tiles of the expert GEMMs: 64 * moe_nrb rows.  320-row tiles (NRB 5)
 // when the routing averages more than 192 rows per expert: an even top-k
 // routing then spreads the experts' rows over ~256 +- 50, which 256-row tiles
@@ -158,13 +199,14 @@ static inline int moe_nrb(int64_t routed_rows, int64_t experts) {
   return routed_rows > 192 * experts ? 5 : 4;
 }
 
-// Per-chunk expert histogram: counts[c][e] for chunk c (hist: E ints of LDS).
-KQ_DEV void moe_count_chunk(const int32_t* __restrict__ idx, int R, int E, int32_t* __restrict__ counts,
+// Per-chunk expert histogram of the CR rows of chunk c: counts[c][e]
+// (hist: E ints of LDS).
+KQ_DEV void moe_count_chunk(const int32_t* __restrict__ idx, int R, int CR, int E, int32_t* __restrict__ counts,
                             int c, int* hist) {
   for (int i = threadIdx.x; i < E; i += kSortChunk) hist[i] = 0;
   __syncthreads();
-  const int r = c * kSortChunk + threadIdx.x;
-  if (r < R) {
+  const int r = c * CR + (int)threadIdx.x;
+  if ((int)threadIdx.x < CR && r < R) {
     const int e = idx[r];
     if (e >= 0 && e < E) atomicAdd(&hist[e], 1);
   }
@@ -204,6 +246,33 @@ KQ_DEV int block_exclusive_scan(int* v, int* tmp, int n) {
   return total;
 }
 
+// The row-tile table from the experts' row counts: tile i -> (expert, first
+// row, end row, 0); unused entries get expert -1; tile_count = tiles in use.
+// Thread t < E writes expert t's tiles (first[t]: its first tile index,
+// start[t]: its first sorted row, rows[t]: its row count); all threads clear
+// the unused entries.
+KQ_DEV void moe_write_tiles(const int* first, const int* start, const int* rows, int E, int BM, int total_tiles,
+                            int max_tiles, int32_t* __restrict__ tiles, int32_t* __restrict__ tile_count) {
+  const int t = threadIdx.x;
+  if (t < E) {
+    const int nt = (rows[t] + BM - 1) / BM;
+    for (int i = 0; i < nt && first[t] + i < max_tiles; ++i) {
+      int32_t* d = tiles + 4 * (first[t] + i);
+      d[0] = t;
+      d[1] = start[t] + i * BM;
+      d[2] = min(start[t] + rows[t], start[t] + (i + 1) * BM);
+      d[3] = 0;
+    }
+  }
+  if (t == 0) tile_count[0] = min(total_tiles, max_tiles);
+  for (int i = total_tiles + t; i < max_tiles; i += blockDim.x) {
+    tiles[4 * i] = -1;
+    tiles[4 * i + 1] = 0;
+    tiles[4 * i + 2] = 0;
+    tiles[4 * i + 3] = 0;
+  }
+}
+
 // Chunk slices of the scan: the largest power of two with 2 * slices * E <=
 // 1024 (at least 1), so slices * E threads each scan one run of chunks.
 __host__ __device__ inline int moe_scan_slices(int E) {
@@ -212,12 +281,11 @@ __host__ __device__ inline int moe_scan_slices(int E) {
   return slices;
 }
 
-// One 1024-thread workgroup: column-wise exclusive scan of counts[C][E] into
-// base[c][e] (sorted position of chunk c's first row of expert e), expert
-// offsets, the row-tile table (tile i -> (expert, first row, end row, 0);
-// unused entries get expert -1) and the count of tiles in use.  Thread
-// (slice, e) scans a contiguous run of chunks.  PER > 0: the run has at most
-// PER chunks, and the thread issues all its count loads at once into
+// One 1024-thread workgroup (chunk tables too large for moe_scan_scatter):
+// column-wise exclusive scan of counts[C][E] into base[c][e] (sorted position
+// of chunk c's first row of expert e), expert offsets and the row-tile table.
+// Thread (slice, e) scans a contiguous run of chunks.  PER > 0: the run has
+// at most PER chunks, and the thread issues all its count loads at once into
 // registers (unconditional loads from clamped, in-range addresses, so no load
 // sits under a branch and they overlap) and keeps them for the second pass;
 // PER = 0: any run length, one load at a time.
@@ -226,7 +294,7 @@ __global__ void __launch_bounds__(1024)
 moe_scan_kernel(const int32_t* __restrict__ counts, int C, int E, int BM, int max_tiles,
                 int32_t* __restrict__ offsets, int32_t* __restrict__ base, int32_t* __restrict__ tiles,
                 int32_t* __restrict__ tile_count) {
-  __shared__ int part[1024], tot[1024], ntile[1024], tmp[1024];
+  __shared__ int part[1024], tot[1024], rows[1024], ntile[1024], tmp[1024];
   const int t = threadIdx.x;
   const int slices = moe_scan_slices(E);
   const int per = (C + slices - 1) / slices;
@@ -257,12 +325,12 @@ moe_scan_kernel(const int32_t* __restrict__ counts, int C, int E, int BM, int ma
       run += v;
     }
     tot[t] = run;
+    rows[t] = run;
     ntile[t] = (run + BM - 1) / BM;
   }
   __syncthreads();
   const int total_rows = block_exclusive_scan(tot, tmp, E);     // tot -> expert offsets
   const int total_tiles = block_exclusive_scan(ntile, tmp, E);  // ntile -> first tile
-  (void)total_rows;
   if (active) {
     int run = tot[e] + part[t];
     if constexpr (PER > 0) {
@@ -278,43 +346,27 @@ moe_scan_kernel(const int32_t* __restrict__ counts, int C, int E, int BM, int ma
       }
     }
   }
-  if (t < E) {
-    offsets[t] = tot[t];
-    if (t == E - 1) offsets[E] = total_rows;
-    const int rows = (t == E - 1 ? total_rows : tot[t + 1]) - tot[t];
-    const int nt = (rows + BM - 1) / BM;
-    for (int i = 0; i < nt && ntile[t] + i < max_tiles; ++i) {
-      int32_t* d = tiles + 4 * (ntile[t] + i);
-      d[0] = t;
-      d[1] = tot[t] + i * BM;
-      d[2] = min(tot[t] + rows, tot[t] + (i + 1) * BM);
-      d[3] = 0;
-    }
-  }
-  if (t == 0) tile_count[0] = min(total_tiles, max_tiles);
-  for (int i = total_tiles + t; i < max_tiles; i += 1024) {
-    tiles[4 * i] = -1;
-    tiles[4 * i + 1] = 0;
-    tiles[4 * i + 2] = 0;
-    tiles[4 * i + 3] = 0;
-  }
+  if (t < E) offsets[t] = tot[t];
+  if (t == 0) offsets[E] = total_rows;
+  moe_write_tiles(ntile, tot, rows, E, BM, total_tiles, max_tiles, tiles, tile_count);
 }
 
-// Sorted position of row r = base[chunk][e] + its rank among the chunk's
-// earlier rows routed to the same expert (stable).  The rank is the rows of
-// expert e in the chunk's earlier waves (per-wave counts in LDS, whist[w][e])
-// plus the earlier lanes of this wave with expert e: one ballot per bit of
-// the expert id leaves the mask of lanes whose id equals this lane's.
-// sorted_tok[pos] is the token of the routed row at sorted position pos (the
-// gate_up GEMM's row source), inv[r] the sorted position of routed row r.
-__global__ void __launch_bounds__(kSortChunk)
-moe_scatter_kernel(const int32_t* __restrict__ idx, int R, int E, int top_k, const int32_t* __restrict__ base,
-                   int32_t* __restrict__ sorted_tok, int32_t* __restrict__ inv) {
-  extern __shared__ int whist[];   // [kSortChunk / 64][E]
-  const int c = blockIdx.x, t = threadIdx.x;
+// Sorted position of row r = base[e] (chunk c's first row of expert e) + its
+// rank among the chunk's earlier rows routed to the same expert (stable).
+// The rank is the rows of expert e in the chunk's earlier waves (per-wave
+// counts in LDS, whist[w][e]) plus the earlier lanes of this wave with expert
+// e: one ballot per bit of the expert id leaves the mask of lanes whose id
+// equals this lane's.  sorted_tok[pos] is the token of the routed row at
+// sorted position pos (the gate_up GEMM's row source), inv[r] the sorted
+// position of routed row r.
+KQ_DEV void moe_scatter_chunk(const int32_t* __restrict__ idx, int R, int CR, int E, int top_k, int c,
+                              const int32_t* base, int* whist, int32_t* __restrict__ sorted_tok,
+                              int32_t* __restrict__ inv) {
+  const int t = threadIdx.x;
   const int w = t >> 6, lane = t & 63;
-  const int r = c * kSortChunk + t;
-  const int e = r < R ? idx[r] : -1;
+  const int r = c * CR + t;
+  const bool in = t < CR && r < R;
+  const int e = in ? idx[r] : -1;
   const bool ok = e >= 0 && e < E;
   for (int i = t; i < (kSortChunk / 64) * E; i += kSortChunk) whist[i] = 0;
   const int nbits = E > 1 ? 32 - __builtin_clz((unsigned)(E - 1)) : 0;
@@ -328,39 +380,146 @@ moe_scatter_kernel(const int32_t* __restrict__ idx, int R, int E, int top_k, con
   __syncthreads();   // whist cleared
   if (ok && rank_in == 0) whist[w * E + e] = __popcll(same);
   __syncthreads();
-  if (r >= R) return;
+  if (!in) return;
   if (!ok) {
     inv[r] = -1;
     return;
   }
   int rank = rank_in;
   for (int w2 = 0; w2 < w; ++w2) rank += whist[w2 * E + e];
-  const int pos = base[(int64_t)c * E + e] + rank;
+  const int pos = base[e] + rank;
   // (pos < R always holds for a consistent base table; the check keeps a
   // position outside the buffer from ever being written or combined)
   if (pos < R) sorted_tok[pos] = r / top_k;
   inv[r] = pos < R ? pos : -1;
 }
 
-// --------------------------------------------------- 1x128 activation quant
-// One 2048-element span (256 threads x 8) of row `row`: 16 threads per 1x128
-// block, e4m3 values and the block's scale.
-KQ_DEV void act_quant_fp8_blocks_span(const uint16_t* __restrict__ x, int dtype, int K, int64_t ldx, bool vec,
-                                      uint8_t* __restrict__ xq, float* __restrict__ xs, int64_t row, int y) {
-  const int k0 = y * 2048 + threadIdx.x * 8;
-  const uint16_t* xr = x + row * ldx;
-  float v[8];
-  if (vec && k0 + 8 <= K) {
-    const u32x4 raw = *(const u32x4*)(xr + k0);
+__global__ void __launch_bounds__(kSortChunk)
+moe_scatter_kernel(const int32_t* __restrict__ idx, int R, int CR, int E, int top_k,
+                   const int32_t* __restrict__ base, int32_t* __restrict__ sorted_tok, int32_t* __restrict__ inv) {
+  extern __shared__ int whist[];   // [kSortChunk / 64][E]
+  const int c = blockIdx.x;
+  moe_scatter_chunk(idx, R, CR, E, top_k, c, base + (int64_t)c * E, whist, sorted_tok, inv);
+}
+
+// Scan and scatter in one launch (E <= 256, C * E <= kFusedScanMax): chunk
+// c's workgroup sums the histogram table itself — per expert, the rows of the
+// chunks before c and of all chunks (thread (slice, e) one run of chunks, 16
+// loads in flight) — scans the expert totals into offsets, and scatters its
+// rows; workgroup 0 also writes the expert offsets and the row-tile table.
+// Every workgroup derives the same totals, so the positions are those of the
+// two-launch form.
+__global__ void __launch_bounds__(kSortChunk)
+moe_scan_scatter_kernel(const int32_t* __restrict__ idx, int R, int CR, int E, int top_k,
+                        const int32_t* __restrict__ counts, int C, int BM, int max_tiles,
+                        int32_t* __restrict__ offsets, int32_t* __restrict__ tiles,
+                        int32_t* __restrict__ tile_count, int32_t* __restrict__ sorted_tok,
+                        int32_t* __restrict__ inv) {
+  __shared__ int part_pre[4 * kSortChunk], part_tot[4 * kSortChunk], sbase[kSortChunk], soff[kSortChunk];
+  __shared__ int srows[kSortChunk], sfirst[kSortChunk], tmp[kSortChunk];
+  __shared__ int whist[(kSortChunk / 64) * kSortChunk];
+  const int c = blockIdx.x, t = threadIdx.x;
+  // thread (slice, q) sums experts [VW q, VW q + VW) over one run of chunks
+  // (16-byte loads of four experts when E % 4 == 0)
+  const int VW = E % 4 == 0 ? 4 : 1;
+  const int Q = E / VW, S = kSortChunk / Q;  // chunk slices (E <= kSortChunk)
+  const int q = t % Q, sl = t / Q;
+  int pre[4] = {0, 0, 0, 0}, tot[4] = {0, 0, 0, 0};
+  if (sl < S) {
+    const int c0 = (int)((int64_t)C * sl / S), c1 = (int)((int64_t)C * (sl + 1) / S);
+    for (int cc = c0; cc < c1; cc += 16) {
+      if (VW == 4) {
+        i32x4 v[16];
 #pragma unroll
-    for (int d = 0; d < 4; ++d) {
-      v[2 * d] = dtype == KQ_DTYPE_BF16 ? bf16_to_f32(raw[d] & 0xffffu) : f16_to_f32(raw[d] & 0xffffu);
-      v[2 * d + 1] = dtype == KQ_DTYPE_BF16 ? bf16_to_f32(raw[d] >> 16) : f16_to_f32(raw[d] >> 16);
+        for (int u = 0; u < 16; ++u) v[u] = *(const i32x4*)(counts + (int64_t)min(cc + u, c1 - 1) * E + 4 * q);
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int x = cc + u < c1 ? v[u][i] : 0;
+            tot[i] += x;
+            pre[i] += cc + u < c ? x : 0;
+          }
+        }
+      } else {
+        int v[16];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) v[u] = counts[(int64_t)min(cc + u, c1 - 1) * E + q];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+          const int x = cc + u < c1 ? v[u] : 0;
+          tot[0] += x;
+          pre[0] += cc + u < c ? x : 0;
+        }
+      }
     }
+    for (int i = 0; i < VW; ++i) {
+      part_pre[sl * E + VW * q + i] = pre[i];
+      part_tot[sl * E + VW * q + i] = tot[i];
+    }
+  }
+  __syncthreads();
+  if (t < E) {
+    int before = 0, rows = 0;
+    for (int s2 = 0; s2 < S; ++s2) {
+      before += part_pre[s2 * E + t];
+      rows += part_tot[s2 * E + t];
+    }
+    sbase[t] = before;
+    srows[t] = rows;
+    soff[t] = rows;
+    sfirst[t] = (rows + BM - 1) / BM;
+  }
+  __syncthreads();
+  const int total_rows = block_exclusive_scan(soff, tmp, E);      // soff -> expert offsets
+  const int total_tiles = block_exclusive_scan(sfirst, tmp, E);   // sfirst -> first tile
+  if (t < E) sbase[t] += soff[t];
+  if (c == 0) {
+    if (t < E) offsets[t] = soff[t];
+    if (t == 0) offsets[E] = total_rows;
+    moe_write_tiles(sfirst, soff, srows, E, BM, total_tiles, max_tiles, tiles, tile_count);
+  }
+  __syncthreads();   // sbase complete
+  moe_scatter_chunk(idx, R, CR, E, top_k, c, sbase, whist, sorted_tok, inv);
+}
+
+// --------------------------------------------------- 1x128 activation quant
+// A quantization unit is kQuantRows consecutive rows x one 2048-element span
+// (256 threads x 8 elements, 16 threads per 1x128 block): the threads issue
+// the rows' 16-byte loads back to back, then quantize row by row.  (One row
+// per 256-thread workgroup left the C5 token pass latency-bound at 9 us.)
+constexpr int kQuantRows = 4;
+
+// Raw 16-bit elements of thread tx in span y of rows [row0, row0 +
+// kQuantRows) (rows past `rows` repeat the last row; elements past K read 0).
+KQ_DEV void aq_load_rows(const uint16_t* __restrict__ x, int K, int64_t ldx, bool vec, int64_t row0,
+                         int64_t rows, int y, int tx, u32x4 (&raw)[kQuantRows]) {
+  const int k0 = y * 2048 + tx * 8;
+  if (vec && k0 + 8 <= K) {
+#pragma unroll
+    for (int j = 0; j < kQuantRows; ++j) raw[j] = *(const u32x4*)(x + min(row0 + j, rows - 1) * ldx + k0);
   } else {
 #pragma unroll
-    for (int e = 0; e < 8; ++e)
-      v[e] = k0 + e < K ? (dtype == KQ_DTYPE_BF16 ? bf16_to_f32(xr[k0 + e]) : f16_to_f32(xr[k0 + e])) : 0.0f;
+    for (int j = 0; j < kQuantRows; ++j) {
+      const uint16_t* xr = x + min(row0 + j, rows - 1) * ldx;
+      uint32_t h[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) h[e] = k0 + e < K ? xr[k0 + e] : 0u;
+      raw[j] = u32x4{h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16)};
+    }
+  }
+}
+
+// 1x128 block scale of thread tx's 16-lane group (s = max(amax, 1e-12) /
+// 448), e4m3 values of its 8 elements, stored with the block's scale.
+KQ_DEV void aq_quant8(const u32x4 raw, int dtype, int K, uint8_t* __restrict__ xq, float* __restrict__ xs,
+                      int64_t row, int y, int tx) {
+  const int k0 = y * 2048 + tx * 8;
+  float v[8];
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    v[2 * d] = dtype == KQ_DTYPE_BF16 ? bf16_to_f32(raw[d] & 0xffffu) : f16_to_f32(raw[d] & 0xffffu);
+    v[2 * d + 1] = dtype == KQ_DTYPE_BF16 ? bf16_to_f32(raw[d] >> 16) : f16_to_f32(raw[d] >> 16);
   }
   // block amax as an integer max of |bits|: inf and NaN order above every
   // finite magnitude, so a NaN in the block makes the scale NaN (torch's amax
@@ -398,33 +557,97 @@ KQ_DEV void act_quant_fp8_blocks_span(const uint16_t* __restrict__ x, int dtype,
   } else {
     for (int e = 0; e < 8 && k0 + e < K; ++e) qr[k0 + e] = (uint8_t)(((e < 4 ? lo : hi) >> (8 * (e & 3))) & 0xffu);
   }
-  if ((threadIdx.x & 15) == 0) xs[row * ((K + 127) / 128) + k0 / 128] = s;
+  if ((tx & 15) == 0) xs[row * ((K + 127) / 128) + k0 / 128] = s;
 }
 
-// Grid (rows, ceil(K / 2048)); 256 threads x 8 elements; 16 threads per block.
+// Rows [row0, row0 + kQuantRows) of `rows`, span y, by the 256 threads tx =
+// 0..255 (whole waves; the row-count test is uniform over them).
+KQ_DEV void act_quant_fp8_blocks_unit(const uint16_t* __restrict__ x, int dtype, int K, int64_t ldx, bool vec,
+                                      int64_t row0, int64_t rows, int y, uint8_t* __restrict__ xq,
+                                      float* __restrict__ xs, int tx) {
+  u32x4 raw[kQuantRows];
+  aq_load_rows(x, K, ldx, vec, row0, rows, y, tx, raw);
+#pragma unroll
+  for (int j = 0; j < kQuantRows; ++j)
+    if (row0 + j < rows) aq_quant8(raw[j], dtype, K, xq, xs, row0 + j, y, tx);
+}
+
+// Grid (row groups, spans): blockIdx.y is the span, blockIdx.x strides over
+// groups of kQuantRows rows.
 __global__ void __launch_bounds__(256)
-act_quant_fp8_blocks_kernel(const uint16_t* __restrict__ x, int dtype, int K, int64_t ldx, bool vec,
+act_quant_fp8_blocks_kernel(const uint16_t* __restrict__ x, int dtype, int K, int64_t ldx, bool vec, int64_t rows,
                             uint8_t* __restrict__ xq, float* __restrict__ xs) {
-  act_quant_fp8_blocks_span(x, dtype, K, ldx, vec, xq, xs, blockIdx.x, blockIdx.y);
+  for (int64_t g = blockIdx.x; g * kQuantRows < rows; g += gridDim.x)
+    act_quant_fp8_blocks_unit(x, dtype, K, ldx, vec, g * kQuantRows, rows, (int)blockIdx.y, xq, xs, threadIdx.x);
 }
 
-// MoE: the chunk histograms (blocks [0, C)) and the token quantization
-// (blocks C + row * KY + y) in one launch; neither reads the other's output.
-static_assert(kSortChunk == 256, "a sort chunk and a quantization span both take 256 threads");
+// Quantization unit u of a MoE call's tokens: row group u / KY, span u % KY.
+KQ_DEV void moe_quant_unit(const uint16_t* __restrict__ x, int dtype, int K, bool vec, int KY, int u, int64_t rows,
+                           uint8_t* __restrict__ xq, float* __restrict__ xs, int tx) {
+  const int y = u % KY, g = u / KY;
+  act_quant_fp8_blocks_unit(x, dtype, K, K, vec, (int64_t)g * kQuantRows, rows, y, xq, xs, tx);
+}
+
+// MoE with the caller's routing: the chunk histograms (workgroups [0, C))
+// and the token quantization (one unit per workgroup after them) in one
+// launch; neither reads the other's output.
+static_assert(kSortChunk == 256, "a sort chunk and a quantization unit both take 256 threads");
 __global__ void __launch_bounds__(256)
-moe_count_quant_kernel(const int32_t* __restrict__ idx, int R, int E, int32_t* __restrict__ counts, int C,
-                       const uint16_t* __restrict__ x, int dtype, int K, int64_t ldx, bool vec, int KY,
+moe_count_quant_kernel(const int32_t* __restrict__ idx, int R, int CR, int E, int32_t* __restrict__ counts, int C,
+                       const uint16_t* __restrict__ x, int dtype, int K, bool vec, int KY, int64_t T,
                        uint8_t* __restrict__ xq, float* __restrict__ xs) {
   extern __shared__ int hist[];
   const int b = blockIdx.x;
-  if (b < C) {
-    moe_count_chunk(idx, R, E, counts, b, hist);
-  } else {
-    const int q = b - C;
-    act_quant_fp8_blocks_span(x, dtype, K, ldx, vec, xq, xs, q / KY, q % KY);
-  }
+  if (b < C) moe_count_chunk(idx, R, CR, E, counts, b, hist);
+  else moe_quant_unit(x, dtype, K, vec, KY, b - C, T, xq, xs, threadIdx.x);
 }
 
+// MoE from router logits, 1024-thread workgroups: workgroup c < C routes the
+// chunk's tokens (kSortChunk / k of them; wave w takes tokens w, w + 16, ...
+// two at a time, their selection chains interleaved), writes topk_idx /
+// topk_w and the chunk's expert histogram; each of the other workgroups
+// quantizes four token units (256 threads per unit).  Routing
+// needs many waves in flight: one chunk per 256-thread workgroup (8 tokens
+// per wave in turn) took 24.7 us where the one-token-per-wave routing kernel
+// takes 6 us for C5's 4096 tokens.
+constexpr int kRouteThreads = 1024;
+constexpr int kRouteWaves = kRouteThreads / 64;
+template <int PL>
+__global__ void __launch_bounds__(kRouteThreads)
+moe_route_count_quant_kernel(const void* __restrict__ logits, int ldtype, int T, int E, int k, int norm,
+                             int32_t* __restrict__ idx, float* __restrict__ w, int32_t* __restrict__ counts, int C,
+                             const uint16_t* __restrict__ x, int dtype, int K, bool vec, int KY, int units,
+                             uint8_t* __restrict__ xq, float* __restrict__ xs) {
+  extern __shared__ int hist[];   // E counters, then the chunk's expert ids (kSortChunk)
+  const int b = blockIdx.x;
+  if (b >= C) {
+    // four quantization units, one per 256 threads
+    const int u = (b - C) * (kRouteThreads / 256) + (int)(threadIdx.x >> 8);
+    if (u < units) moe_quant_unit(x, dtype, K, vec, KY, u, T, xq, xs, threadIdx.x & 255);
+    return;
+  }
+  int* sids = hist + E;
+  for (int i = threadIdx.x; i < E; i += kRouteThreads) hist[i] = 0;
+  const int TPC = kSortChunk / k;   // k <= kRouteMaxTopK
+  const int t0 = b * TPC, nt = min(TPC, T - t0);
+  const int wv = wave_id();
+  for (int i = wv; i < nt; i += 2 * kRouteWaves) {
+    const int i1 = min(i + kRouteWaves, nt - 1);
+    float v[2][PL];
+    route_load<PL>(logits, ldtype, t0 + i, E, v[0]);
+    route_load<PL>(logits, ldtype, t0 + i1, E, v[1]);
+    const int tt[2] = {t0 + i, t0 + i1};
+    const int live = i + kRouteWaves < nt ? 2 : 1;
+    route_tokens<PL, 2>(v, tt, live, E, k, norm, idx, w, sids + i * k, kRouteWaves * k);
+  }
+  __syncthreads();   // hist cleared, the chunk's ids in LDS
+  if ((int)threadIdx.x < nt * k) {
+    const int e = sids[threadIdx.x];
+    if (e >= 0 && e < E) atomicAdd(&hist[e], 1);
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < E; i += kRouteThreads) counts[(int64_t)b * E + i] = hist[i];
+}
 
 // ------------------------------------------------------------------ combine
 // out[t] = sum over slots s (in order) of fp32(y[inv[t*k+s]]) * w[t*k+s].
@@ -513,7 +736,8 @@ static size_t align256(size_t v) { return (v + 255) / 256 * 256; }
 
 static MoeWorkspace moe_layout(int64_t T, int64_t H, int64_t I, int64_t E, int64_t k) {
   const int64_t R = T * k;
-  const int64_t C = (R + kSortChunk - 1) / kSortChunk;
+  const int64_t CR = moe_chunk_rows((int)k);
+  const int64_t C = (R + CR - 1) / CR;
   const int64_t BM = 64 * moe_nrb(R, E);
   const int64_t max_tiles = (R + BM - 1) / BM + E;
   MoeWorkspace w{};
@@ -540,9 +764,130 @@ static bool quant_dtype_ok(int d) { return d == KQ_DTYPE_F16 || d == KQ_DTYPE_BF
 static void launch_act_quant_blocks(const void* x, int dtype, int64_t rows, int64_t K, int64_t ldx,
                                     uint8_t* xq, float* xs, hipStream_t st) {
   const bool vec = ((uintptr_t)x % 16) == 0 && (ldx % 8) == 0;
-  const dim3 grid((unsigned)rows, (unsigned)((K + 2047) / 2048));
-  hipLaunchKernelGGL(act_quant_fp8_blocks_kernel, grid, dim3(256), 0, st, (const uint16_t*)x, dtype,
-                     (int)K, ldx, vec, xq, xs);
+  const int64_t groups = (rows + kQuantRows - 1) / kQuantRows;
+  const dim3 grid((unsigned)std::min<int64_t>(groups, 1 << 20), (unsigned)((K + 2047) / 2048));
+  hipLaunchKernelGGL(act_quant_fp8_blocks_kernel, grid, dim3(256), 0, st, (const uint16_t*)x, dtype, (int)K, ldx,
+                     vec, rows, xq, xs);
+}
+
+// Shapes of one MoE call and its workspace pointers.
+struct MoeCall {
+  const void* hidden;
+  int dtype, top_k;
+  int64_t tokens, H, I, E;
+  int R, CR, C, nrb, BM, max_tiles, KY;
+  int units;            // token quantization units (kQuantRows rows x one 2048-element span)
+  bool vec;
+  int32_t *counts, *base, *offsets, *tiles, *tile_count, *sorted, *inv;
+  uint8_t *xq, *actq;
+  float *xs, *acts;
+  uint16_t* y;
+};
+
+static MoeCall moe_call(const void* hidden, int dtype, int64_t tokens, int64_t H, int64_t I, int64_t E,
+                        int top_k, void* workspace) {
+  const MoeWorkspace L = moe_layout(tokens, H, I, E, top_k);
+  uint8_t* ws = (uint8_t*)workspace;
+  MoeCall m{};
+  m.hidden = hidden; m.dtype = dtype; m.top_k = top_k;
+  m.tokens = tokens; m.H = H; m.I = I; m.E = E;
+  m.R = (int)(tokens * top_k);
+  m.CR = moe_chunk_rows(top_k);
+  m.C = (m.R + m.CR - 1) / m.CR;
+  m.nrb = moe_nrb(m.R, E);
+  m.BM = 64 * m.nrb;
+  m.max_tiles = (m.R + m.BM - 1) / m.BM + (int)E;
+  m.KY = (int)((H + 2047) / 2048);
+  m.units = (int)((tokens + kQuantRows - 1) / kQuantRows) * m.KY;
+  m.vec = ((uintptr_t)hidden % 16) == 0 && (H % 8) == 0;
+  m.counts = (int32_t*)(ws + L.counts);
+  m.base = (int32_t*)(ws + L.base);
+  m.offsets = (int32_t*)(ws + L.offsets);
+  m.tiles = (int32_t*)(ws + L.tiles);
+  m.tile_count = (int32_t*)(ws + L.tile_count);
+  m.sorted = (int32_t*)(ws + L.sorted);
+  m.inv = (int32_t*)(ws + L.inv);
+  m.xq = ws + L.xq;
+  m.xs = (float*)(ws + L.xs);
+  m.actq = ws + L.actq;
+  m.acts = (float*)(ws + L.acts);
+  m.y = (uint16_t*)(ws + L.y);
+  return m;
+}
+
+// After the chunk histograms and the token quantization: the stable sort's
+// scan and scatter (one launch when the histogram table is small, else the
+// one-workgroup scan and the scatter), both grouped GEMMs and the combine.
+static void moe_sort_experts_combine(const MoeCall& m, const int32_t* topk_idx, const float* topk_w,
+                                     const uint8_t* w13, const float* s13, const uint8_t* w2,
+                                     const float* s2, void* out, hipStream_t st) {
+  const int E = (int)m.E;
+  if (E <= kSortChunk && (int64_t)m.C * E <= kFusedScanMax) {
+    hipLaunchKernelGGL(moe_scan_scatter_kernel, dim3(m.C), dim3(kSortChunk), 0, st, topk_idx, m.R, m.CR, E,
+                       m.top_k, m.counts, m.C, m.BM, m.max_tiles, m.offsets, m.tiles, m.tile_count, m.sorted,
+                       m.inv);
+  } else {
+    const int scan_per = (m.C + moe_scan_slices(E) - 1) / moe_scan_slices(E);
+    if (scan_per <= 16)
+      hipLaunchKernelGGL(moe_scan_kernel<16>, dim3(1), dim3(1024), 0, st, m.counts, m.C, E, m.BM, m.max_tiles,
+                         m.offsets, m.base, m.tiles, m.tile_count);
+    else if (scan_per <= 64)
+      hipLaunchKernelGGL(moe_scan_kernel<64>, dim3(1), dim3(1024), 0, st, m.counts, m.C, E, m.BM, m.max_tiles,
+                         m.offsets, m.base, m.tiles, m.tile_count);
+    else
+      hipLaunchKernelGGL(moe_scan_kernel<0>, dim3(1), dim3(1024), 0, st, m.counts, m.C, E, m.BM, m.max_tiles,
+                         m.offsets, m.base, m.tiles, m.tile_count);
+    hipLaunchKernelGGL(moe_scatter_kernel, dim3(m.C), dim3(kSortChunk), (kSortChunk / 64) * E * sizeof(int), st,
+                       topk_idx, m.R, m.CR, E, m.top_k, m.base, m.sorted, m.inv);
+  }
+
+  TileGemmArgs g{};
+  g.x = m.xq; g.xs = m.xs; g.x_rows = (int)m.tokens; g.gather = m.sorted; g.gather_rows = m.R;
+  g.w = w13; g.ws = s13; g.mtile_table = m.tiles; g.mtile_count = m.tile_count;
+  g.N = (int)(2 * m.I); g.K = (int)m.H; g.I = (int)m.I;
+  g.mtiles = m.max_tiles; g.ntiles = (int)(m.I / 128);
+  g.actq = m.actq; g.acts = m.acts; g.out_dtype = m.dtype; g.bias_dtype = KQ_DTYPE_NONE;
+  if (m.nrb == 5) tg_launch<kTgFp8, true, kTgEpiSwiGluQuant, 5>(g, st);
+  else tg_launch<kTgFp8, true, kTgEpiSwiGluQuant, 4>(g, st);
+
+  TileGemmArgs d{};
+  d.x = m.actq; d.xs = m.acts; d.x_rows = m.R; d.gather = nullptr;
+  d.w = w2; d.ws = s2; d.mtile_table = m.tiles; d.mtile_count = m.tile_count;
+  d.N = (int)m.H; d.K = (int)m.I; d.I = 0;
+  d.mtiles = m.max_tiles; d.ntiles = (int)((m.H + kTgBN - 1) / kTgBN);
+  d.out = m.y; d.out_dtype = m.dtype; d.bias = nullptr; d.bias_dtype = KQ_DTYPE_NONE;
+  if (m.nrb == 5) tg_launch<kTgFp8, true, kTgEpiStore, 5>(d, st);
+  else tg_launch<kTgFp8, true, kTgEpiStore, 4>(d, st);
+
+  hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)m.tokens), dim3(256), 0, st, m.y, m.dtype, m.inv, topk_w,
+                     m.top_k, (int)m.H, (uint16_t*)out);
+}
+
+// Shape checks shared by both MoE entry points; 0 or an error code.
+static int moe_check_shape(const char* name, int dtype, int64_t tokens, int64_t hidden_size, int64_t inter,
+                           int64_t experts, int top_k, void* workspace, size_t workspace_bytes) {
+  if (!quant_dtype_ok(dtype)) {
+    set_error("%s: hidden dtype must be fp16 or bf16", name);
+    return KQ_EUNSUPPORTED;
+  }
+  if (tokens < 0 || hidden_size < kTgBK || (hidden_size % kTgBK) != 0 || inter < kTgBK ||
+      (inter % kTgBK) != 0 || experts < 1 || experts > 1024 || top_k < 1 || top_k > experts ||
+      hidden_size > kTgBK * kTgMaxKB || inter > kTgBK * kTgMaxKB || tokens * top_k > 0x7fffffffLL ||
+      hidden_size * 2 * inter > 0x7fffffffLL || tokens * hidden_size > 0x7fffffffLL ||
+      tokens * top_k * inter > 0x7fffffffLL) {
+    set_error("%s: bad shape tokens=%lld hidden=%lld inter=%lld experts=%lld top_k=%d (hidden and inter "
+              "must be multiples of 128)",
+              name, (long long)tokens, (long long)hidden_size, (long long)inter, (long long)experts, top_k);
+    return KQ_EINVAL;
+  }
+  if (tokens == 0) return KQ_OK;
+  const MoeWorkspace L = moe_layout(tokens, hidden_size, inter, experts, top_k);
+  if (workspace == nullptr || workspace_bytes < L.total) {
+    set_error("%s: workspace of %zu bytes is smaller than the %zu bytes this call needs", name,
+              workspace ? workspace_bytes : (size_t)0, L.total);
+    return KQ_EWORKSPACE;
+  }
+  return KQ_OK;
 }
 
 }  // namespace kq
@@ -584,8 +929,9 @@ extern "C" int kq_act_quant_fp8_blocks(const void* x, int x_dtype, int64_t rows,
     set_error("kq_act_quant_fp8_blocks: activation dtype must be fp16 or bf16");
     return KQ_EUNSUPPORTED;
   }
-  if (rows < 0 || k < 1 || ldx < k || rows > 0x7fffffffLL || k > 0x7fffffffLL) {
-    set_error("kq_act_quant_fp8_blocks: bad shape rows=%lld k=%lld", (long long)rows, (long long)k);
+  if (rows < 0 || k < 1 || ldx < k || rows > 0x7fffffffLL || k > 65535LL * 2048) {
+    set_error("kq_act_quant_fp8_blocks: bad shape rows=%lld k=%lld (k <= 65535 * 2048)", (long long)rows,
+              (long long)k);
     return KQ_EINVAL;
   }
   if (rows == 0) return KQ_OK;
@@ -630,88 +976,60 @@ extern "C" int kq_moe_block_fp8_experts(const void* hidden, int dtype, int64_t t
                                         const uint8_t* w13, const float* s13, const uint8_t* w2,
                                         const float* s2, void* out, void* workspace,
                                         size_t workspace_bytes, void* stream) {
-  if (!quant_dtype_ok(dtype)) {
-    set_error("kq_moe_block_fp8_experts: hidden dtype must be fp16 or bf16");
+  const int bad = moe_check_shape("kq_moe_block_fp8_experts", dtype, tokens, hidden_size, inter, experts,
+                                  top_k, workspace, workspace_bytes);
+  if (bad != KQ_OK || tokens == 0) return bad;
+  hipStream_t st = (hipStream_t)stream;
+  const MoeCall m = moe_call(hidden, dtype, tokens, hidden_size, inter, experts, top_k, workspace);
+  // chunk histograms and the token quantization share one launch
+  const int64_t blocks = (int64_t)m.C + m.units;
+  hipLaunchKernelGGL(moe_count_quant_kernel, dim3((unsigned)blocks), dim3(kSortChunk), m.E * sizeof(int), st,
+                     topk_idx, m.R, m.CR, (int)m.E, m.counts, m.C, (const uint16_t*)hidden, dtype, (int)m.H, m.vec,
+                     m.KY, m.tokens, m.xq, m.xs);
+  moe_sort_experts_combine(m, topk_idx, topk_w, w13, s13, w2, s2, out, st);
+  return check_launch("kq_moe_block_fp8_experts");
+}
+
+extern "C" int kq_moe_routed_block_fp8_experts(const void* logits, int logits_dtype, int norm_topk_prob,
+                                               const void* hidden, int dtype, int64_t tokens,
+                                               int64_t hidden_size, int64_t inter, int64_t experts,
+                                               int top_k, const uint8_t* w13, const float* s13,
+                                               const uint8_t* w2, const float* s2, int32_t* topk_idx,
+                                               float* topk_w, void* out, void* workspace,
+                                               size_t workspace_bytes, void* stream) {
+  if (logits_dtype != KQ_DTYPE_F16 && logits_dtype != KQ_DTYPE_BF16 && logits_dtype != KQ_DTYPE_F32) {
+    set_error("kq_moe_routed_block_fp8_experts: logits must be fp16, bf16 or fp32");
     return KQ_EUNSUPPORTED;
   }
-  if (tokens < 0 || hidden_size < kTgBK || (hidden_size % kTgBK) != 0 || inter < kTgBK ||
-      (inter % kTgBK) != 0 || experts < 1 || experts > 1024 || top_k < 1 || top_k > experts ||
-      hidden_size > kTgBK * kTgMaxKB || inter > kTgBK * kTgMaxKB || tokens * top_k > 0x7fffffffLL ||
-      hidden_size * 2 * inter > 0x7fffffffLL || tokens * hidden_size > 0x7fffffffLL ||
-      tokens * top_k * inter > 0x7fffffffLL) {
-    set_error("kq_moe_block_fp8_experts: bad shape tokens=%lld hidden=%lld inter=%lld experts=%lld "
-              "top_k=%d (hidden and inter must be multiples of 128)",
-              (long long)tokens, (long long)hidden_size, (long long)inter, (long long)experts, top_k);
+  if (experts > 64 * kRouteMaxPerLane || top_k > kRouteMaxTopK || tokens > 0x7fffffffLL / 64) {
+    set_error("kq_moe_routed_block_fp8_experts: routing supports experts <= %d and top_k <= %d "
+              "(experts=%lld top_k=%d)", 64 * kRouteMaxPerLane, kRouteMaxTopK, (long long)experts, top_k);
     return KQ_EINVAL;
   }
-  if (tokens == 0) return KQ_OK;
-  const MoeWorkspace L = moe_layout(tokens, hidden_size, inter, experts, top_k);
-  if (workspace == nullptr || workspace_bytes < L.total) {
-    set_error("kq_moe_block_fp8_experts: workspace of %zu bytes is smaller than the %zu bytes "
-              "this call needs", workspace ? workspace_bytes : (size_t)0, L.total);
-    return KQ_EWORKSPACE;
+  const int bad = moe_check_shape("kq_moe_routed_block_fp8_experts", dtype, tokens, hidden_size, inter, experts,
+                                  top_k, workspace, workspace_bytes);
+  if (bad != KQ_OK || tokens == 0) return bad;
+  if (logits == nullptr || topk_idx == nullptr || topk_w == nullptr) {
+    set_error("kq_moe_routed_block_fp8_experts: logits, topk_idx and topk_w are required");
+    return KQ_EINVAL;
   }
   hipStream_t st = (hipStream_t)stream;
-  uint8_t* ws = (uint8_t*)workspace;
-  int32_t* counts = (int32_t*)(ws + L.counts);
-  int32_t* base = (int32_t*)(ws + L.base);
-  int32_t* offsets = (int32_t*)(ws + L.offsets);
-  int32_t* tiles = (int32_t*)(ws + L.tiles);
-  int32_t* tile_count = (int32_t*)(ws + L.tile_count);
-  int32_t* sorted = (int32_t*)(ws + L.sorted);
-  int32_t* inv = (int32_t*)(ws + L.inv);
-  uint8_t* xq = ws + L.xq;
-  float* xs = (float*)(ws + L.xs);
-  uint8_t* actq = ws + L.actq;
-  float* acts = (float*)(ws + L.acts);
-  uint16_t* y = (uint16_t*)(ws + L.y);
-  const int R = (int)(tokens * top_k);
-  const int C = (R + kSortChunk - 1) / kSortChunk;
-  const int E = (int)experts;
-  const int nrb = moe_nrb(R, E), BM = 64 * nrb;
-  const int max_tiles = (R + BM - 1) / BM + E;
-
-  // chunk histograms and the token quantization share one launch
-  {
-    const int KY = (int)((hidden_size + 2047) / 2048);
-    const bool vec = ((uintptr_t)hidden % 16) == 0 && (hidden_size % 8) == 0;
-    const int64_t blocks = (int64_t)C + tokens * KY;
-    hipLaunchKernelGGL(moe_count_quant_kernel, dim3((unsigned)blocks), dim3(kSortChunk), E * sizeof(int), st,
-                       topk_idx, R, E, counts, C, (const uint16_t*)hidden, dtype, (int)hidden_size,
-                       (int64_t)hidden_size, vec, KY, xq, xs);
-  }
-  const int scan_per = (C + moe_scan_slices(E) - 1) / moe_scan_slices(E);
-  if (scan_per <= 16)
-    hipLaunchKernelGGL(moe_scan_kernel<16>, dim3(1), dim3(1024), 0, st, counts, C, E, BM, max_tiles,
-                       offsets, base, tiles, tile_count);
-  else if (scan_per <= 64)
-    hipLaunchKernelGGL(moe_scan_kernel<64>, dim3(1), dim3(1024), 0, st, counts, C, E, BM, max_tiles,
-                       offsets, base, tiles, tile_count);
-  else
-    hipLaunchKernelGGL(moe_scan_kernel<0>, dim3(1), dim3(1024), 0, st, counts, C, E, BM, max_tiles,
-                       offsets, base, tiles, tile_count);
-  hipLaunchKernelGGL(moe_scatter_kernel, dim3(C), dim3(kSortChunk), (kSortChunk / 64) * E * sizeof(int), st,
-                     topk_idx, R, E, top_k, base, sorted, inv);
-
-  TileGemmArgs g{};
-  g.x = xq; g.xs = xs; g.x_rows = (int)tokens; g.gather = sorted; g.gather_rows = R;
-  g.w = w13; g.ws = s13; g.mtile_table = tiles; g.mtile_count = tile_count;
-  g.N = (int)(2 * inter); g.K = (int)hidden_size; g.I = (int)inter;
-  g.mtiles = max_tiles; g.ntiles = (int)(inter / 128);
-  g.actq = actq; g.acts = acts; g.out_dtype = dtype; g.bias_dtype = KQ_DTYPE_NONE;
-  if (nrb == 5) tg_launch<kTgFp8, true, kTgEpiSwiGluQuant, 5>(g, st);
-  else tg_launch<kTgFp8, true, kTgEpiSwiGluQuant, 4>(g, st);
-
-  TileGemmArgs d{};
-  d.x = actq; d.xs = acts; d.x_rows = R; d.gather = nullptr;
-  d.w = w2; d.ws = s2; d.mtile_table = tiles; d.mtile_count = tile_count;
-  d.N = (int)hidden_size; d.K = (int)inter; d.I = 0;
-  d.mtiles = max_tiles; d.ntiles = (int)((hidden_size + kTgBN - 1) / kTgBN);
-  d.out = y; d.out_dtype = dtype; d.bias = nullptr; d.bias_dtype = KQ_DTYPE_NONE;
-  if (nrb == 5) tg_launch<kTgFp8, true, kTgEpiStore, 5>(d, st);
-  else tg_launch<kTgFp8, true, kTgEpiStore, 4>(d, st);
-
-  hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)tokens), dim3(256), 0, st, y, dtype, inv, topk_w,
-                     top_k, (int)hidden_size, (uint16_t*)out);
-  return check_launch("kq_moe_block_fp8_experts");
+  const MoeCall m = moe_call(hidden, dtype, tokens, hidden_size, inter, experts, top_k, workspace);
+  // routing, the chunk histograms and the token quantization in one launch
+  const int64_t per_block = kRouteThreads / 256;
+  const int64_t blocks = (int64_t)m.C + (m.units + per_block - 1) / per_block;
+  const size_t lds = (size_t)(m.E + kSortChunk) * sizeof(int);
+  const int T = (int)tokens, E = (int)experts, norm = norm_topk_prob ? 1 : 0;
+  const dim3 grid((unsigned)blocks), block(kRouteThreads);
+#define KQ_ROUTE_LAUNCH(PL)                                                                                    \
+  hipLaunchKernelGGL(moe_route_count_quant_kernel<PL>, grid, block, lds, st, logits, logits_dtype, T, E, top_k, \
+                     norm, topk_idx, topk_w, m.counts, m.C, (const uint16_t*)hidden, dtype, (int)m.H, m.vec,    \
+                     m.KY, m.units, m.xq, m.xs)
+  if (E <= 64) KQ_ROUTE_LAUNCH(1);
+  else if (E <= 128) KQ_ROUTE_LAUNCH(2);
+  else if (E <= 256) KQ_ROUTE_LAUNCH(4);
+  else KQ_ROUTE_LAUNCH(kRouteMaxPerLane);
+#undef KQ_ROUTE_LAUNCH
+  moe_sort_experts_combine(m, topk_idx, topk_w, w13, s13, w2, s2, out, st);
+  return check_launch("kq_moe_routed_block_fp8_experts");
 }

@@ -11,9 +11,11 @@ On a gfx950 device the whole expert path is one C call
 (``kq_moe_block_fp8_experts``): device-side stable sort of the routed rows by
 expert, per-token activation quantization, grouped GEMM gate_up with a fused
 SwiGLU + 1x128 quantization epilogue, grouped GEMM down, and the fp32
-slot-order combine (moe_parallel.py:255-283).  Routing is
-``kq_moe_route_topk``.  Nothing synchronizes with the host, so a block can be
-captured in a HIP graph.  On the CPU the reference's own loop semantics run
+slot-order combine (moe_parallel.py:255-283).  Routing alone is
+``kq_moe_route_topk``; the block's forward routes inside the same call
+(``kq_moe_routed_block_fp8_experts``), where the routing, the sort's expert
+histograms and the token quantization share one launch.  Nothing
+synchronizes with the host, so a block can be captured in a HIP graph.  On the CPU the reference's own loop semantics run
 (``forward_reference`` of each projection, ``index_add_`` combine).
 """
 
@@ -265,6 +267,43 @@ class GroupedBlockFp8Experts:
         )
         return out
 
+    def forward_logits(self, hidden: torch.Tensor, logits: torch.Tensor, top_k: int,
+                       norm_topk_prob: bool = True
+                       ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+        """Routing from ``logits [T, E]`` and the routed experts in one library
+        call (``kq_moe_routed_block_fp8_experts``): the same outputs, bit for
+        bit, as :func:`route_logits` followed by :meth:`forward`.  Returns
+        ``(out, topk_indices int32 [T, k], topk_weights fp32 [T, k])``."""
+
+        if not self.supports(hidden):
+            raise RuntimeError("block-FP8 grouped experts need fp16/bf16 device rows of the packed width")
+        if logits.ndim != 2 or logits.shape[0] != hidden.shape[0]:
+            raise ValueError("router logits must be [tokens, experts] with one row per token")
+        experts = self.w13.shape[0]
+        if logits.shape[1] != experts:
+            raise ValueError(f"router logits have {logits.shape[1]} experts, the pack {experts}")
+        if logits.device != hidden.device:
+            raise ValueError("router logits must be on the hidden states' device")
+        hidden = hidden.contiguous()
+        logits = logits.contiguous()
+        tokens = hidden.shape[0]
+        indices = torch.empty((tokens, top_k), device=hidden.device, dtype=torch.int32)
+        weights = torch.empty((tokens, top_k), device=hidden.device, dtype=torch.float32)
+        out = torch.empty_like(hidden)
+        if tokens == 0:
+            return out, indices, weights
+        need = int(_native.library().kq_moe_workspace_size(tokens, self.hidden, self.inter,
+                                                            experts, top_k))
+        ws = _native.workspace(hidden.device, need)
+        _native.call(
+            "kq_moe_routed_block_fp8_experts", logits.data_ptr(), _native.dtype_code(logits.dtype),
+            int(bool(norm_topk_prob)), hidden.data_ptr(), _native.dtype_code(hidden.dtype), tokens,
+            self.hidden, self.inter, experts, top_k, self.w13.data_ptr(), self.s13.data_ptr(),
+            self.w2.data_ptr(), self.s2.data_ptr(), indices.data_ptr(), weights.data_ptr(),
+            out.data_ptr(), ws.data_ptr(), ws.numel(), _native.stream_handle(hidden.device),
+        )
+        return out, indices, weights
+
 
 # ------------------------------------------------------------------- mixing
 def mix_experts(hidden, experts, topk_indices, topk_weights, grouped=None) -> torch.Tensor:
@@ -334,8 +373,8 @@ class Qwen3BlockFp8MoeBlock(nn.Module):
         flat = hidden.reshape(-1, shape[-1])
         grouped = getattr(self, "_grouped_experts", None)
         if flat.is_cuda and grouped is not None and grouped.supports(flat):
-            indices, weights = _route(self.gate(flat), self.top_k, self.norm_topk_prob)
-            return grouped.forward(flat, indices, weights).reshape(shape)
+            out, _, _ = grouped.forward_logits(flat, self.gate(flat), self.top_k, self.norm_topk_prob)
+            return out.reshape(shape)
         indices, weights = route_experts(self, flat)
         return mix_experts(flat, self.experts, indices, weights).reshape(shape)
 

@@ -199,9 +199,9 @@ class MoeFromLogits(torch.nn.Module):
     def forward(self, hidden: torch.Tensor) -> torch.Tensor:
         from kairyu_amd import moe
 
-        indices, weights = moe._route(self.logits, self.top_k, self.norm_topk_prob)
         pack = moe.GroupedBlockFp8Experts.from_tensors(self.w13, self.s13, self.w2, self.s2)
-        return pack.forward(hidden, indices, weights)
+        out, _, _ = pack.forward_logits(hidden, self.logits, self.top_k, self.norm_topk_prob)
+        return out
 
 
 def moe_layer(tokens: int = 4096, hidden: int = 2048, inter: int = 768, experts: int = 128,

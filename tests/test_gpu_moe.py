@@ -203,6 +203,70 @@ def test_sort_scan_forms_match_oracle(cuda, tokens, top_k, experts):
                      **_NARROW)
 
 
+@pytest.mark.parametrize("tokens,hidden,inter,experts,top_k,ldtype,norm", [
+    (333, 256, 128, 60, 6, torch.float32, True),     # 42 tokens (252 rows) per sort chunk
+    (100, 128, 256, 4, 1, torch.bfloat16, False),    # top-1: 256 tokens per chunk, full softmax
+    (257, 256, 128, 200, 8, torch.float16, True),    # 4 logits per lane, a one-token last chunk
+    (64, 128, 128, 512, 8, torch.float32, False),    # 8 logits per lane; E > 256: the two-launch scan
+    (9000, 128, 128, 128, 8, torch.float32, True),   # 282 chunks x 128 experts: past the one-launch scan
+    (1, 128, 128, 8, 2, torch.bfloat16, True),
+    (40, 128, 128, 64, 40, torch.float32, True),     # top_k > 32 is the routing's limit: rejected
+])
+def test_routed_call_matches_route_then_experts(cuda, tokens, hidden, inter, experts, top_k, ldtype, norm):
+    """kq_moe_routed_block_fp8_experts (routing, histograms and token
+    quantization in one launch; scan and scatter in one launch where the
+    histogram table is small) against kq_moe_route_topk followed by
+    kq_moe_block_fp8_experts: indices, weights and outputs equal bit for bit
+    (the latter pair is checked against the oracle by the tests above), for
+    every logits-per-lane form, chunk geometry and both scan forms."""
+    banner(f"moe routed call tokens={tokens} E={experts} k={top_k} {ldtype} norm={norm}")
+    pack = _pack(experts, hidden, inter, seed=tokens + experts, device=cuda)
+    g = torch.Generator().manual_seed(tokens * 3 + top_k)
+    x = torch.randn(tokens, hidden, generator=g).to(torch.bfloat16).to(cuda)
+    logits = torch.randn(tokens, experts, generator=g)
+    logits[::5] = torch.round(logits[::5] * 2) / 2  # exact ties
+    logits = logits.to(ldtype).to(cuda)
+    if top_k > 32:
+        with pytest.raises(ValueError, match="top_k <= 32"):
+            pack.forward_logits(x, logits, top_k, norm)
+        return
+    idx, w = hmoe._route(logits, top_k, norm)
+    expected = pack.forward(x, idx, w)
+    out, idx2, w2 = pack.forward_logits(x, logits, top_k, norm)
+    assert torch.equal(idx2, idx)
+    assert torch.equal(w2.view(torch.int32), w.view(torch.int32))
+    assert torch.equal(out.view(torch.int16), expected.view(torch.int16))
+
+
+def test_routed_call_graph_replays_match_eager(cuda):
+    """The one-call block forward captured in a HIP graph: every replay (with
+    eager calls of the same function between them) gives the eager bits."""
+    pack = _pack(16, 256, 128, seed=7, device=cuda)
+    g = torch.Generator().manual_seed(8)
+    x = torch.randn(300, 256, generator=g).to(torch.bfloat16).to(cuda)
+    logits = torch.randn(300, 16, generator=g).to(cuda)
+
+    def step():
+        return pack.forward_logits(x, logits, 4, True)[0]
+
+    eager = step().clone()
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        step()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = step()
+    for i in range(4):
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), i
+        step()
+        torch.cuda.synchronize()
+
+
 def test_row_tile_heights_agree_bit_for_bit(cuda):
     """1500 tokens x top-4 over 16 experts average 375 rows per expert, so the
     whole call runs 320-row tiles (several per expert, with tails); 128-token
@@ -265,7 +329,10 @@ def test_block_module_uses_grouped_path_and_matches_oracle(cuda):
         assert pack is not None and pack.w13.is_cuda
         gpu_out = block(x.to(cuda))
         idx, w = hmoe.route_logits(block.gate(x.to(cuda).reshape(-1, 256)), 2)
+        two_calls = pack.forward(x.to(cuda).reshape(-1, 256), idx, w)
     assert gpu_out.shape == x.shape
+    # the block routes inside the experts call: the same bits as route + experts
+    assert torch.equal(gpu_out.reshape(-1, 256), two_calls)
     expected = _oracle_moe(pack, x.reshape(-1, 256), idx.cpu().numpy(), w.cpu().numpy())
     assert_moe_close(np32(gpu_out).reshape(-1, 256), expected, "bfloat16", label="block module", **_NARROW)
 
