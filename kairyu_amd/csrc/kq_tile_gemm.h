@@ -122,14 +122,21 @@ KQ_DEV int tg_chunk(int r, int c) {
   else return c ^ ((r >> 1) & 7);
 }
 
-// Output staging rows of 128 bytes (the epilogues): 16-byte chunk c of row r
-// at c ^ ((r >> 1) & 7).  A row covers half of the 64 four-byte banks, so the
-// 16 rows an epilogue write spans (lanes 16 apart: one row each) need row
-// parity and chunk to differ between any two of them; with c ^ (r & 7) rows r
-// and r + 8 met on the same banks (a two-way conflict on every staging
-// write).  The read-back (8 lanes per row, two rows per 16 lanes) is
-// conflict-free under any per-row permutation.
-KQ_DEV int tg_stage_chunk(int r, int c) { return c ^ ((r >> 1) & 7); }
+// Output staging rows of 128 bytes (the epilogues): unit u of row r at unit
+// u ^ (r & 15) (8-byte units) or u ^ ((r & 15) << 1) (4-byte units).  The
+// 16 consecutive lanes of an epilogue write hold the same unit of 16 rows;
+// XOR-ing by the row puts them on 16 distinct units, i.e. all 32 four-byte
+// banks of a 128-byte bank row.  (A permutation of 16-byte chunks leaves the
+// 16 lanes on 8 chunks at one half-chunk offset: a two-way conflict on every
+// staging write, 0.46 of the MoE down GEMM's LDS-active cycles.)  The
+// read-back takes row r's 16-byte chunk c from chunk c ^ ((r & 15) >> 1),
+// whose two 8-byte halves are swapped when r is odd.
+KQ_DEV int tg_stage_off8(int r, int u) { return r * 128 + ((u ^ (r & 15)) << 3); }
+KQ_DEV int tg_stage_off4(int r, int u) { return r * 128 + ((u ^ ((r & 15) << 1)) << 2); }
+KQ_DEV i32x4 tg_stage_read(const uint8_t* stg, int r, int c) {
+  const i32x4 v = *(const i32x4*)(stg + r * 128 + ((c ^ ((r & 15) >> 1)) << 4));
+  return (r & 1) ? i32x4{v[2], v[3], v[0], v[1]} : v;
+}
 
 // Global -> LDS copies of 16 / 4 bytes per lane (buffer_load ... lds): lane i
 // of the wave writes at LDS byte address lds + i * size; `lds` is wave-uniform
@@ -584,7 +591,7 @@ tile_gemm_kernel(TileGemmArgs a) {
         __syncthreads();
         const int IB = a.I / 128;
         // the tile's BM x 128 e4m3 block goes through the idle pipeline stage
-        // (row r at r*128, 16-byte chunk c at tg_stage_chunk(r, c)) so that the global
+        // (row r at r*128, 4-byte units permuted by tg_stage_off4) so that the global
         // stores below write whole 128-byte rows
         uint8_t* stg = smem + L::X + (st ^ 1) * (BM * kTgBK);
   #pragma unroll
@@ -601,7 +608,7 @@ tile_gemm_kernel(TileGemmArgs a) {
               v[q] = fminf(fmaxf(div_by_recip((q & 1) ? tg_hi(pv[j][mb][q >> 1], ODT) : tg_lo(pv[j][mb][q >> 1], ODT), s, rs),
                                  -448.0f), 448.0f);
             const int col = 64 * wn + 16 * j + 4 * lg;
-            *(uint32_t*)(stg + lrow * 128 + (tg_stage_chunk(lrow, col >> 4) << 4) + (col & 15)) =
+            *(uint32_t*)(stg + tg_stage_off4(lrow, col >> 2)) =
                 pack4_e4m3(v[0], v[1], v[2], v[3]);
           }
           if (wn == 0 && lg == 0 && row0 + lrow < row_end) a.acts[(int64_t)(row0 + lrow) * IB + ntile] = s;
@@ -612,7 +619,7 @@ tile_gemm_kernel(TileGemmArgs a) {
           const int r = 64 * i + (tid >> 3), c = tid & 7;
           if (row0 + r < row_end)
             *(i32x4*)(a.actq + (int64_t)(row0 + r) * a.I + ntile * 128 + c * 16) =
-                *(const i32x4*)(stg + r * 128 + (tg_stage_chunk(r, c) << 4));
+                tg_stage_read(stg, r, c);
         }
       } else if constexpr (EPI == kTgEpiSwiGluStore) {
         // gate and up of activation column 64 * wn + 16 * j + 4 * lg + q
@@ -676,7 +683,7 @@ tile_gemm_kernel(TileGemmArgs a) {
         const float* eX = (const float*)(smem + L::Epi) + buf * 3 * 256;
         // each wave's output rows go through its 8 KB of the idle pipeline
         // stage in passes of up to four row blocks by 64 columns ([m][64
-        // columns], 16-byte chunk c of row m at tg_stage_chunk(m, c)), so every global
+        // columns], 8-byte units permuted by tg_stage_off8), so every global
         // store writes whole 128-byte row segments; rows of 8-aligned N only
         // (others store directly)
         uint8_t* stg = smem + (wave < 4 ? L::W : L::X) + (st ^ 1) * (wave < 4 ? kTgBN * kTgBK : BM * kTgBK) +
@@ -713,7 +720,7 @@ tile_gemm_kernel(TileGemmArgs a) {
                                        (uint16_t)(word[1] >> 16)};
                 if (staged) {
                   const int cb = 32 * jj + 8 * lg;  // byte column within the 128-byte row
-                  *(u32x2*)(stg + ml * 128 + (tg_stage_chunk(ml, cb >> 4) << 4) + (cb & 15)) = word;
+                  *(u32x2*)(stg + tg_stage_off8(ml, cb >> 3)) = word;
                 } else if (grow < row_end) {
                   uint16_t* dst = (uint16_t*)a.out + (int64_t)grow * a.N + n;
   #pragma unroll
@@ -738,7 +745,7 @@ tile_gemm_kernel(TileGemmArgs a) {
                 const int ml = 8 * i + (ln >> 3), c = ln & 7;
                 const int grow = row0 + 16 * (4 * (mg + (ml >> 4)) + wm) + (ml & 15);
                 const int n = ntile * kTgBN + 128 * wn + 64 * half + 8 * c;
-                const i32x4 v = *(const i32x4*)(stg + ml * 128 + (tg_stage_chunk(ml, c) << 4));
+                const i32x4 v = tg_stage_read(stg, ml, c);
                 if (grow < row_end && n < a.N) *(i32x4*)((uint16_t*)a.out + (int64_t)grow * a.N + n) = v;
               }
             }
