@@ -603,21 +603,34 @@ moe_count_quant_kernel(const int32_t* __restrict__ idx, int R, int CR, int E, in
 }
 
 // MoE from router logits, 1024-thread workgroups: workgroup c < C routes the
-// chunk's tokens (kSortChunk / k of them; wave w takes tokens w, w + 16, ...
-// two at a time, their selection chains interleaved), writes topk_idx /
-// topk_w and the chunk's expert histogram; each of the other workgroups
-// quantizes four token units (256 threads per unit).  Routing
-// needs many waves in flight: one chunk per 256-thread workgroup (8 tokens
-// per wave in turn) took 24.7 us where the one-token-per-wave routing kernel
-// takes 6 us for C5's 4096 tokens.
+// chunk's TPC tokens, writes topk_idx / topk_w and the chunk's expert
+// histogram; each of the other workgroups quantizes four token units (256
+// threads per unit).  TPC <= 16: one token per wave; more: wave w takes
+// tokens w, w + 16, ... two at a time, their selection chains interleaved.
+// Routing needs many waves in flight: one chunk per 256-thread workgroup (8
+// tokens per wave in turn) took 24.7 us for C5's 4096 tokens, 32-token chunks
+// (2 per wave) 15.4 us, where the one-token-per-wave routing kernel takes
+// 6 us.
 constexpr int kRouteThreads = 1024;
 constexpr int kRouteWaves = kRouteThreads / 64;
+
+// Tokens per sort chunk of the routed call: one per route wave where the
+// chunk table still fits the one-launch scan (and a chunk holds at most
+// kSortChunk rows), else kSortChunk / k.
+static inline int moe_routed_chunk_tokens(int64_t T, int k, int64_t E) {
+  const int full = kSortChunk / k;  // k <= kRouteMaxTopK
+  if (full > kRouteWaves && E <= kSortChunk && (T + kRouteWaves - 1) / kRouteWaves * E <= kFusedScanMax)
+    return kRouteWaves;
+  return full;
+}
+
 template <int PL>
 __global__ void __launch_bounds__(kRouteThreads)
 moe_route_count_quant_kernel(const void* __restrict__ logits, int ldtype, int T, int E, int k, int norm,
-                             int32_t* __restrict__ idx, float* __restrict__ w, int32_t* __restrict__ counts, int C,
-                             const uint16_t* __restrict__ x, int dtype, int K, bool vec, int KY, int units,
-                             uint8_t* __restrict__ xq, float* __restrict__ xs) {
+                             int TPC, int32_t* __restrict__ idx, float* __restrict__ w,
+                             int32_t* __restrict__ counts, int C, const uint16_t* __restrict__ x, int dtype,
+                             int K, bool vec, int KY, int units, uint8_t* __restrict__ xq,
+                             float* __restrict__ xs) {
   extern __shared__ int hist[];   // E counters, then the chunk's expert ids (kSortChunk)
   const int b = blockIdx.x;
   if (b >= C) {
@@ -628,10 +641,16 @@ moe_route_count_quant_kernel(const void* __restrict__ logits, int ldtype, int T,
   }
   int* sids = hist + E;
   for (int i = threadIdx.x; i < E; i += kRouteThreads) hist[i] = 0;
-  const int TPC = kSortChunk / k;   // k <= kRouteMaxTopK
   const int t0 = b * TPC, nt = min(TPC, T - t0);
   const int wv = wave_id();
-  for (int i = wv; i < nt; i += 2 * kRouteWaves) {
+  if (TPC <= kRouteWaves) {
+    if (wv < nt) {
+      float v[1][PL];
+      route_load<PL>(logits, ldtype, t0 + wv, E, v[0]);
+      const int tt[1] = {t0 + wv};
+      route_tokens<PL, 1>(v, tt, 1, E, k, norm, idx, w, sids + wv * k, 0);
+    }
+  } else for (int i = wv; i < nt; i += 2 * kRouteWaves) {
     const int i1 = min(i + kRouteWaves, nt - 1);
     float v[2][PL];
     route_load<PL>(logits, ldtype, t0 + i, E, v[0]);
@@ -737,7 +756,12 @@ static size_t align256(size_t v) { return (v + 255) / 256 * 256; }
 static MoeWorkspace moe_layout(int64_t T, int64_t H, int64_t I, int64_t E, int64_t k) {
   const int64_t R = T * k;
   const int64_t CR = moe_chunk_rows((int)k);
-  const int64_t C = (R + CR - 1) / CR;
+  // chunks of either call: the caller's routing (CR rows) or the routed call
+  int64_t C = (R + CR - 1) / CR;
+  if (k <= kRouteMaxTopK) {
+    const int64_t tpc = moe_routed_chunk_tokens(T, (int)k, E);
+    C = std::max(C, (T + tpc - 1) / tpc);
+  }
   const int64_t BM = 64 * moe_nrb(R, E);
   const int64_t max_tiles = (R + BM - 1) / BM + E;
   MoeWorkspace w{};
@@ -776,6 +800,7 @@ struct MoeCall {
   int dtype, top_k;
   int64_t tokens, H, I, E;
   int R, CR, C, nrb, BM, max_tiles, KY;
+  int tpc;              // routed call: tokens per sort chunk (CR = tpc * top_k)
   int units;            // token quantization units (kQuantRows rows x one 2048-element span)
   bool vec;
   int32_t *counts, *base, *offsets, *tiles, *tile_count, *sorted, *inv;
@@ -785,14 +810,15 @@ struct MoeCall {
 };
 
 static MoeCall moe_call(const void* hidden, int dtype, int64_t tokens, int64_t H, int64_t I, int64_t E,
-                        int top_k, void* workspace) {
+                        int top_k, void* workspace, bool routed) {
   const MoeWorkspace L = moe_layout(tokens, H, I, E, top_k);
   uint8_t* ws = (uint8_t*)workspace;
   MoeCall m{};
   m.hidden = hidden; m.dtype = dtype; m.top_k = top_k;
   m.tokens = tokens; m.H = H; m.I = I; m.E = E;
   m.R = (int)(tokens * top_k);
-  m.CR = moe_chunk_rows(top_k);
+  m.tpc = routed ? moe_routed_chunk_tokens(tokens, top_k, E) : 0;
+  m.CR = routed ? m.tpc * top_k : moe_chunk_rows(top_k);
   m.C = (m.R + m.CR - 1) / m.CR;
   m.nrb = moe_nrb(m.R, E);
   m.BM = 64 * m.nrb;
@@ -980,7 +1006,7 @@ extern "C" int kq_moe_block_fp8_experts(const void* hidden, int dtype, int64_t t
                                   top_k, workspace, workspace_bytes);
   if (bad != KQ_OK || tokens == 0) return bad;
   hipStream_t st = (hipStream_t)stream;
-  const MoeCall m = moe_call(hidden, dtype, tokens, hidden_size, inter, experts, top_k, workspace);
+  const MoeCall m = moe_call(hidden, dtype, tokens, hidden_size, inter, experts, top_k, workspace, false);
   // chunk histograms and the token quantization share one launch
   const int64_t blocks = (int64_t)m.C + m.units;
   hipLaunchKernelGGL(moe_count_quant_kernel, dim3((unsigned)blocks), dim3(kSortChunk), m.E * sizeof(int), st,
@@ -1014,7 +1040,7 @@ extern "C" int kq_moe_routed_block_fp8_experts(const void* logits, int logits_dt
     return KQ_EINVAL;
   }
   hipStream_t st = (hipStream_t)stream;
-  const MoeCall m = moe_call(hidden, dtype, tokens, hidden_size, inter, experts, top_k, workspace);
+  const MoeCall m = moe_call(hidden, dtype, tokens, hidden_size, inter, experts, top_k, workspace, true);
   // routing, the chunk histograms and the token quantization in one launch
   const int64_t per_block = kRouteThreads / 256;
   const int64_t blocks = (int64_t)m.C + (m.units + per_block - 1) / per_block;
@@ -1023,8 +1049,8 @@ extern "C" int kq_moe_routed_block_fp8_experts(const void* logits, int logits_dt
   const dim3 grid((unsigned)blocks), block(kRouteThreads);
 #define KQ_ROUTE_LAUNCH(PL)                                                                                    \
   hipLaunchKernelGGL(moe_route_count_quant_kernel<PL>, grid, block, lds, st, logits, logits_dtype, T, E, top_k, \
-                     norm, topk_idx, topk_w, m.counts, m.C, (const uint16_t*)hidden, dtype, (int)m.H, m.vec,    \
-                     m.KY, m.units, m.xq, m.xs)
+                     norm, m.tpc, topk_idx, topk_w, m.counts, m.C, (const uint16_t*)hidden, dtype, (int)m.H,    \
+                     m.vec, m.KY, m.units, m.xq, m.xs)
   if (E <= 64) KQ_ROUTE_LAUNCH(1);
   else if (E <= 128) KQ_ROUTE_LAUNCH(2);
   else if (E <= 256) KQ_ROUTE_LAUNCH(4);
