@@ -873,8 +873,8 @@ static void moe_sort_experts_combine(const MoeCall& m, const int32_t* topk_idx, 
   g.N = (int)(2 * m.I); g.K = (int)m.H; g.I = (int)m.I;
   g.mtiles = m.max_tiles; g.ntiles = (int)(m.I / 128);
   g.actq = m.actq; g.acts = m.acts; g.out_dtype = m.dtype; g.bias_dtype = KQ_DTYPE_NONE;
-  if (m.nrb == 5) tg_launch<kTgFp8, true, kTgEpiSwiGluQuant, 5>(g, st);
-  else tg_launch<kTgFp8, true, kTgEpiSwiGluQuant, 4>(g, st);
+  if (m.nrb == 5) tg_launch<kTgFp8, true, kTgEpiSwiGluQuant, 5, true>(g, st);
+  else tg_launch<kTgFp8, true, kTgEpiSwiGluQuant, 4, true>(g, st);
 
   TileGemmArgs d{};
   d.x = m.actq; d.xs = m.acts; d.x_rows = m.R; d.gather = nullptr;
@@ -882,8 +882,8 @@ static void moe_sort_experts_combine(const MoeCall& m, const int32_t* topk_idx, 
   d.N = (int)m.H; d.K = (int)m.I; d.I = 0;
   d.mtiles = m.max_tiles; d.ntiles = (int)((m.H + kTgBN - 1) / kTgBN);
   d.out = m.y; d.out_dtype = m.dtype; d.bias = nullptr; d.bias_dtype = KQ_DTYPE_NONE;
-  if (m.nrb == 5) tg_launch<kTgFp8, true, kTgEpiStore, 5>(d, st);
-  else tg_launch<kTgFp8, true, kTgEpiStore, 4>(d, st);
+  if (m.nrb == 5) tg_launch<kTgFp8, true, kTgEpiStore, 5, true>(d, st);
+  else tg_launch<kTgFp8, true, kTgEpiStore, 4, true>(d, st);
 
   hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)m.tokens), dim3(256), 0, st, m.y, m.dtype, m.inv, topk_w,
                      m.top_k, (int)m.H, (uint16_t*)out);
