@@ -242,9 +242,6 @@ tile_gemm_kernel(TileGemmArgs a) {
   const int o_lo = lr * kTgBK + (tg_chunk<FMT>(lr, FMT == kTgFp8 ? 2 * lg : lg) << 4);
   const int o_hi = lr * kTgBK + (tg_chunk<FMT>(lr, FMT == kTgFp8 ? 2 * lg + 1 : 4 + lg) << 4);
 
-  // tile row of this lane's results in row block mb
-  auto trow = [&](int mb) { return 16 * (4 * mb + wm) + lr; };
-
   float* sRed = (float*)(smem + L::Red);
 
   // ---- tile metadata.  A row tile's table entry is (expert, first row, end
