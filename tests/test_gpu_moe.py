@@ -238,6 +238,45 @@ def test_routed_call_matches_route_then_experts(cuda, tokens, hidden, inter, exp
     assert torch.equal(out.view(torch.int16), expected.view(torch.int16))
 
 
+@pytest.mark.parametrize("tokens,experts,top_k", [(333, 60, 6), (4096, 128, 8), (9000, 128, 8)])
+def test_routed_call_fits_the_exact_workspace(cuda, tokens, experts, top_k):
+    """The routed call's sort chunks (16 tokens where the chunk table fits
+    the one-launch scan) outnumber the given-routing call's; both run in
+    exactly kq_moe_workspace_size bytes (a buffer of that size with a guard
+    region behind it that must stay untouched) and give the two-call bits."""
+    banner(f"moe exact workspace tokens={tokens} E={experts} k={top_k}")
+    hidden, inter = 128, 128
+    pack = _pack(experts, hidden, inter, seed=tokens, device=cuda)
+    g = torch.Generator().manual_seed(tokens + 3)
+    x = torch.randn(tokens, hidden, generator=g).to(torch.bfloat16).to(cuda)
+    logits = torch.randn(tokens, experts, generator=g).to(cuda)
+    idx, w = hmoe._route(logits, top_k, True)
+    expected = pack.forward(x, idx, w)
+    need = int(_native.library().kq_moe_workspace_size(tokens, hidden, inter, experts, top_k))
+    guard = 1 << 16
+    buf = torch.full((need + guard,), 0x5A, dtype=torch.uint8, device=cuda)
+    out = torch.empty_like(x)
+    idx2 = torch.empty(tokens, top_k, dtype=torch.int32, device=cuda)
+    w2 = torch.empty(tokens, top_k, dtype=torch.float32, device=cuda)
+    stream = _native.stream_handle(cuda)
+    _native.call("kq_moe_routed_block_fp8_experts", logits.data_ptr(), _native.dtype_code(logits.dtype), 1,
+                 x.data_ptr(), _native.dtype_code(x.dtype), tokens, hidden, inter, experts, top_k,
+                 pack.w13.data_ptr(), pack.s13.data_ptr(), pack.w2.data_ptr(), pack.s2.data_ptr(),
+                 idx2.data_ptr(), w2.data_ptr(), out.data_ptr(), buf.data_ptr(), need, stream)
+    assert torch.equal(idx2, idx) and torch.equal(out.view(torch.int16), expected.view(torch.int16))
+    out2 = torch.empty_like(x)
+    _native.call("kq_moe_block_fp8_experts", x.data_ptr(), _native.dtype_code(x.dtype), tokens, hidden, inter,
+                 experts, top_k, idx.data_ptr(), w.data_ptr(), pack.w13.data_ptr(), pack.s13.data_ptr(),
+                 pack.w2.data_ptr(), pack.s2.data_ptr(), out2.data_ptr(), buf.data_ptr(), need, stream)
+    assert torch.equal(out2.view(torch.int16), expected.view(torch.int16))
+    assert bool((buf[need:] == 0x5A).all())
+    with pytest.raises(RuntimeError, match="workspace"):
+        _native.call("kq_moe_routed_block_fp8_experts", logits.data_ptr(), _native.dtype_code(logits.dtype), 1,
+                     x.data_ptr(), _native.dtype_code(x.dtype), tokens, hidden, inter, experts, top_k,
+                     pack.w13.data_ptr(), pack.s13.data_ptr(), pack.w2.data_ptr(), pack.s2.data_ptr(),
+                     idx2.data_ptr(), w2.data_ptr(), out.data_ptr(), buf.data_ptr(), need - 256, stream)
+
+
 def test_routed_call_graph_replays_match_eager(cuda):
     """The one-call block forward captured in a HIP graph: every replay (with
     eager calls of the same function between them) gives the eager bits."""
