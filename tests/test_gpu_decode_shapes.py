@@ -104,3 +104,37 @@ def test_w8a8_decode_projection_shapes_match_oracle(cuda, shape, fmt, m):
                                                 np32(module.weight_scale), None)
     assert np.array_equal(acc.cpu().numpy().astype(np.int64), eacc)
     assert np.array_equal(bits(out), bf16_bits(expected).view(np.int16))
+
+
+@pytest.mark.parametrize("n,k", [(4096, 14336), (3584, 18944), (2048, 4224)])
+def test_long_k_act_order_decode_fits_the_exact_workspace(cuda, n, k):
+    """Act-order decode with K split across workgroups needs the gathered x
+    and the fp32 split partials in one workspace: the call runs in exactly
+    kq_w4a16_workspace_size bytes (an upper bound over the shape's paths; a
+    guard region behind it stays untouched), gives the module forward's bits,
+    and a buffer smaller than the gathered x alone is refused."""
+    from kairyu_amd import _native
+    from kairyu_amd.kernels import quant_gemm_hip as hip
+
+    m = 16
+    banner(f"exact workspace act-order decode N={n} K={k}")
+    wl = workloads.gptq_layer(m=m, n=n, k=k, device=cuda, act_order=True)
+    module = wl.module
+    expected = module(wl.x)
+    mode, weight, perm = hip._gptq_operands(module, cuda)
+    need = int(_native.library().kq_w4a16_workspace_size(m, n, k, mode))
+    guard = 1 << 16
+    buf = torch.full((need + guard,), 0x5A, dtype=torch.uint8, device=cuda)
+    out = torch.empty_like(expected)
+
+    def call(nbytes):
+        _native.call("kq_w4a16_tiled_gemm", wl.x.data_ptr(), _native.dtype_code(wl.x.dtype),
+                     weight.tiles.data_ptr(), _native.ptr(weight.zeros), weight.zero_offset,
+                     module.scales.data_ptr(), _native.ptr(perm), None, _native.DTYPE_NONE, out.data_ptr(),
+                     m, n, k, module.group_size, buf.data_ptr(), nbytes, _native.stream_handle(cuda))
+
+    call(need)
+    assert torch.equal(out.view(torch.int16), expected.view(torch.int16))
+    assert bool((buf[need:] == 0x5A).all())
+    with pytest.raises(RuntimeError, match="workspace"):
+        call(m * k)  # half the fp16 gathered x
