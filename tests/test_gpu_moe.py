@@ -210,6 +210,8 @@ def test_sort_scan_forms_match_oracle(cuda, tokens, top_k, experts):
     (64, 128, 128, 512, 8, torch.float32, False),    # 8 logits per lane; E > 256: the two-launch scan
     (9000, 128, 128, 128, 8, torch.float32, True),   # 282 chunks x 128 experts: past the one-launch scan
     (1, 128, 128, 8, 2, torch.bfloat16, True),
+    (150, 128, 128, 64, 16, torch.bfloat16, True),   # 16 tokens (256 rows) per chunk
+    (70, 128, 128, 96, 32, torch.float32, False),    # 8 tokens per chunk: half the routing waves idle
     (40, 128, 128, 64, 40, torch.float32, True),     # top_k > 32 is the routing's limit: rejected
 ])
 def test_routed_call_matches_route_then_experts(cuda, tokens, hidden, inter, experts, top_k, ldtype, norm):
