@@ -528,8 +528,9 @@ DECODE_SHAPES = [("Llama-3-8B down_proj", 4096, 14336), ("Llama-3-8B k_proj", 10
                  ("Qwen2-7B q_proj", 3584, 3584), ("Qwen2-7B down_proj", 3584, 18944)]
 
 # The reference's published microbenchmark (RTX PRO 6000 Blackwell, N = K =
-# 4096, bf16 x, seed 205; bench/results/quant-gemm-rtxpro6000-2026-07-27.json
-# as quoted in BASELINE.md): median ms of module(x) per scheme and M.
+# 4096, bf16 x, seed 205; the reference's
+# bench/results/quant-gemm-rtxpro6000-2026-07-27.json): median ms of
+# module(x) per scheme and M.
 REFERENCE_MICROBENCH_MS = {("fp8", 1): 0.11891, ("fp8", 128): 0.11754, ("int8", 1): 0.10899,
                            ("int8", 128): 0.11770, ("awq", 1): 0.08890, ("awq", 128): 0.29862,
                            ("gptq", 1): 0.10749, ("gptq", 128): 0.26109}
