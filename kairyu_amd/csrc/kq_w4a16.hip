@@ -1541,10 +1541,23 @@ static void launch_prefill_shape(const W4Args& a, hipStream_t stream) {
 }
 
 // 64 x 128 tiles up to M = 64 (twice the column tiles of 256-wide ones, no
-// idle activation rows; a 4-stage ring), 128 x 256 beyond with all 8 waves
-// side by side along N (each weight word dequantized once per tile).
-// Measured on C2 (N = 28672, K = 4096): M = 64 34.4 -> 33.4 us against
-// 3 stages; M = 512 152 -> 140 us against 2 x 4 waves of 64 x 64.
+// idle activation rows; a 4-stage ring), 128 x 256 or 128 x 512 beyond with
+// all 8 waves side by side along N (each weight word dequantized once per
+// tile).  Measured on C2 (N = 28672, K = 4096): M = 64 34.4 -> 33.4 us
+// against 3 stages; M = 512 152 -> 140 us against 2 x 4 waves of 64 x 64.
+// A 128 x 512 tile copies a third fewer bytes per MFMA (its 128 x 128-k
+// activation block serves twice the columns) but fits only a 2-stage ring
+// (65 KB stages): a round of them over the CUs takes 1.72x a round of
+// 128 x 256 tiles (C2: 119 against 69 us), so they run where that takes
+// fewer rounds' time: C2 M = 512 138 -> 119 us (224 tiles, one round against
+// two), M = 1024 281 -> 236 us, M = 2048 511 -> 474 us; M <= 256 and
+// N = 4096 keep the 128 x 256 tiles (M = 128: 68 against 107 us).
+static bool prefill_wide(const W4Args& a) {
+  const int64_t cus = device_cus(), mb = (a.M + 127) / 128;
+  const int64_t wide = mb * ((a.N + 511) / 512), narrow = mb * ((a.N + 255) / 256);
+  return 43 * ((wide + cus - 1) / cus) < 25 * ((narrow + cus - 1) / cus);
+}
+
 static void launch_prefill(const W4Args& a, hipStream_t stream) {
   if (a.swiglu) {
     // M > 64 (kq_w4a16_tiled_swiglu_gemm): each wave's two column tiles are a
@@ -1555,6 +1568,7 @@ static void launch_prefill(const W4Args& a, hipStream_t stream) {
     return;
   }
   if (a.M <= 64) launch_prefill_shape<4, 1, 1, 4>(a, stream);
+  else if (prefill_wide(a)) launch_prefill_shape<8, 4, 1, 2>(a, stream);
   else launch_prefill_shape<8, 2, 1, 3>(a, stream);
 }
 

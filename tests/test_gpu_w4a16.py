@@ -165,6 +165,29 @@ def test_prefill_gemm_matches_oracle(cuda, kind, m, dtype):
     check_w4a16(out, module, x, label=f"{kind} m={m}")
 
 
+# 128 x 512 prefill tiles (chosen on 256 CUs where they take fewer rounds: here
+# 3 row tiles x 43 column tiles = 129 of them against 258 of 128 x 256):
+# M = 300 ends in a 44-row tile, N = 22008 in a 504-column tile whose last
+# 16-column block is half used.
+@pytest.mark.parametrize("kind", ["awq", "gptq", "gptq_act_order"])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_wide_prefill_tiles_match_oracle(cuda, kind, dtype):
+    banner(f"w4a16 wide prefill {kind} {dtype}")
+    m, k, n, group = 300, 1024, 22008, 128
+    g = torch.Generator().manual_seed(2000 + len(kind))
+    if kind == "awq":
+        module = _awq_module(k, n, group=group, seed=31, random_packed=True)
+    else:
+        g_idx = (torch.randperm(k, generator=g) // group).to(torch.int32) if kind == "gptq_act_order" \
+            else (torch.arange(k) // group).to(torch.int32)
+        module = _gptq_module(k, n, group=group, seed=32, g_idx=g_idx, random_packed=True)
+        module.g_idx.copy_(g_idx)
+    module = module.to(cuda)
+    x = torch.randn(m, k, generator=g).to(dtype)
+    out = module(x.to(cuda))
+    check_w4a16(out, module, x, label=f"wide {kind}")
+
+
 @pytest.mark.parametrize("mode", ["uniform", "act_order", "arbitrary"])
 @pytest.mark.parametrize("m", [1, 16, 33, 100])
 def test_gptq_group_modes(cuda, mode, m):
