@@ -490,9 +490,25 @@ tile_gemm_kernel(TileGemmArgs a) {
         f32x4 blk[kTgLag + 1];
 #pragma unroll
         for (int mb = 0; mb < NRB; ++mb) xf[mb] = tg_load(sX + mb * 64 * kTgBK, o_lo, o_hi);
+        // 256-row tiles: the next weight fragment's LDS read goes out before
+        // this one's MFMAs, and the fence keeps the scheduler from sinking it
+        // to its use (otherwise each fragment's read latency stalls its MFMAs:
+        // C3 M = 8192 377 -> 362 us, C4 M = 4096 272 -> 265 us; a second
+        // fragment ahead measured the same).  320-row tiles have no registers
+        // for the second buffer.
+        constexpr bool PF = NRB == 4;
+        TgFrag wfb[2];
+        if constexpr (PF) wfb[0] = tg_load(sW, o_lo, o_hi);
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-          const TgFrag wf = tg_load(sW + j * 16 * kTgBK, o_lo, o_hi);
+          TgFrag wf;
+          if constexpr (PF) {
+            if (j + 1 < 8) wfb[(j + 1) & 1] = tg_load(sW + (j + 1) * 16 * kTgBK, o_lo, o_hi);
+            __builtin_amdgcn_sched_barrier(0);
+            wf = wfb[j & 1];
+          } else {
+            wf = tg_load(sW + j * 16 * kTgBK, o_lo, o_hi);
+          }
 #pragma unroll
           for (int mb = 0; mb < NRB; ++mb) {
             if constexpr (FMT == kTgI8) {
