@@ -1551,22 +1551,31 @@ static void launch_prefill_shape(const W4Args& a, hipStream_t stream) {
                      mblocks, tiles);
 }
 
-// 64 x 128 tiles up to M = 64 (twice the column tiles of 256-wide ones, no
-// idle activation rows; a 4-stage ring), 128 x 256 or 128 x 512 beyond with
-// all 8 waves side by side along N (each weight word dequantized once per
-// tile).  Measured on C2 (N = 28672, K = 4096): M = 64 34.4 -> 33.4 us
-// against 3 stages; M = 512 152 -> 140 us against 2 x 4 waves of 64 x 64.
-// A 128 x 512 tile copies a third fewer bytes per MFMA (its 128 x 128-k
-// activation block serves twice the columns) but fits only a 2-stage ring
-// (65 KB stages): a round of them over the CUs takes 1.72x a round of
-// 128 x 256 tiles (C2: 119 against 69 us), so they run where that takes
-// fewer rounds' time: C2 M = 512 138 -> 119 us (224 tiles, one round against
-// two), M = 1024 281 -> 236 us, M = 2048 511 -> 474 us; M <= 256 and
-// N = 4096 keep the 128 x 256 tiles (M = 128: 68 against 107 us).
-static bool prefill_wide(const W4Args& a) {
-  const int64_t cus = device_cus(), mb = (a.M + 127) / 128;
-  const int64_t wide = mb * ((a.N + 511) / 512), narrow = mb * ((a.N + 255) / 256);
-  return 43 * ((wide + cus - 1) / cus) < 25 * ((narrow + cus - 1) / cus);
+// Tile shapes: 64 x 128 (4-stage ring), 128 x 128 and 128 x 256 (3 stages),
+// 128 x 512 (2 stages of 65 KB), all with the 8 waves side by side along N
+// (each weight word dequantized once per tile).  Larger tiles copy fewer
+// bytes per MFMA but are fewer; the launch takes the shape with the least
+// estimated time, rounds of tiles over the CUs times a tile's time under
+// full load, measured on C2 (N = 28672, K = 4096): 33, 45, 65 and 112 us.
+// Against 128 x 256 tiles from M = 65 on (same process, outputs
+// bit-identical): C2 M = 128 61.1 -> 45.3 us (128 x 128), M = 512
+// 138 -> 119 us, M = 1024 281 -> 236, M = 2048 511 -> 474 (128 x 512);
+// N = 4096 M = 512 63.4 -> 33.2 us and N = 14336 M = 128 61.0 -> 31.2 us
+// (64 x 128).  (M = 64: the 4-stage ring 34.4 -> 33.4 us against 3 stages;
+// 2 x 4 waves of 64 x 64 took M = 512 152 against 140 us.)
+enum { kPfSmall = 0, kPfSquare = 1, kPfNarrow = 2, kPfWide = 3 };
+static int prefill_shape(const W4Args& a) {
+  if (a.M <= 64) return kPfSmall;
+  const int64_t cus = device_cus();
+  auto rounds = [&](int64_t bm, int64_t bn) {
+    return ((a.M + bm - 1) / bm * ((a.N + bn - 1) / bn) + cus - 1) / cus;
+  };
+  const int64_t t[4] = {33 * rounds(64, 128), 45 * rounds(128, 128), 65 * rounds(128, 256),
+                        112 * rounds(128, 512)};
+  int best = kPfWide;  // ties: the larger tile (fewer bytes)
+  for (int s = kPfNarrow; s >= kPfSmall; --s)
+    if (t[s] < t[best]) best = s;
+  return best;
 }
 
 static void launch_prefill(const W4Args& a, hipStream_t stream) {
@@ -1578,9 +1587,12 @@ static void launch_prefill(const W4Args& a, hipStream_t stream) {
     launch_prefill_shape<8, 2, 1, 3, true>(a, stream);
     return;
   }
-  if (a.M <= 64) launch_prefill_shape<4, 1, 1, 4>(a, stream);
-  else if (prefill_wide(a)) launch_prefill_shape<8, 4, 1, 2>(a, stream);
-  else launch_prefill_shape<8, 2, 1, 3>(a, stream);
+  switch (prefill_shape(a)) {
+    case kPfSmall: launch_prefill_shape<4, 1, 1, 4>(a, stream); break;
+    case kPfSquare: launch_prefill_shape<8, 1, 1, 3>(a, stream); break;
+    case kPfNarrow: launch_prefill_shape<8, 2, 1, 3>(a, stream); break;
+    default: launch_prefill_shape<8, 4, 1, 2>(a, stream); break;
+  }
 }
 
 template <int XDT, int S, int SPG>

@@ -142,9 +142,10 @@ def test_awq_all_paths(cuda, m, dtype):
     check_w4a16(out, module, x, label=f"m={m}")
 
 
-# Prefill GEMM (M > 16, tiled weights, K and group multiples of 128): 64x128
-# tiles up to M = 64, 128x256 beyond; N = 392 ends in a half-used 16-column
-# tile and a partial 128/256-column tile, M = 17 / 65 / 300 partial row tiles.
+# Prefill GEMM (M > 16, tiled weights, K and group multiples of 128): at
+# N = 392 every M takes 64x128 tiles (one round of them); N = 392 ends in a
+# half-used 16-column tile and a partial 128-column tile, M = 17 / 65 / 300
+# partial row tiles.
 @pytest.mark.parametrize("kind", ["awq", "gptq", "gptq_act_order"])
 @pytest.mark.parametrize("m", [17, 64, 65, 300])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
@@ -165,16 +166,36 @@ def test_prefill_gemm_matches_oracle(cuda, kind, m, dtype):
     check_w4a16(out, module, x, label=f"{kind} m={m}")
 
 
-# 128 x 512 prefill tiles (chosen on 256 CUs where they take fewer rounds: here
-# 3 row tiles x 43 column tiles = 129 of them against 258 of 128 x 256):
-# M = 300 ends in a 44-row tile, N = 22008 in a 504-column tile whose last
-# 16-column block is half used.
+# The prefill launch picks the tile shape with the least estimated time,
+# rounds of tiles over the CUs times a measured per-tile time; this restates
+# that choice for 256 CUs only to confirm that each case below reaches the
+# shape it is meant to cover.
+def _prefill_shape(m, n, cus=256):
+    if m <= 64:
+        return "64x128"
+    def rounds(bm, bn):
+        return (-(-m // bm) * -(-n // bn) + cus - 1) // cus
+    t = {"64x128": 33 * rounds(64, 128), "128x128": 45 * rounds(128, 128),
+         "128x256": 65 * rounds(128, 256), "128x512": 112 * rounds(128, 512)}
+    best = "128x512"
+    for s in ("128x256", "128x128", "64x128"):
+        if t[s] < t[best]:
+            best = s
+    return best
+
+
+# Every M > 64 tile shape with ragged rows (M = 100 / 200 / 300 end in a
+# partial row tile) and, for 128 x 512, N = 22008: a 504-column last tile
+# whose last 16-column block is half used.
+@pytest.mark.parametrize("shape,m,n", [("128x128", 100, 28672), ("128x256", 200, 28672),
+                                       ("128x512", 300, 22008), ("64x128", 300, 4096)])
 @pytest.mark.parametrize("kind", ["awq", "gptq", "gptq_act_order"])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
-def test_wide_prefill_tiles_match_oracle(cuda, kind, dtype):
-    banner(f"w4a16 wide prefill {kind} {dtype}")
-    m, k, n, group = 300, 1024, 22008, 128
-    g = torch.Generator().manual_seed(2000 + len(kind))
+def test_prefill_tile_shapes_match_oracle(cuda, shape, m, n, kind, dtype):
+    assert _prefill_shape(m, n) == shape
+    banner(f"w4a16 prefill {shape} {kind} m={m} n={n} {dtype}")
+    k, group = 1024, 128
+    g = torch.Generator().manual_seed(2000 + m + len(kind))
     if kind == "awq":
         module = _awq_module(k, n, group=group, seed=31, random_packed=True)
     else:
@@ -185,7 +206,7 @@ def test_wide_prefill_tiles_match_oracle(cuda, kind, dtype):
     module = module.to(cuda)
     x = torch.randn(m, k, generator=g).to(dtype)
     out = module(x.to(cuda))
-    check_w4a16(out, module, x, label=f"wide {kind}")
+    check_w4a16(out, module, x, label=f"{shape} {kind}")
 
 
 @pytest.mark.parametrize("mode", ["uniform", "act_order", "arbitrary"])
@@ -274,15 +295,16 @@ def test_graph_replays_match_eager(cuda):
 
 
 def test_graph_replays_prefill_and_gemv_paths(cuda):
-    """The prefill GEMM (both tile shapes, act-order included) and the decode
-    GEMV captured in one graph; every replay matches eager."""
+    """The prefill GEMM (64x128 and 128x256 tiles, act-order included) and the
+    decode GEMV captured in one graph; every replay matches eager."""
     banner("w4a16 graph replay: prefill + gemv")
     awq = _awq_module(1024, 392, group=128, seed=21, random_packed=True).to(cuda)
-    gptq = _gptq_module(1024, 392, group=128, seed=22, random_packed=True,
+    gptq = _gptq_module(1024, 28672, group=128, seed=22, random_packed=True,
                         g_idx=(torch.randperm(1024) // 128).to(torch.int32)).to(cuda)
     gemv = _gptq_module(4096, 4096, group=128, seed=23, random_packed=True).to(cuda)
+    assert _prefill_shape(64, 392) == "64x128" and _prefill_shape(200, 28672) == "128x256"
     cases = ((awq, torch.randn(64, 1024, device=cuda, dtype=torch.float16)),
-             (gptq, torch.randn(300, 1024, device=cuda, dtype=torch.bfloat16)),
+             (gptq, torch.randn(200, 1024, device=cuda, dtype=torch.bfloat16)),
              (gemv, torch.randn(16, 4096, device=cuda, dtype=torch.float16)))
     eager = [m(x).clone() for m, x in cases]
     torch.cuda.synchronize()
