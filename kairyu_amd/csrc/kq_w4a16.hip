@@ -979,13 +979,14 @@ struct W4pShape {
 };
 
 // SWIGLU: the operand interleaves gate and up 16-column tiles (2p gate, 2p + 1
-// up), so each wave's pair of column tiles (TN = 2) holds both halves of its
-// 16 output columns and the epilogue writes silu(gate) * up into out [M][N/2].
+// up), so each pair of a wave's column tiles (TN = 2 or 4) holds both halves
+// of 16 output columns and the epilogue writes silu(gate) * up into
+// out [M][N/2].
 template <int TM, int TN, int WM, int NS, bool SWIGLU = false>
 __global__ void __launch_bounds__(512)
 w4a16_prefill_kernel(W4Args a, int mblocks, int tiles) {
   using S = W4pShape<TM, TN, WM>;
-  static_assert(!SWIGLU || TN == 2, "the SwiGLU epilogue pairs a wave's two column tiles");
+  static_assert(!SWIGLU || TN % 2 == 0, "the SwiGLU epilogue pairs a wave's column tiles");
   __shared__ __attribute__((aligned(16))) uint8_t smem[NS * S::Stage + 8 * 256];
   const int lane = lane_id();
   const int wave = __builtin_amdgcn_readfirstlane(wave_id());
@@ -1129,37 +1130,42 @@ w4a16_prefill_kernel(W4Args a, int mblocks, int tiles) {
   // epilogue: lane (c, g) of block (tn, i) holds rows m = .. + c, columns
   // n = .. + 4g .. 4g+3
   if constexpr (SWIGLU) {
-    const int ng = n0 + wn * 32 + 4 * g;     // gate column of the interleaved operand (up: + 16)
     const int width = a.N / 2;
-    const int oc = n0 / 2 + wn * 16 + 4 * g;  // output column
-    float bg[4] = {0.f, 0.f, 0.f, 0.f}, bu[4] = {0.f, 0.f, 0.f, 0.f};
-    if (a.bias_dtype != KQ_DTYPE_NONE)
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        bg[q] = ng + q < a.N ? load_as_f32(a.bias, a.bias_dtype, ng + q) : 0.f;
-        bu[q] = ng + 16 + q < a.N ? load_as_f32(a.bias, a.bias_dtype, ng + 16 + q) : 0.f;
-      }
+    for (int pp = 0; pp < TN / 2; ++pp) {
+      // pair pp: gate column tile wn * TN + 2 pp of the interleaved operand,
+      // its up tile the next one; output columns 16 of them
+      const int ng = n0 + (wn * TN + 2 * pp) * 16 + 4 * g;
+      const int oc = n0 / 2 + (wn * TN / 2 + pp) * 16 + 4 * g;
+      float bg[4] = {0.f, 0.f, 0.f, 0.f}, bu[4] = {0.f, 0.f, 0.f, 0.f};
+      if (a.bias_dtype != KQ_DTYPE_NONE)
 #pragma unroll
-    for (int i = 0; i < TM; ++i) {
-      const int m = m0 + (wm * TM + i) * 16 + c;
-      if (m >= a.M) continue;
-      uint16_t o[4];
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        float gv = acc[0][i][q], uv = acc[1][i][q];
-        if (a.bias_dtype != KQ_DTYPE_NONE) {
-          gv = __fadd_rn(gv, bg[q]);
-          uv = __fadd_rn(uv, bu[q]);
+        for (int q = 0; q < 4; ++q) {
+          bg[q] = ng + q < a.N ? load_as_f32(a.bias, a.bias_dtype, ng + q) : 0.f;
+          bu[q] = ng + 16 + q < a.N ? load_as_f32(a.bias, a.bias_dtype, ng + 16 + q) : 0.f;
         }
-        o[q] = swiglu_bits(gv, uv, a.out_dtype);
-      }
-      uint16_t* dst = a.out + (int64_t)m * width + oc;
-      if (oc + 3 < width) {
-        *(u32x2*)dst = u32x2{(uint32_t)o[0] | ((uint32_t)o[1] << 16), (uint32_t)o[2] | ((uint32_t)o[3] << 16)};
-      } else {
 #pragma unroll
-        for (int q = 0; q < 4; ++q)
-          if (oc + q < width) dst[q] = o[q];
+      for (int i = 0; i < TM; ++i) {
+        const int m = m0 + (wm * TM + i) * 16 + c;
+        if (m >= a.M) continue;
+        uint16_t o[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          float gv = acc[2 * pp][i][q], uv = acc[2 * pp + 1][i][q];
+          if (a.bias_dtype != KQ_DTYPE_NONE) {
+            gv = __fadd_rn(gv, bg[q]);
+            uv = __fadd_rn(uv, bu[q]);
+          }
+          o[q] = swiglu_bits(gv, uv, a.out_dtype);
+        }
+        uint16_t* dst = a.out + (int64_t)m * width + oc;
+        if (oc + 3 < width) {
+          *(u32x2*)dst = u32x2{(uint32_t)o[0] | ((uint32_t)o[1] << 16), (uint32_t)o[2] | ((uint32_t)o[3] << 16)};
+        } else {
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            if (oc + q < width) dst[q] = o[q];
+        }
       }
     }
     return;
@@ -1580,11 +1586,13 @@ static int prefill_shape(const W4Args& a) {
 
 static void launch_prefill(const W4Args& a, hipStream_t stream) {
   if (a.swiglu) {
-    // M > 64 (kq_w4a16_tiled_swiglu_gemm): each wave's two column tiles are a
-    // gate/up pair.  (A 64 x 256 form for M <= 64 halves the workgroups of the
-    // 64 x 128 tiles: C2's gate/up at M = 64 took 45.3 us fused against 41.8 us
-    // for the 64 x 128 GEMM and the elementwise pass.)
-    launch_prefill_shape<8, 2, 1, 3, true>(a, stream);
+    // M > 64 (kq_w4a16_tiled_swiglu_gemm): each pair of a wave's column tiles
+    // is a gate/up pair; 128 x 512 tiles where prefill_shape would take them,
+    // else 128 x 256.  (A 64 x 256 form for M <= 64 halves the workgroups of
+    // the 64 x 128 tiles: C2's gate/up at M = 64 took 45.3 us fused against
+    // 41.8 us for the 64 x 128 GEMM and the elementwise pass.)
+    if (prefill_shape(a) == kPfWide) launch_prefill_shape<8, 4, 1, 2, true>(a, stream);
+    else launch_prefill_shape<8, 2, 1, 3, true>(a, stream);
     return;
   }
   switch (prefill_shape(a)) {

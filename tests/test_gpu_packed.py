@@ -146,12 +146,13 @@ _SWIGLU_CASES = [
     ("gptq-sym", 16, 4096, 4096, torch.float16, False),
     ("gptq-sym-ao", 1, 4096, 4096, torch.bfloat16, False),
     ("awq", 5, 4096, 4096, torch.float16, True),
-    ("gptq", 100, 1024, 1024, torch.bfloat16, False),      # prefill: GEMM + elementwise pass
+    ("gptq", 100, 1024, 1024, torch.bfloat16, False),      # prefill, 128 x 256 SwiGLU tiles
     ("gptq-sym-ao", 7, 4128, 512, torch.float16, False),   # skinny shape: two passes
     ("awq", 64, 2048, 1024, torch.float16, False),
     # W4A16 prefill SwiGLU epilogue: a ragged last 256-column tile, act-order, real widths
     ("gptq-ao", 48, 2048, 1040, torch.float16, True),
-    ("awq", 300, 4096, 11008, torch.bfloat16, False),
+    ("awq", 300, 4096, 11008, torch.bfloat16, False),      # 128 x 512 SwiGLU tiles (two pairs per wave)
+    ("gptq-ao", 512, 1024, 10880, torch.float16, True),     # ... ending in a half-used 512-column tile
     # real MLP widths: 2-4 gate/up pairs per workgroup, uneven shares, K = 2048 (S = 4)
     ("gptq-sym-ao", 1, 4096, 14336, torch.float16, False),
     ("gptq", 16, 4096, 14336, torch.bfloat16, False),
