@@ -780,9 +780,9 @@ static void launch_skinny(const uint8_t* xq, const uint8_t* w, int K, const Epi&
 
 // Work units per 256x256 tile for the tile engine at M > 64, 0 when it does
 // not apply: 1 with at least one tile per CU; otherwise the K range is split
-// (2..4 ways, >= 8 K blocks each) when that fills at least half the CUs and
-// the workspace holds the fp32/int32 partials.  Shapes it declines take the
-// 128x128 kernel.
+// (2..4 ways, >= 8 K blocks each) when that fills at least half the CUs, else
+// up to 8 ways with >= 4 K blocks each, where the workspace holds the
+// fp32/int32 partials.  Shapes it declines take the 128x128 kernel.
 static int tile_engine_splits(int64_t m, int64_t n, int K, const void* workspace, size_t ws_bytes) {
   if (m * K >= ((int64_t)1 << 31) || n * K >= ((int64_t)1 << 31)) return 0;
   const int64_t tiles = ((m + kTgBM - 1) / kTgBM) * ((n + kTgBN - 1) / kTgBN);
@@ -793,6 +793,14 @@ static int tile_engine_splits(int64_t m, int64_t n, int K, const void* workspace
     if (kb / s >= 8 && tiles * s * 2 >= cus && workspace &&
         (size_t)s * (size_t)(m * n) * 4 <= ws_bytes)
       return s;
+  // Too few tiles to fill half the CUs that way: split K up to 8 ways (at
+  // least 4 K blocks per unit) rather than run the 128x128 kernel with a
+  // workgroup per 128x128 tile.  N = K = 4096 (same process, outputs
+  // bit-identical): FP8 M = 128 56.1 -> 26.4 us, M = 256 55.7 -> 28.9, INT8
+  // M = 128 51.1 -> 27.2; N = 1024 M = 512 45.9 -> 28.9.  (Where the rule
+  // above applies, 8 ways were slower: M = 512 34.8 -> 38.8 us.)
+  for (int s = (int)std::min<int64_t>(8, cus / tiles); s >= 2; --s)
+    if (kb / s >= 4 && workspace && (size_t)s * (size_t)(m * n) * 4 <= ws_bytes) return s;
   return 0;
 }
 

@@ -81,7 +81,7 @@ def test_int8_fused_output_bit_exact_with_bias(cuda, fixtures, case):
 @pytest.mark.parametrize("m", [1, 5, 16, 17, 33, 64, 65, 200])
 @pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float16])
 def test_int8_accumulators_and_output_bit_exact_all_paths(cuda, m, out_dtype):
-    n, k = 160, 3584  # split-K on the skinny path; 2x2 tiles on the tiled path
+    n, k = 160, 3584  # split-K on the skinny path; beyond M = 64 the tile engine, K split 7 ways
     banner(f"int8 paths m={m} dtype={out_dtype}")
     module = _int8_module(k, n, seed=m).to(cuda)
     x = torch.randn(m, k, generator=torch.Generator().manual_seed(100 + m)).to(out_dtype)
@@ -272,6 +272,56 @@ def test_fp8_tile_engine_split_k_matches_oracle(cuda, m, n, k):
     x = torch.randn(m, k, generator=torch.Generator().manual_seed(k)).to(torch.bfloat16)
     out = module(x.to(cuda))
     check_fp8(out, x, module, label=f"m={m} n={n} k={k}")
+
+
+# Too few 256x256 tiles to fill half the CUs with <= 4 splits of >= 8 K blocks:
+# K split up to 8 ways of >= 4 K blocks (8 ways for both shapes on 256 CUs;
+# the second is ragged in N (N % 8 != 0) and K).
+DEEP_SPLIT_SHAPES = [(128, 4096, 4096), (256, 2044, 4160)]
+
+
+@pytest.mark.parametrize("m,n,k", DEEP_SPLIT_SHAPES)
+def test_int8_deep_split_k_bit_exact(cuda, m, n, k):
+    banner(f"int8 deep split-k m={m} n={n} k={k}")
+    cus = torch.cuda.get_device_properties(cuda).multi_processor_count
+    if cus == 256:
+        assert hip._native.library().kq_w8a8_workspace_size(m, n, k) == 8 * m * n * 4
+    module = _int8_module(k, n, seed=m + n).to(cuda)
+    x = torch.randn(m, k, generator=torch.Generator().manual_seed(k)).to(torch.bfloat16)
+    acc = torch.empty(m, n, dtype=torch.int32, device=cuda)
+    out = hip.int8_linear_forward(x.to(cuda), module, accumulators=acc)
+    expected, xq, xs, eacc = olinear.int8_forward(
+        np32(x), module.weight.cpu().numpy(), module.weight_scale.cpu().numpy(), np32(module.bias))
+    assert np.array_equal(acc.cpu().numpy().astype(np.int64), eacc)
+    assert np.array_equal(np32(out), expected)
+
+
+@pytest.mark.parametrize("m,n,k", DEEP_SPLIT_SHAPES)
+def test_fp8_deep_split_k_matches_oracle(cuda, m, n, k):
+    banner(f"fp8 deep split-k m={m} n={n} k={k}")
+    module = _fp8_module(k, n, seed=m + n).to(cuda)
+    x = torch.randn(m, k, generator=torch.Generator().manual_seed(k)).to(torch.bfloat16)
+    out = module(x.to(cuda))
+    check_fp8(out, x, module, label=f"m={m} n={n} k={k}")
+
+
+# The 128x128 tiled kernel: M > 64 with K too short to split (K = 768: six K
+# blocks) and fewer 256x256 tiles than CUs; 2x2 tiles, ragged in M and N.
+@pytest.mark.parametrize("m", [65, 200])
+def test_w8a8_tiled_kernel_matches_oracle(cuda, m):
+    banner(f"w8a8 128x128 tiles m={m}")
+    n, k = 160, 768
+    assert hip._native.library().kq_w8a8_workspace_size(m, n, k) == 0
+    module = _int8_module(k, n, seed=m).to(cuda)
+    x = torch.randn(m, k, generator=torch.Generator().manual_seed(300 + m)).to(torch.bfloat16)
+    acc = torch.empty(m, n, dtype=torch.int32, device=cuda)
+    out = hip.int8_linear_forward(x.to(cuda), module, accumulators=acc)
+    expected, xq, xs, eacc = olinear.int8_forward(
+        np32(x), module.weight.cpu().numpy(), module.weight_scale.cpu().numpy(), np32(module.bias))
+    assert np.array_equal(acc.cpu().numpy().astype(np.int64), eacc)
+    assert np.array_equal(np32(out), expected)
+    fmod = _fp8_module(k, n, seed=m).to(cuda)
+    check_fp8(fmod(x.to(cuda)), x, fmod, label=f"128x128 fp8 m={m}")
 
 
 # Whole-K tiles (at least one 256x256 tile per CU: no split-K); the second
