@@ -1587,12 +1587,20 @@ static int prefill_shape(const W4Args& a) {
 static void launch_prefill(const W4Args& a, hipStream_t stream) {
   if (a.swiglu) {
     // M > 64 (kq_w4a16_tiled_swiglu_gemm): each pair of a wave's column tiles
-    // is a gate/up pair; 128 x 512 tiles where prefill_shape would take them,
-    // else 128 x 256.  (A 64 x 256 form for M <= 64 halves the workgroups of
-    // the 64 x 128 tiles: C2's gate/up at M = 64 took 45.3 us fused against
-    // 41.8 us for the 64 x 128 GEMM and the elementwise pass.)
-    if (prefill_shape(a) == kPfWide) launch_prefill_shape<8, 4, 1, 2, true>(a, stream);
-    else launch_prefill_shape<8, 2, 1, 3, true>(a, stream);
+    // is a gate/up pair; 64 x 256 (4 stages), 128 x 256 or 128 x 512 tiles by
+    // the same estimate as prefill_shape, a 64 x 256 round taking 45 us on
+    // C2's K.  Gate/up I = 14336 at M = 80 / 128 took 59.3 / 62.0 us on
+    // 128 x 256 tiles and 45.0 / 45.6 us on 64 x 256 ones (outputs
+    // bit-identical).  (At M <= 64 the fused 64 x 256 form is not used: it took
+    // 45.3 us against 41.8 us for the 64 x 128 GEMM and the elementwise pass.)
+    const int64_t cus = device_cus();
+    auto rounds = [&](int64_t bm, int64_t bn) {
+      return ((a.M + bm - 1) / bm * ((a.N + bn - 1) / bn) + cus - 1) / cus;
+    };
+    const int64_t ts = 45 * rounds(64, 256), tn = 65 * rounds(128, 256), tw = 112 * rounds(128, 512);
+    if (tw <= tn && tw <= ts) launch_prefill_shape<8, 4, 1, 2, true>(a, stream);
+    else if (tn <= ts) launch_prefill_shape<8, 2, 1, 3, true>(a, stream);
+    else launch_prefill_shape<4, 2, 1, 4, true>(a, stream);
     return;
   }
   switch (prefill_shape(a)) {

@@ -146,7 +146,8 @@ _SWIGLU_CASES = [
     ("gptq-sym", 16, 4096, 4096, torch.float16, False),
     ("gptq-sym-ao", 1, 4096, 4096, torch.bfloat16, False),
     ("awq", 5, 4096, 4096, torch.float16, True),
-    ("gptq", 100, 1024, 1024, torch.bfloat16, False),      # prefill, 128 x 256 SwiGLU tiles
+    ("gptq", 100, 1024, 1024, torch.bfloat16, False),      # prefill, 64 x 256 SwiGLU tiles
+    ("gptq-ao", 200, 1024, 14336, torch.float16, True),     # prefill, 128 x 256 SwiGLU tiles
     ("gptq-sym-ao", 7, 4128, 512, torch.float16, False),   # skinny shape: two passes
     ("awq", 64, 2048, 1024, torch.float16, False),
     # W4A16 prefill SwiGLU epilogue: a ragged last 256-column tile, act-order, real widths
