@@ -984,7 +984,7 @@ struct W4pShape {
 // out [M][N/2].
 template <int TM, int TN, int WM, int NS, bool SWIGLU = false>
 __global__ void __launch_bounds__(512)
-w4a16_prefill_kernel(W4Args a, int mblocks, int tiles) {
+w4a16_prefill_kernel(W4Args a, int mblocks, int tiles, int ksplit) {
   using S = W4pShape<TM, TN, WM>;
   static_assert(!SWIGLU || TN % 2 == 0, "the SwiGLU epilogue pairs a wave's column tiles");
   __shared__ __attribute__((aligned(16))) uint8_t smem[NS * S::Stage + 8 * 256];
@@ -992,14 +992,18 @@ w4a16_prefill_kernel(W4Args a, int mblocks, int tiles) {
   const int wave = __builtin_amdgcn_readfirstlane(wave_id());
   const int wm = wave / S::WN, wn = wave % S::WN;
   const int c = lane & 15, g = lane >> 4;
-  // XCD-contiguous tile ranges (row block fastest: an XCD's consecutive tiles
-  // share weight tiles in its L2)
-  const int per = (tiles + 7) / 8;
-  const int t = (blockIdx.x & 7) * per + (blockIdx.x >> 3);
-  if (t >= tiles) return;
+  // XCD-contiguous unit ranges (row block fastest: an XCD's consecutive tiles
+  // share weight tiles in its L2; the K splits of a tile are consecutive units)
+  const int total = tiles * ksplit;
+  const int per = (total + 7) / 8;
+  const int u = (blockIdx.x & 7) * per + (blockIdx.x >> 3);
+  if (u >= total) return;
+  const int t = u / ksplit, split = u - t * ksplit;
   const int mb = t % mblocks, nb = t / mblocks;
   const int m0 = mb * S::BM, n0 = nb * S::BN;
   const int K = a.K, nst = K / 128;
+  // this unit's stages [kb0, kb1) (ksplit <= nst / 2: at least two)
+  const int kb0 = (int)((int64_t)nst * split / ksplit), kb1 = (int)((int64_t)nst * (split + 1) / ksplit);
   const int ngroups = K / a.G;
   const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)smem;
 
@@ -1066,13 +1070,13 @@ w4a16_prefill_kernel(W4Args a, int mblocks, int tiles) {
 
 #pragma unroll
   for (int i = 0; i < NS - 1; ++i)
-    if (i < nst) issue(i, i);
-  w4p_wait_stages<S::Ops, NS - 2>(min(NS - 2, nst - 1));
+    if (kb0 + i < kb1) issue(kb0 + i, (kb0 + i) % NS);
+  w4p_wait_stages<S::Ops, NS - 2>(min(NS - 2, kb1 - kb0 - 1));
   __syncthreads();
 
-  for (int kb = 0; kb < nst; ++kb) {
+  for (int kb = kb0; kb < kb1; ++kb) {
     const int slot = kb % NS;
-    if (kb + NS - 1 < nst) issue(kb + NS - 1, (kb + NS - 1) % NS);
+    if (kb + NS - 1 < kb1) issue(kb + NS - 1, (kb + NS - 1) % NS);
     const uint8_t* st = smem + slot * S::Stage;
     // this stage's scales and zeros of the wave's column tiles (one group)
     uint32_t zq0[TN], zq1[TN], sq[TN];
@@ -1123,7 +1127,7 @@ w4a16_prefill_kernel(W4Args a, int mblocks, int tiles) {
     }
     // stage kb+1 landed (the stages issued after it may stay in flight), and
     // every wave is done with stage kb before it is refilled
-    w4p_wait_stages<S::Ops, NS - 2>(min(NS - 2, nst - 2 - kb));
+    w4p_wait_stages<S::Ops, NS - 2>(min(NS - 2, kb1 - 2 - kb));
     __syncthreads();
   }
 
@@ -1165,6 +1169,28 @@ w4a16_prefill_kernel(W4Args a, int mblocks, int tiles) {
 #pragma unroll
           for (int q = 0; q < 4; ++q)
             if (oc + q < width) dst[q] = o[q];
+        }
+      }
+    }
+    return;
+  }
+  if (ksplit > 1) {
+    // this split's fp32 partial sums; the W4 split-K reduce adds the splits in
+    // order and applies bias and the cast
+#pragma unroll
+    for (int tn = 0; tn < TN; ++tn) {
+      const int n = n0 + (wn * TN + tn) * 16 + 4 * g;
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        const int m = m0 + (wm * TM + i) * 16 + c;
+        if (m >= a.M || n >= a.N) continue;
+        float* dst = a.partials + ((int64_t)split * a.M + m) * a.N + n;
+        if (n + 3 < a.N) {
+          *(f32x4*)dst = acc[tn][i];
+        } else {
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            if (n + q < a.N) dst[q] = acc[tn][i][q];
         }
       }
     }
@@ -1548,13 +1574,13 @@ static bool prefill_applies(const W4Args& a, int gmode) {
 }
 
 template <int TM, int TN, int WM, int NS, bool SWIGLU = false>
-static void launch_prefill_shape(const W4Args& a, hipStream_t stream) {
+static void launch_prefill_shape(const W4Args& a, hipStream_t stream, int ksplit = 1) {
   using S = W4pShape<TM, TN, WM>;
   const int mblocks = (a.M + S::BM - 1) / S::BM;
   const int tiles = mblocks * ((a.N + S::BN - 1) / S::BN);
-  const int grid = 8 * ((tiles + 7) / 8);
+  const int grid = 8 * ((tiles * ksplit + 7) / 8);
   hipLaunchKernelGGL((w4a16_prefill_kernel<TM, TN, WM, NS, SWIGLU>), dim3(grid), dim3(512), 0, stream, a,
-                     mblocks, tiles);
+                     mblocks, tiles, ksplit);
 }
 
 // Tile shapes: 64 x 128 (4-stage ring), 128 x 128 and 128 x 256 (3 stages),
@@ -1584,7 +1610,26 @@ static int prefill_shape(const W4Args& a) {
   return best;
 }
 
-static void launch_prefill(const W4Args& a, hipStream_t stream) {
+// K splits of the 64 x 128 tiles where they leave at least half the CUs idle
+// (M <= 64 on narrow projections, e.g. Llama-3-8B down N = 4096: 32 tiles
+// over K = 14336): up to 16 splits of at least two stages whose fp32 partials
+// fit past the staged activations in `avail` bytes and, together with them,
+// in KQ_W4A16_NOALLOC_SCRATCH_BYTES (so the allocation-free entry splits as
+// the workspace entry does); the W4 split-K reduce sums them.
+static int prefill_splits(const W4Args& a, size_t avail) {
+  if (a.swiglu || prefill_shape(a) != kPfSmall) return 1;
+  const int64_t cus = device_cus();
+  const int64_t tiles = (a.M + 63) / 64 * ((a.N + 127) / 128);
+  if (2 * tiles > cus) return 1;
+  const size_t x16 = ((size_t)a.M * (size_t)a.K * 2 + 255) / 256 * 256;
+  const size_t cap = x16 < (size_t)KQ_W4A16_NOALLOC_SCRATCH_BYTES ? (size_t)KQ_W4A16_NOALLOC_SCRATCH_BYTES - x16 : 0;
+  avail = std::min(avail, cap);
+  int64_t s = std::min<int64_t>({16, cus / tiles, (a.K / 128) / 2});
+  while (s > 1 && (size_t)s * (size_t)a.M * (size_t)a.N * 4 > avail) --s;
+  return (int)std::max<int64_t>(1, s);
+}
+
+static void launch_prefill(const W4Args& a, int ksplit, hipStream_t stream) {
   if (a.swiglu) {
     // M > 64 (kq_w4a16_tiled_swiglu_gemm): each pair of a wave's column tiles
     // is a gate/up pair; 64 x 256 (4 stages), 128 x 256 or 128 x 512 tiles by
@@ -1604,7 +1649,7 @@ static void launch_prefill(const W4Args& a, hipStream_t stream) {
     return;
   }
   switch (prefill_shape(a)) {
-    case kPfSmall: launch_prefill_shape<4, 1, 1, 4>(a, stream); break;
+    case kPfSmall: launch_prefill_shape<4, 1, 1, 4>(a, stream, ksplit); break;
     case kPfSquare: launch_prefill_shape<8, 1, 1, 3>(a, stream); break;
     case kPfNarrow: launch_prefill_shape<8, 2, 1, 3>(a, stream); break;
     default: launch_prefill_shape<8, 4, 1, 2>(a, stream); break;
@@ -1736,13 +1781,21 @@ static int run_w4(const char* what, int fmt, W4Args a, int gmode, void* workspac
       return KQ_EWORKSPACE;
     }
     uint16_t* x16 = (uint16_t*)workspace;
+    const size_t x16_al = (x16_bytes + 255) / 256 * 256;
+    const int ks = prefill_splits(a, ws_bytes > x16_al ? ws_bytes - x16_al : 0);
+    a.partials = ks > 1 ? (float*)((uint8_t*)workspace + x16_al) : nullptr;
     const int64_t threads = (int64_t)a.M * a.K / 8;
     hipLaunchKernelGGL(w4a16_prep_x_mma_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0,
                        stream, a.x, a.x_dtype, a.ldx, gmode == kGroupsPermuted ? a.perm : nullptr,
                        a.M, a.K, x16);
     a.x = x16;
     a.ldx = a.K;
-    launch_prefill(a, stream);
+    launch_prefill(a, ks, stream);
+    if (ks > 1) {
+      ReduceArgs r{a.partials, ks, a.M, a.N, nullptr, nullptr, 0, a.bias, a.bias_dtype,
+                   a.out, a.out_dtype, nullptr};
+      launch_splitk_reduce(kReduceW4, r, stream);
+    }
     return check_launch(what);
   }
   W4Plan p = plan_w4(a.M, a.N, a.K, needs_x16, ws_bytes, workspace != nullptr);
@@ -1789,7 +1842,8 @@ static int run_w4(const char* what, int fmt, W4Args a, int gmode, void* workspac
 
 using namespace kq;
 
-extern "C" size_t kq_w4a16_workspace_size(int64_t m, int64_t n, int64_t k, int gidx_mode) {
+// The scratch a call needs at least (the prefill GEMM without K splits).
+static size_t w4_min_workspace(int64_t m, int64_t n, int64_t k, int gidx_mode) {
   if (m <= 0 || n <= 0 || k <= 0) return 0;
   // a generous workspace lets the planner choose split-K freely
   const W4Plan p = plan_w4((int)m, (int)n, (int)k, gidx_mode == kGroupsPermuted,
@@ -1800,6 +1854,19 @@ extern "C" size_t kq_w4a16_workspace_size(int64_t m, int64_t n, int64_t k, int g
   const size_t gv = (gidx_mode == kGroupsPermuted ? ((size_t)m * (size_t)k * 2 + 255) / 256 * 256 : 0) +
                     gv_split_bytes(m, n, k);
   return std::max({p.x16_bytes + p.partial_bytes, x16, gv});
+}
+
+extern "C" size_t kq_w4a16_workspace_size(int64_t m, int64_t n, int64_t k, int gidx_mode) {
+  const size_t need = w4_min_workspace(m, n, k, gidx_mode);
+  if (need == 0 || m <= 16 || m > 0x7fffffff || n > 0x7fffffff || k > 0x7fffffff) return need;
+  // the prefill GEMM's K-split partials past its staged activations
+  W4Args a{};
+  a.M = (int)m;
+  a.N = (int)n;
+  a.K = (int)k;
+  const int ks = prefill_splits(a, (size_t)1 << 40);
+  const size_t x16 = ((size_t)m * (size_t)k * 2 + 255) / 256 * 256;
+  return ks > 1 ? std::max(need, x16 + (size_t)ks * (size_t)m * (size_t)n * 4) : need;
 }
 
 // Offset of the SwiGLU two-pass intermediate: after the GEMM's own scratch.

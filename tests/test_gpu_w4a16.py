@@ -209,6 +209,52 @@ def test_prefill_tile_shapes_match_oracle(cuda, shape, m, n, kind, dtype):
     check_w4a16(out, module, x, label=f"{shape} {kind}")
 
 
+# K splits of the 64x128 prefill tiles where they would leave at least half
+# the CUs idle: up to 16 splits of >= 2 stages whose fp32 partials fit, with
+# the staged activations, in the allocation-free entry's scratch; the W4
+# split-K reduce sums them and adds the bias.  Restated for 256 CUs to check
+# the workspace size each case below reports.
+def _prefill_splits(m, n, k, cus=256):
+    if _prefill_shape(m, n, cus) != "64x128":
+        return 1
+    tiles = -(-m // 64) * -(-n // 128)
+    if 2 * tiles > cus:
+        return 1
+    x16 = (m * k * 2 + 255) // 256 * 256
+    s = min(16, cus // tiles, (k // 128) // 2)
+    while s > 1 and x16 + s * m * n * 4 > (16 << 20):
+        s -= 1
+    return max(1, s)
+
+
+# Llama-3-8B down (8 splits of 14 stages), k_proj (16 of 2), Qwen2-7B q_proj
+# at M = 17 (9 uneven splits of 28 stages) and a 64x128 shape beyond M = 64.
+@pytest.mark.parametrize("m,n,k,splits", [(64, 4096, 14336, 8), (40, 1024, 4096, 16), (17, 3584, 3584, 9),
+                                          (300, 2048, 2048, 3)])
+@pytest.mark.parametrize("kind", ["awq", "gptq_act_order"])
+def test_split_k_prefill_matches_oracle(cuda, m, n, k, splits, kind):
+    assert _prefill_splits(m, n, k) == splits
+    cus = torch.cuda.get_device_properties(cuda).multi_processor_count
+    if cus == 256:
+        x16 = (m * k * 2 + 255) // 256 * 256
+        mode = hip.GIDX_PERMUTED if kind == "gptq_act_order" else hip.GIDX_UNIFORM
+        assert hip._native.library().kq_w4a16_workspace_size(m, n, k, mode) == x16 + splits * m * n * 4
+    banner(f"w4a16 split-k prefill {kind} m={m} n={n} k={k} splits={splits}")
+    group = 128
+    g = torch.Generator().manual_seed(3000 + m)
+    if kind == "awq":
+        module = _awq_module(k, n, group=group, seed=m + 1, random_packed=True)
+    else:
+        g_idx = (torch.randperm(k, generator=g) // group).to(torch.int32)
+        module = _gptq_module(k, n, group=group, seed=m + 2, g_idx=g_idx, random_packed=True)
+        module.g_idx.copy_(g_idx)
+    module = module.to(cuda)
+    dtype = torch.float16 if m % 2 == 0 else torch.bfloat16
+    x = torch.randn(m, k, generator=g).to(dtype)
+    out = module(x.to(cuda))
+    check_w4a16(out, module, x, label=f"split-k {kind} m={m} n={n}")
+
+
 @pytest.mark.parametrize("mode", ["uniform", "act_order", "arbitrary"])
 @pytest.mark.parametrize("m", [1, 16, 33, 100])
 def test_gptq_group_modes(cuda, mode, m):
