@@ -121,9 +121,9 @@ size_t kq_w8a8_linear_workspace_size(int64_t m, int64_t n, int64_t k);
  * rows), and out [m][i_width] (activation dtype) = silu(g) * u for gate
  * column c and up column i_width + c, with the roundings of
  * kq_w8a8_*_linear followed by kq_swiglu (bit-identical to that pair).
- * Prefill shapes apply SwiGLU in the tile engine's epilogue (the [m][2I]
- * projection never reaches memory); other shapes run the pair through the
- * workspace.  Replaces the reference MLP's act_fn(gate(x)) * up(x)
+ * Prefill shapes apply SwiGLU in the tile engine's epilogue and decode shapes
+ * (m <= 16, k % 128 == 0) in the decode GEMM's (the [m][2I] projection never
+ * reaches memory); other shapes run the pair through the workspace.  Replaces the reference MLP's act_fn(gate(x)) * up(x)
  * (kairyu/models/layers.py:243-244) over its packed projections
  * (kairyu/models/packed_linear.py:58-149) for FP8 / INT8 W8A8. */
 int kq_w8a8_i8_swiglu_linear(const void* x, int x_dtype, int64_t ldx, const int8_t* w,

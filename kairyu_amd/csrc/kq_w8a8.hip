@@ -50,6 +50,9 @@ struct Epi {
   int out_dtype;
   int32_t* acc_out;
   int M, N;
+  // decode kernels only: N = 2I packed gate / up weight rows [gate; up], the
+  // output out[M][I] = silu(gate) * up (SwiGLU epilogue); 0: out[M][N]
+  int swiglu;
 };
 
 template <int FMT>
@@ -66,6 +69,41 @@ KQ_DEV void epi_store(const Epi& ep, int m, int n, typename W8Traits<FMT>::Acc a
   v = __fmul_rn(v, ep.ws_per_channel ? ep.wscale[n] : ep.wscale[0]);
   if (ep.bias_dtype != KQ_DTYPE_NONE) v = __fadd_rn(v, load_as_f32(ep.bias, ep.bias_dtype, n));
   ((uint16_t*)ep.out)[(int64_t)m * ep.N + n] = f32_to_out(v, ep.out_dtype);
+}
+
+// Decode tiles with the SwiGLU epilogue: tile t pairs gate rows [8t, 8t + 8)
+// (tile rows 0..7) with up rows [I + 8t, I + 8t + 8) (tile rows 8..15), so a
+// lane's column j and column j ^ 8 are one gate / up pair.  Weight row of tile
+// row r, or -1 past the I activation columns.
+KQ_DEV int swiglu_row(int t, int r, int I) {
+  const int c = 8 * t + (r & 7);
+  return c < I ? (r < 8 ? c : I + c) : -1;
+}
+
+// The decode epilogue with SwiGLU: the store epilogue's ((acc * xs) * ws) +
+// bias for both columns of a pair, then swiglu_bits (the elementwise pass's
+// roundings) -- the bits of the packed linear followed by kq_swiglu.  Lane
+// (j, kg) holds column j of tile t for rows 4kg..4kg+3; all 64 lanes take part
+// (the pair exchange is a cross-lane read).
+template <int FMT>
+KQ_DEV void epi_swiglu(const Epi& ep, const float* xs, int t, int j, int kg,
+                       typename W8Traits<FMT>::Acc acc) {
+  const int I = ep.N >> 1;
+  const int n = swiglu_row(t, j, I);
+  const float ws = n >= 0 ? (ep.ws_per_channel ? ep.wscale[n] : ep.wscale[0]) : 0.0f;
+  const float b = n >= 0 && ep.bias_dtype != KQ_DTYPE_NONE ? load_as_f32(ep.bias, ep.bias_dtype, n) : 0.0f;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int m = kg * 4 + r;
+    float v = 0.0f;
+    if (n >= 0 && m < ep.M) {
+      v = __fmul_rn(__fmul_rn((float)acc[r], xs[m]), ws);
+      if (ep.bias_dtype != KQ_DTYPE_NONE) v = __fadd_rn(v, b);
+    }
+    const float u = __shfl_xor(v, 8, 64);
+    if (j < 8 && n >= 0 && m < ep.M)
+      ((uint16_t*)ep.out)[(int64_t)m * I + 8 * t + j] = swiglu_bits(v, u, ep.out_dtype);
+  }
 }
 
 // Raw 32-bit pattern of accumulator element r.  (Goes through a scalar
@@ -238,7 +276,10 @@ KQ_DEV void wait_vm() {
 
 constexpr int kDecStage = 4096;  // 2 KB weight block + 2 KB activation block
 
-template <int FMT, int R, int NW, int XH>
+// SW: the SwiGLU epilogue (Epi::swiglu); workgroup t holds the 16 weight rows
+// of swiglu_row (the whole weight is one buffer: 2I * K < 2^31), otherwise
+// rows [16t, 16t + 16).
+template <int FMT, int R, int NW, int XH, bool SW>
 __global__ void __launch_bounds__(64 * NW)
 w8a8_decode_kernel(const uint8_t* __restrict__ xq, const uint8_t* __restrict__ w, int K, Epi ep) {
   constexpr int TF = FMT == kFmtFp8 ? kTgFp8 : kTgI8;
@@ -254,7 +295,8 @@ w8a8_decode_kernel(const uint8_t* __restrict__ xq, const uint8_t* __restrict__ w
   const int per_wave = (nst + NW - 1) / NW;
   const int sbeg = wave * per_wave;
   const int nmy = max(0, min(nst, sbeg + per_wave) - sbeg);
-  const i32x4 rw = make_rsrc(w + (int64_t)n0 * K, (uint32_t)(min(kSkinnyCols, ep.N - n0) * K));
+  const i32x4 rw = SW ? make_rsrc(w, (uint32_t)(ep.N * K))
+                      : make_rsrc(w + (int64_t)n0 * K, (uint32_t)(min(kSkinnyCols, ep.N - n0) * K));
   const i32x4 rx = make_rsrc(xq, (uint32_t)(ep.M * K));
   const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)ring +
                         wave * R * kDecStage;
@@ -263,7 +305,12 @@ w8a8_decode_kernel(const uint8_t* __restrict__ xq, const uint8_t* __restrict__ w
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
     const int r = 8 * h + (lane >> 3), c = tg_chunk<TF>(r, lane & 7);
-    vw[h] = r * K + c * 16;
+    if constexpr (SW) {
+      const int n = swiglu_row((int)blockIdx.x, r, ep.N >> 1);
+      vw[h] = n >= 0 ? n * K + c * 16 : kTgOob;
+    } else {
+      vw[h] = r * K + c * 16;
+    }
     vx[h] = r < ep.M ? r * K + c * 16 : kTgOob;
   }
   auto issue = [&](int st, int q) {
@@ -321,18 +368,35 @@ w8a8_decode_kernel(const uint8_t* __restrict__ xq, const uint8_t* __restrict__ w
       if constexpr (FMT == kFmtI8) acc[r] += (int)bits;
       else acc[r] = __fadd_rn(acc[r], __uint_as_float(bits));
     }
+  if constexpr (SW) {
+    epi_swiglu<FMT>(ep, ep.xscale, (int)blockIdx.x, j, kg, acc);
+  } else {
 #pragma unroll
-  for (int r = 0; r < 4; ++r) epi_store<FMT>(ep, kg * 4 + r, n0 + j, acc, r);
+    for (int r = 0; r < 4; ++r) epi_store<FMT>(ep, kg * 4 + r, n0 + j, acc, r);
+  }
+}
+
+// Workgroups of a decode launch: one per 16 weight rows; with the SwiGLU
+// epilogue one per 8 activation columns (8 gate + 8 up rows).
+static dim3 decode_grid(const Epi& ep) {
+  return ep.swiglu ? dim3((unsigned)((ep.N / 2 + 7) / 8)) : dim3((unsigned)((ep.N + kSkinnyCols - 1) / kSkinnyCols));
+}
+
+template <int FMT, int R, int NW, bool SW>
+static void launch_decode_sw(const uint8_t* xq, const uint8_t* w, int K, const Epi& ep,
+                             hipStream_t stream) {
+  const dim3 grid = decode_grid(ep), block(64 * NW);
+  if (ep.M <= 8)
+    hipLaunchKernelGGL((w8a8_decode_kernel<FMT, R, NW, 1, SW>), grid, block, 0, stream, xq, w, K, ep);
+  else
+    hipLaunchKernelGGL((w8a8_decode_kernel<FMT, R, NW, 2, SW>), grid, block, 0, stream, xq, w, K, ep);
 }
 
 template <int FMT, int R, int NW>
 static void launch_decode_nw(const uint8_t* xq, const uint8_t* w, int K, const Epi& ep,
                              hipStream_t stream) {
-  const dim3 grid((ep.N + kSkinnyCols - 1) / kSkinnyCols), block(64 * NW);
-  if (ep.M <= 8)
-    hipLaunchKernelGGL((w8a8_decode_kernel<FMT, R, NW, 1>), grid, block, 0, stream, xq, w, K, ep);
-  else
-    hipLaunchKernelGGL((w8a8_decode_kernel<FMT, R, NW, 2>), grid, block, 0, stream, xq, w, K, ep);
+  if (ep.swiglu) launch_decode_sw<FMT, R, NW, true>(xq, w, K, ep, stream);
+  else launch_decode_sw<FMT, R, NW, false>(xq, w, K, ep, stream);
 }
 
 // Waves and ring depth of the decode kernels.  With at least one workgroup
@@ -387,8 +451,9 @@ static void launch_decode(const uint8_t* xq, const uint8_t* w, int K, const Epi&
 // element takes the reciprocal path when it is finite and the row scale lies
 // in [2^-60, FLT_MAX] (there both paths give the same byte), otherwise IEEE
 // division -- decided per wave and stage, so they match the quantizer's
-// row-level choice; the row scale enters in the epilogue.
-template <int FMT, int R, int NW, int MR>
+// row-level choice; the row scale enters in the epilogue.  SW: the SwiGLU
+// epilogue and weight rows of w8a8_decode_kernel<..., true>.
+template <int FMT, int R, int NW, int MR, bool SW>
 __global__ void __launch_bounds__(64 * NW)
 w8a8_decode_quant_kernel(const uint16_t* __restrict__ x, int x_dtype, int ldx, int scale_mode,
                          const float* __restrict__ scale_in, const uint8_t* __restrict__ w, int K,
@@ -413,7 +478,8 @@ w8a8_decode_quant_kernel(const uint16_t* __restrict__ x, int x_dtype, int ldx, i
   const int per_wave = (nst + NW - 1) / NW;
   const int sbeg = wave * per_wave;
   const int nmy = max(0, min(nst, sbeg + per_wave) - sbeg);
-  const i32x4 rw = make_rsrc(w + (int64_t)n0 * K, (uint32_t)(min(kSkinnyCols, ep.N - n0) * K));
+  const i32x4 rw = SW ? make_rsrc(w, (uint32_t)(ep.N * K))
+                      : make_rsrc(w + (int64_t)n0 * K, (uint32_t)(min(kSkinnyCols, ep.N - n0) * K));
   const i32x4 rx = make_rsrc(x, (uint32_t)(((int64_t)(M - 1) * ldx + K) * 2));
   const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)ring +
                         wave * R * kDecStage;
@@ -421,7 +487,12 @@ w8a8_decode_quant_kernel(const uint16_t* __restrict__ x, int x_dtype, int ldx, i
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
     const int r = 8 * h + (lane >> 3), c = tg_chunk<TF>(r, lane & 7);
-    vw[h] = r * K + c * 16;
+    if constexpr (SW) {
+      const int n = swiglu_row((int)blockIdx.x, r, ep.N >> 1);
+      vw[h] = n >= 0 ? n * K + c * 16 : kTgOob;
+    } else {
+      vw[h] = r * K + c * 16;
+    }
   }
   const int xr = lane >> 4;  // raw rows 0..3, 16 chunks of 8 elements each
   const int32_t vx = xr < M ? (xr * ldx + (lane & 15) * 8) * 2 : kTgOob;
@@ -571,6 +642,10 @@ w8a8_decode_quant_kernel(const uint16_t* __restrict__ x, int x_dtype, int ldx, i
       if constexpr (FMT == kFmtI8) acc[r] += (int)bits;
       else acc[r] = __fadd_rn(acc[r], __uint_as_float(bits));
     }
+  if constexpr (SW) {
+    epi_swiglu<FMT>(ep, srow, (int)blockIdx.x, j, kg, acc);
+    return;
+  }
   const int n = n0 + j;
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
@@ -590,24 +665,32 @@ w8a8_decode_quant_kernel(const uint16_t* __restrict__ x, int x_dtype, int ldx, i
   }
 }
 
+template <int FMT, int MR, bool SW>
+static void launch_decode_quant_sw(const uint16_t* x, int x_dtype, int ldx, int scale_mode,
+                                   const float* scale_in, const uint8_t* w, int K, const Epi& ep,
+                                   hipStream_t stream) {
+  const DecForm f = decode_form(ep.N, K, ep.M);
+  const dim3 grid = decode_grid(ep);
+  if (f.nw == 16)
+    hipLaunchKernelGGL((w8a8_decode_quant_kernel<FMT, 2, 16, MR, SW>), grid, dim3(1024), 0, stream, x,
+                       x_dtype, ldx, scale_mode, scale_in, w, K, ep);
+  else if (f.nw == 8)
+    hipLaunchKernelGGL((w8a8_decode_quant_kernel<FMT, 4, 8, MR, SW>), grid, dim3(512), 0, stream, x,
+                       x_dtype, ldx, scale_mode, scale_in, w, K, ep);
+  else if (f.nw == 4)
+    hipLaunchKernelGGL((w8a8_decode_quant_kernel<FMT, 4, 4, MR, SW>), grid, dim3(256), 0, stream, x,
+                       x_dtype, ldx, scale_mode, scale_in, w, K, ep);
+  else
+    hipLaunchKernelGGL((w8a8_decode_quant_kernel<FMT, 2, 2, MR, SW>), grid, dim3(128), 0, stream, x,
+                       x_dtype, ldx, scale_mode, scale_in, w, K, ep);
+}
+
 template <int FMT, int MR>
 static void launch_decode_quant_mr(const uint16_t* x, int x_dtype, int ldx, int scale_mode,
                                    const float* scale_in, const uint8_t* w, int K, const Epi& ep,
                                    hipStream_t stream) {
-  const DecForm f = decode_form(ep.N, K, ep.M);
-  const dim3 grid((ep.N + kSkinnyCols - 1) / kSkinnyCols);
-  if (f.nw == 16)
-    hipLaunchKernelGGL((w8a8_decode_quant_kernel<FMT, 2, 16, MR>), grid, dim3(1024), 0, stream, x,
-                       x_dtype, ldx, scale_mode, scale_in, w, K, ep);
-  else if (f.nw == 8)
-    hipLaunchKernelGGL((w8a8_decode_quant_kernel<FMT, 4, 8, MR>), grid, dim3(512), 0, stream, x,
-                       x_dtype, ldx, scale_mode, scale_in, w, K, ep);
-  else if (f.nw == 4)
-    hipLaunchKernelGGL((w8a8_decode_quant_kernel<FMT, 4, 4, MR>), grid, dim3(256), 0, stream, x,
-                       x_dtype, ldx, scale_mode, scale_in, w, K, ep);
-  else
-    hipLaunchKernelGGL((w8a8_decode_quant_kernel<FMT, 2, 2, MR>), grid, dim3(128), 0, stream, x,
-                       x_dtype, ldx, scale_mode, scale_in, w, K, ep);
+  if (ep.swiglu) launch_decode_quant_sw<FMT, MR, true>(x, x_dtype, ldx, scale_mode, scale_in, w, K, ep, stream);
+  else launch_decode_quant_sw<FMT, MR, false>(x, x_dtype, ldx, scale_mode, scale_in, w, K, ep, stream);
 }
 
 // One activation row (MR = 1); the kernel also takes MR = 2 and 4.
@@ -820,6 +903,12 @@ static int run_w8a8(const char* what, const uint8_t* xq, const uint8_t* w, int64
   }
   if (m == 0) return KQ_OK;
   const int K = (int)k;
+  if (ep.swiglu && !(m <= 16 && K % 128 == 0 && ((uintptr_t)xq % 16) == 0 && ((uintptr_t)w % 16) == 0 &&
+                     n * k < ((int64_t)1 << 31))) {
+    set_error("%s: the SwiGLU epilogue runs in the decode kernels only (m=%lld k=%lld)", what,
+              (long long)m, (long long)k);
+    return KQ_EINVAL;
+  }
   if ((K % 16) != 0 || ((uintptr_t)xq % 16) || ((uintptr_t)w % 16)) {
     const int64_t total = m * n;
     hipLaunchKernelGGL(w8a8_generic_kernel<FMT>, dim3((unsigned)((total + 255) / 256)),
@@ -1003,9 +1092,11 @@ extern "C" int kq_w8a8_fp8_linear(const void* x, int x_dtype, int64_t ldx, const
 // Prefill shapes (M > 64, I % 128 == 0, enough 256 x 256 tiles for half the
 // CUs) run the tile engine with the SwiGLU store epilogue: each tile pairs
 // gate columns [n0, n0 + 128) with up columns [I + n0, I + n0 + 128), so the
-// [M, 2I] projection output never reaches memory.  Other shapes run the
-// packed linear into the workspace and the elementwise pass.  Both produce
-// the bits of the packed linear followed by kq_swiglu.
+// [M, 2I] projection output never reaches memory.  Decode shapes (M <= 16,
+// K % 128 == 0) run the decode kernels with the SwiGLU epilogue (each
+// workgroup's 16 weight rows are 8 gate rows and the matching 8 up rows).
+// Other shapes run the packed linear into the workspace and the elementwise
+// pass.  All produce the bits of the packed linear followed by kq_swiglu.
 static bool swiglu_fused_applies(int64_t m, int64_t i_width, int64_t k, const void* x, int64_t ldx,
                                  const void* w) {
   if (m <= 64 || i_width % 128 != 0 || k % 16 != 0 || ((uintptr_t)w % 16) != 0) return false;
@@ -1054,6 +1145,14 @@ static int run_swiglu_linear(const char* what, const void* x, int x_dtype, int64
     a.ksplit = 1;
     tg_launch<FMT == kFmtI8 ? kTgI8 : kTgFp8, false, kTgEpiSwiGluStore>(a, stream);
     return check_launch(what);
+  }
+  if (m >= 1 && m <= 16 && k % 128 == 0 && k <= 65536 && ((uintptr_t)w % 16) == 0 &&
+      ((uintptr_t)workspace % 16) == 0 && n * k < ((int64_t)1 << 31)) {
+    // decode shapes: the decode kernels (one-row fused quantization or the
+    // per-token quantizer first) with the SwiGLU epilogue
+    ep.swiglu = 1;
+    return run_linear<FMT>(what, x, x_dtype, ldx, scale_mode, scale_in, w, m, n, k, ep, workspace,
+                           ws_bytes, stream);
   }
   // two passes: the packed projection [m][2I] in the activation dtype, then SwiGLU
   const size_t tmp_bytes = ((size_t)(m > 0 ? m : 0) * (size_t)n * 2 + 255) / 256 * 256;

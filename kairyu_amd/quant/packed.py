@@ -24,9 +24,10 @@ reference MLP's activation (``kairyu/models/layers.py:243-244``), with
 torch's fp16 / bf16 roundings; for W4A16 in one call whose decode GEMV (M <=
 16) or prefill GEMM (M > 64) applies SwiGLU in its epilogue (gate and up
 16-column blocks interleaved in a derived tiled operand), for W8A8 in one
-call whose prefill tile engine applies it in
-its epilogue (gate rows [n0, n0 + 128) paired with up rows [I + n0, ...) of
-the packed weight, no second copy).
+call whose prefill tile engine or decode GEMM (M <= 16) applies it in its
+epilogue (gate rows [n0, n0 + 128) paired with up rows [I + n0, ...) of the
+packed weight, or 8 gate and 8 up rows per decode workgroup; no second
+copy).
 
 ``create`` returns ``None`` for anything it cannot pack exactly (mixed
 formats, in-features, devices, biases, group sizes, static input scales,
@@ -275,7 +276,8 @@ class QuantLinearPack:
         columns interleaved by 16 in a derived tiled operand,
         ``kq_w4a16_tiled_swiglu_gemm``);
         W8A8 packs run ``kq_w8a8_*_swiglu_linear`` (SwiGLU in the tile
-        engine's epilogue for prefill shapes)."""
+        engine's epilogue for prefill shapes, in the decode GEMM's for
+        M <= 16)."""
 
         if len(self._projections) != 2 or self._out_features[0] != self._out_features[1]:
             raise ValueError("swiglu needs a (gate, up) pack of equal widths")
@@ -311,8 +313,9 @@ class QuantLinearPack:
 
     def _w8a8_swiglu(self, hidden: torch.Tensor, width: int) -> torch.Tensor:
         """One kq_w8a8_*_swiglu_linear call on the packed [gate; up] weight:
-        SwiGLU in the tile engine's epilogue for prefill shapes, the packed
-        GEMM and the elementwise pass otherwise (the same bits either way)."""
+        SwiGLU in the tile engine's epilogue for prefill shapes and in the
+        decode GEMM's for M <= 16, the packed GEMM and the elementwise pass
+        otherwise (the same bits either way)."""
 
         from kairyu_amd import _native
         from kairyu_amd.kernels import quant_gemm_hip as hip

@@ -169,7 +169,8 @@ def projection_pre(module, x: torch.Tensor, add_bias: bool = True) -> tuple[np.n
         return pre.astype(np.float64), np.zeros(pre.shape)
     assert isinstance(module, Fp8Linear)
     w_bits, w_scale = bits(module.weight), np32(module.weight_scale)
-    _, x_bits, x_scale, pre = olinear.fp8_forward(xs, w_bits, w_scale, bias)
+    static = None if module.activation_dynamic else np32(module.input_scale)
+    _, x_bits, x_scale, pre = olinear.fp8_forward(xs, w_bits, w_scale, bias, static_scale=static)
     terms = olinear.fp8_abs_terms(x_bits, w_bits, x_scale, w_scale)
     ws = np.abs(w_scale.astype(np.float64)).reshape(-1, 1)
     x_mag = np.abs(e4m3_decode(x_bits)) * np.abs(np.asarray(x_scale, np.float64)).reshape(-1, 1)

@@ -136,8 +136,8 @@ def test_pack_graph_replays_match_eager(cuda):
 # W4A16: one kq_w4a16_tiled_swiglu_gemm call; decode shapes (here N = 2 x 4096
 # on K = 4096) apply SwiGLU in the GEMV epilogue, others run the tiled GEMM
 # and the elementwise pass.  W8A8: one kq_w8a8_*_swiglu_linear call; prefill
-# shapes apply SwiGLU in the tile engine's epilogue, others run the packed
-# GEMM and kq_swiglu.
+# shapes apply SwiGLU in the tile engine's epilogue, decode shapes (M <= 16)
+# in the decode GEMM's, others run the packed GEMM and kq_swiglu.
 _SWIGLU_CASES = [
     # (scheme, m, k, width, dtype, bias)
     ("gptq", 1, 4096, 4096, torch.float16, False),
@@ -163,6 +163,12 @@ _SWIGLU_CASES = [
     ("gptq", 1, 2048, 11008, torch.bfloat16, True),
     ("fp8", 1, 2048, 2048, torch.bfloat16, True),
     ("fp8", 300, 1024, 1024, torch.float16, False),
+    # decode shapes: SwiGLU in the decode GEMM's epilogue (8 gate + 8 up rows
+    # per workgroup), one-row fused quantization at M = 1
+    ("fp8", 16, 4096, 14336, torch.bfloat16, True),
+    ("fp8-static", 1, 4096, 1004, torch.float16, True),
+    ("int8", 1, 3584, 9472, torch.bfloat16, False),
+    ("int8", 9, 4096, 1028, torch.float16, True),
     # prefill shapes: SwiGLU in the tile engine's epilogue (>= 128 tiles of 256 x 256)
     ("fp8", 1024, 1024, 4096, torch.bfloat16, True),
     ("int8", 2048, 1024, 2048, torch.float16, False),
@@ -172,8 +178,8 @@ _SWIGLU_CASES = [
 
 def _swiglu_pair(scheme, k, width, bias, seed):
     gen = torch.Generator().manual_seed(seed)
-    if scheme in ("fp8", "int8"):
-        make = _fp8 if scheme == "fp8" else _int8
+    if scheme in ("fp8", "fp8-static", "int8"):
+        make = {"fp8": _fp8, "int8": _int8, "fp8-static": lambda k, n, s: _fp8(k, n, s, dynamic=False)}[scheme]
         mods = [make(k, width, seed + i) for i in range(2)]
         if not bias:
             for m in mods:
@@ -272,10 +278,23 @@ def test_swiglu_pack_rejects_diverged_g_idx(cuda):
 @pytest.mark.parametrize("scheme,m,k,width,dtype,bias", [
     ("fp8", 1024, 1024, 4096, torch.bfloat16, True),
     ("int8", 2048, 1024, 2048, torch.float16, False),
+    # decode GEMM epilogue, every decode form: 4 waves (K = 4096, >= 1 tile
+    # per CU), 16 waves (K = 4096, few tiles), 8 waves (K = 14336), 2 waves
+    # (K = 2048 / 3584); fused quantization at M = 1; ragged widths
+    ("fp8", 1, 4096, 4096, torch.bfloat16, True),
+    ("fp8", 2, 4096, 1004, torch.float16, False),
+    ("fp8", 16, 14336, 2048, torch.bfloat16, True),
+    ("fp8-static", 16, 4096, 14336, torch.float16, False),
+    ("fp8-static", 1, 2048, 2052, torch.bfloat16, True),
+    ("int8", 1, 2048, 2048, torch.float16, True),
+    ("int8", 16, 3584, 9472, torch.bfloat16, False),
+    ("int8", 9, 4096, 1028, torch.float16, True),
+    ("int8", 4, 14336, 4096, torch.bfloat16, True),
 ])
 def test_w8a8_swiglu_epilogue_bit_identical_to_two_passes(cuda, scheme, m, k, width, dtype, bias):
-    """The tile engine's SwiGLU store epilogue gives the bits of the packed
-    GEMM followed by the elementwise pass (kq_swiglu) on the same call."""
+    """The SwiGLU epilogues (tile engine for prefill shapes, decode GEMM for
+    M <= 16) give the bits of the packed GEMM followed by the elementwise pass
+    (kq_swiglu) on the same call."""
     from kairyu_amd import _native
 
     gate, up = (mod.to(cuda) for mod in _swiglu_pair(scheme, k, width, bias, seed=m + width))
