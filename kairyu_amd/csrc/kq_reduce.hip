@@ -190,8 +190,34 @@ __global__ void __launch_bounds__(256) splitk_reduce8_kernel(ReduceArgs a) {
   *(u32x4*)((uint16_t*)a.out + base) = u32x4{o[0], o[1], o[2], o[3]};
 }
 
+// W8A8 with SwiGLU: thread = one output (m, c), gate column c and up column
+// I + c of the [M][2I] partial plane, each summed and scaled as above, then
+// swiglu_bits: the bits of the packed epilogue followed by kq_swiglu.
+template <int MODE>
+__global__ void __launch_bounds__(256) splitk_reduce_swiglu_kernel(ReduceArgs a) {
+  const int I = a.N / 2;
+  const int64_t plane = (int64_t)a.M * a.N;
+  const int64_t o = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (o >= (int64_t)a.M * I) return;
+  const int m = (int)(o / I), c = (int)(o - (int64_t)m * I);
+  const int64_t row = (int64_t)m * a.N;
+  auto wscale = [&](int n) -> float {
+    return (MODE == kReduceI8 || a.ws_per_channel) ? a.wscale[n] : a.wscale[0];
+  };
+  const float xs = a.xscale[m];
+  const float g = reduce_epilogue<MODE>(a, row + c, m, c, plane, xs, wscale(c));
+  const float u = reduce_epilogue<MODE>(a, row + I + c, m, I + c, plane, xs, wscale(I + c));
+  ((uint16_t*)a.out)[o] = swiglu_bits(g, u, a.out_dtype);
+}
+
 void launch_splitk_reduce(int mode, const ReduceArgs& a, hipStream_t stream) {
   const int64_t total = (int64_t)a.M * a.N;
+  if (a.swiglu) {
+    const dim3 g((unsigned)((total / 2 + 255) / 256)), b(256);
+    if (mode == kReduceI8) hipLaunchKernelGGL(splitk_reduce_swiglu_kernel<kReduceI8>, g, b, 0, stream, a);
+    else hipLaunchKernelGGL(splitk_reduce_swiglu_kernel<kReduceFp8>, g, b, 0, stream, a);
+    return;
+  }
   if (mode != kReduceW4 && (a.N & 7) == 0 && ((uintptr_t)a.partials & 15) == 0 &&
       ((uintptr_t)a.out & 15) == 0 && ((uintptr_t)a.wscale & 15) == 0 &&
       (!a.acc_out || ((uintptr_t)a.acc_out & 15) == 0)) {

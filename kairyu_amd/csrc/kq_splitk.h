@@ -25,6 +25,9 @@ struct ReduceArgs {
   void* out;
   int out_dtype;
   int32_t* acc_out;      // I8: optional raw accumulators
+  // W8A8: N = 2I packed gate / up columns; out [M][I] = silu(gate) * up of
+  // column c and I + c (the elementwise pass's roundings); no acc_out
+  int swiglu;
 };
 
 // Launches the reduce kernel on `stream` (grid over M*N, 4 outputs/thread).

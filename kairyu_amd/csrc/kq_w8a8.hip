@@ -83,10 +83,10 @@ KQ_DEV int swiglu_row(int t, int r, int I) {
 // The decode epilogue with SwiGLU: the store epilogue's ((acc * xs) * ws) +
 // bias for both columns of a pair, then swiglu_bits (the elementwise pass's
 // roundings) -- the bits of the packed linear followed by kq_swiglu.  Lane
-// (j, kg) holds column j of tile t for rows 4kg..4kg+3; all 64 lanes take part
-// (the pair exchange is a cross-lane read).
+// (j, kg) holds column j of tile t for rows m0 + 4kg .. m0 + 4kg + 3; all 64
+// lanes take part (the pair exchange is a cross-lane read).
 template <int FMT>
-KQ_DEV void epi_swiglu(const Epi& ep, const float* xs, int t, int j, int kg,
+KQ_DEV void epi_swiglu(const Epi& ep, const float* xs, int t, int m0, int j, int kg,
                        typename W8Traits<FMT>::Acc acc) {
   const int I = ep.N >> 1;
   const int n = swiglu_row(t, j, I);
@@ -94,7 +94,7 @@ KQ_DEV void epi_swiglu(const Epi& ep, const float* xs, int t, int j, int kg,
   const float b = n >= 0 && ep.bias_dtype != KQ_DTYPE_NONE ? load_as_f32(ep.bias, ep.bias_dtype, n) : 0.0f;
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
-    const int m = kg * 4 + r;
+    const int m = m0 + kg * 4 + r;
     float v = 0.0f;
     if (n >= 0 && m < ep.M) {
       v = __fmul_rn(__fmul_rn((float)acc[r], xs[m]), ws);
@@ -148,7 +148,10 @@ KQ_DEV T ldb(const void* base, uint32_t byte_off) {
 
 // PRED = false: K is a multiple of the MFMA step, so loads need no guards
 // (rows beyond M / N are clamped to valid memory and never stored).
-template <int FMT, int MT, int U, bool PRED>
+// SW: the SwiGLU epilogue (Epi::swiglu) with the weight rows of swiglu_row;
+// split partials go to the [M][2I] plane by weight row, and the reduce pairs
+// gate column c with up column I + c.
+template <int FMT, int MT, int U, bool PRED, bool SW>
 __global__ void __launch_bounds__(64 * kSkinnyWaves)
 w8a8_skinny_kernel(const uint8_t* __restrict__ xq, const uint8_t* __restrict__ w, int K,
                    int steps_per_split, int splits, Epi ep, void* __restrict__ partials) {
@@ -160,8 +163,8 @@ w8a8_skinny_kernel(const uint8_t* __restrict__ xq, const uint8_t* __restrict__ w
   const int wave = __builtin_amdgcn_readfirstlane(wave_id());
   const int j = lane & 15, kg = lane >> 4;
   const int tile = blockIdx.x / splits, split = blockIdx.x % splits;
-  const int n = tile * kSkinnyCols + j;
-  const bool n_ok = n < ep.N;
+  const int n = SW ? swiglu_row(tile, j, ep.N >> 1) : tile * kSkinnyCols + j;
+  const bool n_ok = SW ? n >= 0 : n < ep.N;
   const int nsteps = (K + T::kStep - 1) / T::kStep;
   const int sbeg = split * steps_per_split;
   const int send = min(nsteps, sbeg + steps_per_split);
@@ -244,9 +247,14 @@ w8a8_skinny_kernel(const uint8_t* __restrict__ xq, const uint8_t* __restrict__ w
 
   if (splits == 1) {
 #pragma unroll
-    for (int t = 0; t < MT; ++t)
+    for (int t = 0; t < MT; ++t) {
+      if constexpr (SW) {
+        epi_swiglu<FMT>(ep, ep.xscale, tile, t * 16, j, kg, acc[t]);
+      } else {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) epi_store<FMT>(ep, t * 16 + kg * 4 + r, n, acc[t], r);
+        for (int r = 0; r < 4; ++r) epi_store<FMT>(ep, t * 16 + kg * 4 + r, n, acc[t], r);
+      }
+    }
     return;
   }
   uint32_t* part = (uint32_t*)partials + (size_t)split * ep.M * ep.N;
@@ -369,7 +377,7 @@ w8a8_decode_kernel(const uint8_t* __restrict__ xq, const uint8_t* __restrict__ w
       else acc[r] = __fadd_rn(acc[r], __uint_as_float(bits));
     }
   if constexpr (SW) {
-    epi_swiglu<FMT>(ep, ep.xscale, (int)blockIdx.x, j, kg, acc);
+    epi_swiglu<FMT>(ep, ep.xscale, (int)blockIdx.x, 0, j, kg, acc);
   } else {
 #pragma unroll
     for (int r = 0; r < 4; ++r) epi_store<FMT>(ep, kg * 4 + r, n0 + j, acc, r);
@@ -643,7 +651,7 @@ w8a8_decode_quant_kernel(const uint16_t* __restrict__ x, int x_dtype, int ldx, i
       else acc[r] = __fadd_rn(acc[r], __uint_as_float(bits));
     }
   if constexpr (SW) {
-    epi_swiglu<FMT>(ep, srow, (int)blockIdx.x, j, kg, acc);
+    epi_swiglu<FMT>(ep, srow, (int)blockIdx.x, 0, j, kg, acc);
     return;
   }
   const int n = n0 + j;
@@ -835,7 +843,8 @@ template <int FMT, int MT>
 static void launch_skinny(const uint8_t* xq, const uint8_t* w, int K, const Epi& ep,
                           void* workspace, size_t ws_bytes, hipStream_t stream) {
   using T = W8Traits<FMT>;
-  const int tiles = (ep.N + kSkinnyCols - 1) / kSkinnyCols;
+  // (SwiGLU: 8 gate + 8 up rows per tile, as many tiles)
+  const int tiles = ep.swiglu ? (ep.N / 2 + 7) / 8 : (ep.N + kSkinnyCols - 1) / kSkinnyCols;
   const int nsteps = (K + T::kStep - 1) / T::kStep;
   // Fill the 256 CUs: split K across workgroups only when there are fewer
   // tiles than CUs and every wave keeps >= 2 MFMA steps.
@@ -846,17 +855,21 @@ static void launch_skinny(const uint8_t* xq, const uint8_t* w, int K, const Epi&
     splits *= 2;
   const int steps_per_split = (nsteps + splits - 1) / splits;
   constexpr int U = MT == 4 ? (FMT == kFmtI8 ? 2 : 1) : (FMT == kFmtI8 ? 4 : 2);
-  if (K % T::kStep == 0)
-    hipLaunchKernelGGL((w8a8_skinny_kernel<FMT, MT, U, false>), dim3(tiles * splits),
-                       dim3(64 * kSkinnyWaves), 0, stream, xq, w, K, steps_per_split, splits, ep,
-                       workspace);
-  else
-    hipLaunchKernelGGL((w8a8_skinny_kernel<FMT, MT, U, true>), dim3(tiles * splits),
-                       dim3(64 * kSkinnyWaves), 0, stream, xq, w, K, steps_per_split, splits, ep,
-                       workspace);
+#define KQ_SKINNY(PRED, SW)                                                                   \
+  hipLaunchKernelGGL((w8a8_skinny_kernel<FMT, MT, U, PRED, SW>), dim3(tiles * splits),        \
+                     dim3(64 * kSkinnyWaves), 0, stream, xq, w, K, steps_per_split, splits, ep, \
+                     workspace)
+  if (K % T::kStep == 0) {
+    if (ep.swiglu) KQ_SKINNY(false, true);
+    else KQ_SKINNY(false, false);
+  } else {
+    if (ep.swiglu) KQ_SKINNY(true, true);
+    else KQ_SKINNY(true, false);
+  }
+#undef KQ_SKINNY
   if (splits > 1) {
     ReduceArgs r{workspace, splits, ep.M, ep.N, ep.xscale, ep.wscale, ep.ws_per_channel,
-                 ep.bias, ep.bias_dtype, ep.out, ep.out_dtype, ep.acc_out};
+                 ep.bias, ep.bias_dtype, ep.out, ep.out_dtype, ep.acc_out, ep.swiglu};
     launch_splitk_reduce(FMT == kFmtI8 ? kReduceI8 : kReduceFp8, r, stream);
   }
 }
@@ -903,10 +916,10 @@ static int run_w8a8(const char* what, const uint8_t* xq, const uint8_t* w, int64
   }
   if (m == 0) return KQ_OK;
   const int K = (int)k;
-  if (ep.swiglu && !(m <= 16 && K % 128 == 0 && ((uintptr_t)xq % 16) == 0 && ((uintptr_t)w % 16) == 0 &&
-                     n * k < ((int64_t)1 << 31))) {
-    set_error("%s: the SwiGLU epilogue runs in the decode kernels only (m=%lld k=%lld)", what,
-              (long long)m, (long long)k);
+  if (ep.swiglu && !(m <= 64 && K % 16 == 0 && ((uintptr_t)xq % 16) == 0 && ((uintptr_t)w % 16) == 0 &&
+                     n * k < ((int64_t)1 << 31) && m * k < ((int64_t)1 << 31))) {
+    set_error("%s: the SwiGLU epilogue runs in the decode and skinny kernels only (m=%lld k=%lld)",
+              what, (long long)m, (long long)k);
     return KQ_EINVAL;
   }
   if ((K % 16) != 0 || ((uintptr_t)xq % 16) || ((uintptr_t)w % 16)) {
@@ -1092,11 +1105,12 @@ extern "C" int kq_w8a8_fp8_linear(const void* x, int x_dtype, int64_t ldx, const
 // Prefill shapes (M > 64, I % 128 == 0, enough 256 x 256 tiles for half the
 // CUs) run the tile engine with the SwiGLU store epilogue: each tile pairs
 // gate columns [n0, n0 + 128) with up columns [I + n0, I + n0 + 128), so the
-// [M, 2I] projection output never reaches memory.  Decode shapes (M <= 16,
-// K % 128 == 0) run the decode kernels with the SwiGLU epilogue (each
-// workgroup's 16 weight rows are 8 gate rows and the matching 8 up rows).
-// Other shapes run the packed linear into the workspace and the elementwise
-// pass.  All produce the bits of the packed linear followed by kq_swiglu.
+// [M, 2I] projection output never reaches memory.  Shapes of M <= 64 (FP8:
+// M <= 32) run the decode or skinny kernels with the SwiGLU epilogue (each workgroup's 16
+// weight rows are 8 gate rows and the matching 8 up rows; split-K partials
+// meet in the reduce, which pairs the columns).  Other shapes run the packed
+// linear into the workspace and the elementwise pass.  All produce the bits
+// of the packed linear followed by kq_swiglu.
 static bool swiglu_fused_applies(int64_t m, int64_t i_width, int64_t k, const void* x, int64_t ldx,
                                  const void* w) {
   if (m <= 64 || i_width % 128 != 0 || k % 16 != 0 || ((uintptr_t)w % 16) != 0) return false;
@@ -1146,10 +1160,16 @@ static int run_swiglu_linear(const char* what, const void* x, int x_dtype, int64
     tg_launch<FMT == kFmtI8 ? kTgI8 : kTgFp8, false, kTgEpiSwiGluStore>(a, stream);
     return check_launch(what);
   }
-  if (m >= 1 && m <= 16 && k % 128 == 0 && k <= 65536 && ((uintptr_t)w % 16) == 0 &&
+  // FP8 at M = 33..64 (four 16-row tiles per skinny workgroup) keeps the two
+  // passes: with the paired rows it measured 8-11% slower (same process,
+  // bit-identical; I = 11008 / 14336 / 18944, K = 4096 / 3584, M = 48 and 64:
+  // e.g. I = 14336 M = 64 105 -> 114 us), while INT8 there and both formats
+  // up to M = 32 measured faster.
+  const int64_t fused_max_m = FMT == kFmtFp8 ? 32 : 64;
+  if (m >= 1 && m <= fused_max_m && k % 16 == 0 && k <= 65536 && ((uintptr_t)w % 16) == 0 &&
       ((uintptr_t)workspace % 16) == 0 && n * k < ((int64_t)1 << 31)) {
-    // decode shapes: the decode kernels (one-row fused quantization or the
-    // per-token quantizer first) with the SwiGLU epilogue
+    // decode shapes: the decode or skinny kernels (one-row fused quantization
+    // or the per-token quantizer first) with the SwiGLU epilogue
     ep.swiglu = 1;
     return run_linear<FMT>(what, x, x_dtype, ldx, scale_mode, scale_in, w, m, n, k, ep, workspace,
                            ws_bytes, stream);
