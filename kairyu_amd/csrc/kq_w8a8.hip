@@ -135,9 +135,14 @@ KQ_DEV typename W8Traits<FMT>::Acc mfma_w8(typename W8Traits<FMT>::Frag a,
 }
 
 // ------------------------------------------------------------------ skinny
-// Workgroup = 16 output columns x a K range; its waves split the K range and
-// reduce through LDS.  Lane (j, kg) streams 16 (INT8) or 32 (FP8) contiguous
-// weight bytes of row n = tile*16 + j straight into the MFMA B operand.
+// Workgroup = NT tiles of 16 output columns x a K range; its waves split the
+// K range.  Lane (j, kg) streams 16 (INT8) or 32 (FP8) contiguous weight
+// bytes of row n = ct*16 + j of each column tile ct straight into the MFMA B
+// operand, and each activation fragment (MT row tiles of 16) feeds the NT
+// column tiles' MFMAs: the activation rows of a K range are read once per NT
+// column tiles (x is re-read by every workgroup of a K range, so NT divides
+// that traffic).  The waves' partial sums meet in LDS; the wave that owns a
+// 16 x 16 block adds the eight partials in wave order (fixed order).
 constexpr int kSkinnyWaves = 8;
 constexpr int kSkinnyCols = 16;
 
@@ -151,20 +156,26 @@ KQ_DEV T ldb(const void* base, uint32_t byte_off) {
 // SW: the SwiGLU epilogue (Epi::swiglu) with the weight rows of swiglu_row;
 // split partials go to the [M][2I] plane by weight row, and the reduce pairs
 // gate column c with up column I + c.
-template <int FMT, int MT, int U, bool PRED, bool SW>
+template <int FMT, int MT, int NT, int U, bool PRED, bool SW>
 __global__ void __launch_bounds__(64 * kSkinnyWaves)
 w8a8_skinny_kernel(const uint8_t* __restrict__ xq, const uint8_t* __restrict__ w, int K,
                    int steps_per_split, int splits, Epi ep, void* __restrict__ partials) {
   using T = W8Traits<FMT>;
   using Acc = typename T::Acc;
   using Frag = typename T::Frag;
-  __shared__ uint32_t red[(kSkinnyWaves - 1) * MT * 4 * 64];
+  constexpr int NB = MT * NT;  // 16 x 16 output blocks of a workgroup
+  __shared__ uint32_t red[kSkinnyWaves * NB * 4 * 64];
   const int lane = lane_id();
   const int wave = __builtin_amdgcn_readfirstlane(wave_id());
   const int j = lane & 15, kg = lane >> 4;
-  const int tile = blockIdx.x / splits, split = blockIdx.x % splits;
-  const int n = SW ? swiglu_row(tile, j, ep.N >> 1) : tile * kSkinnyCols + j;
-  const bool n_ok = SW ? n >= 0 : n < ep.N;
+  const int tile = blockIdx.x / splits, split = blockIdx.x % splits;  // tile: NT column tiles
+  const int I = ep.N >> 1;
+  auto col_of = [&](int nt) -> int {  // weight row of lane column j in column tile nt, -1: none
+    const int ct = tile * NT + nt;
+    if constexpr (SW) return swiglu_row(ct, j, I);
+    const int n = ct * kSkinnyCols + j;
+    return n < ep.N ? n : -1;
+  };
   const int nsteps = (K + T::kStep - 1) / T::kStep;
   const int sbeg = split * steps_per_split;
   const int send = min(nsteps, sbeg + steps_per_split);
@@ -172,14 +183,21 @@ w8a8_skinny_kernel(const uint8_t* __restrict__ xq, const uint8_t* __restrict__ w
   const int wbeg = sbeg + wave * per_wave;
   const int wend = min(send, wbeg + per_wave);
   // loop-invariant 32-bit byte offsets (rows clamped to valid memory)
-  const uint32_t w_boff = (uint32_t)((n_ok ? n : ep.N - 1) * K + kg * T::kLane);
+  uint32_t w_boff[NT];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    const int n = col_of(nt);
+    w_boff[nt] = (uint32_t)((n >= 0 ? n : ep.N - 1) * K + kg * T::kLane);
+  }
   uint32_t x_boff[MT];
 #pragma unroll
   for (int t = 0; t < MT; ++t) x_boff[t] = (uint32_t)(min(t * 16 + j, ep.M - 1) * K + kg * T::kLane);
 
-  Acc acc[MT];
+  Acc acc[MT][NT];
 #pragma unroll
-  for (int t = 0; t < MT; ++t) acc[t] = Acc{0, 0, 0, 0};
+  for (int t = 0; t < MT; ++t)
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) acc[t][nt] = Acc{0, 0, 0, 0};
 
   auto frag = [&](const uint8_t* base, uint32_t off, int k) -> Frag {
     if constexpr (!PRED) {
@@ -195,7 +213,7 @@ w8a8_skinny_kernel(const uint8_t* __restrict__ xq, const uint8_t* __restrict__ w
   };
   // two register batches of U steps: load batch b+1 while computing batch b
   struct Batch {
-    Frag b[U];
+    Frag b[U][NT];
     Frag a[U][MT];
   };
   auto load = [&](Batch& bt, int st0) {
@@ -203,7 +221,8 @@ w8a8_skinny_kernel(const uint8_t* __restrict__ xq, const uint8_t* __restrict__ w
     for (int u = 0; u < U; ++u) {
       const int st = min(st0 + u, wend - 1);  // surplus steps reload; never computed
       const int k = st * T::kStep + kg * T::kLane;
-      bt.b[u] = frag(w + (int64_t)st * T::kStep, w_boff, k);
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) bt.b[u][nt] = frag(w + (int64_t)st * T::kStep, w_boff[nt], k);
 #pragma unroll
       for (int t = 0; t < MT; ++t) bt.a[u][t] = frag(xq + (int64_t)st * T::kStep, x_boff[t], k);
     }
@@ -213,7 +232,9 @@ w8a8_skinny_kernel(const uint8_t* __restrict__ xq, const uint8_t* __restrict__ w
     for (int u = 0; u < U; ++u) {
       if (st0 + u >= wend) break;
 #pragma unroll
-      for (int t = 0; t < MT; ++t) acc[t] = mfma_w8<FMT>(bt.a[u][t], bt.b[u], acc[t]);
+      for (int t = 0; t < MT; ++t)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) acc[t][nt] = mfma_w8<FMT>(bt.a[u][t], bt.b[u][nt], acc[t][nt]);
     }
   };
   Batch b0, b1;
@@ -225,46 +246,47 @@ w8a8_skinny_kernel(const uint8_t* __restrict__ xq, const uint8_t* __restrict__ w
     compute(b1, st + U);
   }
 
-  // fixed-order reduction of the waves' K ranges
-  if (wave > 0) {
-#pragma unroll
-    for (int t = 0; t < MT; ++t)
-#pragma unroll
-      for (int r = 0; r < 4; ++r)
-        red[(((wave - 1) * MT + t) * 4 + r) * 64 + lane] = acc_bits(acc[t], r);
-  }
-  __syncthreads();
-  if (wave != 0) return;
-  for (int w2 = 1; w2 < kSkinnyWaves; ++w2)
-#pragma unroll
-    for (int t = 0; t < MT; ++t)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const uint32_t bits = red[(((w2 - 1) * MT + t) * 4 + r) * 64 + lane];
-        if constexpr (FMT == kFmtI8) acc[t][r] += (int)bits;
-        else acc[t][r] = __fadd_rn(acc[t][r], __uint_as_float(bits));
-      }
-
-  if (splits == 1) {
-#pragma unroll
-    for (int t = 0; t < MT; ++t) {
-      if constexpr (SW) {
-        epi_swiglu<FMT>(ep, ep.xscale, tile, t * 16, j, kg, acc[t]);
-      } else {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) epi_store<FMT>(ep, t * 16 + kg * 4 + r, n, acc[t], r);
-      }
-    }
-    return;
-  }
-  uint32_t* part = (uint32_t*)partials + (size_t)split * ep.M * ep.N;
+  // fixed-order reduction of the waves' K ranges: every wave parks its
+  // partials, then the owner of block b (wave b % 8) adds waves 0..7 in order
 #pragma unroll
   for (int t = 0; t < MT; ++t)
 #pragma unroll
+    for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) red[((wave * NB + t * NT + nt) * 4 + r) * 64 + lane] = acc_bits(acc[t][nt], r);
+  __syncthreads();
+  for (int bk = wave; bk < NB; bk += kSkinnyWaves) {
+    const int t = bk / NT, nt = bk - t * NT;
+    Acc v;
+#pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int m = t * 16 + kg * 4 + r;
-      if (m < ep.M && n_ok) part[(int64_t)m * ep.N + n] = acc_bits(acc[t], r);
+      const uint32_t b0 = red[((0 * NB + bk) * 4 + r) * 64 + lane];
+      if constexpr (FMT == kFmtI8) v[r] = (int)b0;
+      else v[r] = __uint_as_float(b0);
+      for (int w2 = 1; w2 < kSkinnyWaves; ++w2) {
+        const uint32_t bits = red[((w2 * NB + bk) * 4 + r) * 64 + lane];
+        if constexpr (FMT == kFmtI8) v[r] += (int)bits;
+        else v[r] = __fadd_rn(v[r], __uint_as_float(bits));
+      }
     }
+    const int n = col_of(nt);
+    if (splits == 1) {
+      if constexpr (SW) {
+        epi_swiglu<FMT>(ep, ep.xscale, tile * NT + nt, t * 16, j, kg, v);
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (n >= 0) epi_store<FMT>(ep, t * 16 + kg * 4 + r, n, v, r);
+      }
+    } else {
+      uint32_t* part = (uint32_t*)partials + (size_t)split * ep.M * ep.N;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int m = t * 16 + kg * 4 + r;
+        if (m < ep.M && n >= 0) part[(int64_t)m * ep.N + n] = acc_bits(v, r);
+      }
+    }
+  }
 }
 
 // ------------------------------------------------------------------ decode
@@ -839,33 +861,61 @@ __global__ void w8a8_generic_kernel(const uint8_t* __restrict__ xq, const uint8_
 }
 
 // ------------------------------------------------------------------ host
+// Column tiles per skinny workgroup: with MT >= 2 activation row tiles the
+// activation traffic of a K range (every workgroup reads all its rows)
+// outweighs the weights', so NT column tiles share each activation fragment:
+// 4, or 2 for FP8 with four row tiles (its 32-byte fragments in two register
+// batches would spill at 4); the one-row-tile form (M <= 16 with K % 128 !=
+// 0) keeps NT = 1.  kSkinnyNT (the largest) bounds the split count.
+constexpr int kSkinnyNT = 4;
+template <int FMT, int MT>
+constexpr int skinny_nt() {
+  return MT == 1 ? 1 : (FMT == kFmtFp8 && MT == 4 ? 2 : kSkinnyNT);
+}
+
 template <int FMT, int MT>
 static void launch_skinny(const uint8_t* xq, const uint8_t* w, int K, const Epi& ep,
                           void* workspace, size_t ws_bytes, hipStream_t stream) {
   using T = W8Traits<FMT>;
-  // (SwiGLU: 8 gate + 8 up rows per tile, as many tiles)
-  const int tiles = ep.swiglu ? (ep.N / 2 + 7) / 8 : (ep.N + kSkinnyCols - 1) / kSkinnyCols;
+  constexpr int NTG = skinny_nt<FMT, MT>();
+  // (SwiGLU: 8 gate + 8 up rows per column tile, as many tiles)
+  const int ctiles = ep.swiglu ? (ep.N / 2 + 7) / 8 : (ep.N + kSkinnyCols - 1) / kSkinnyCols;
   const int nsteps = (K + T::kStep - 1) / T::kStep;
+  const size_t plane = (size_t)ep.M * ep.N * 4;
   // Fill the 256 CUs: split K across workgroups only when there are fewer
   // tiles than CUs and every wave keeps >= 2 MFMA steps.
-  int splits = 1;
-  const size_t plane = (size_t)ep.M * ep.N * 4;
-  while (workspace && tiles * splits < 256 && nsteps / (splits * 2 * kSkinnyWaves) >= 2 &&
-         plane * splits * 2 <= ws_bytes)
-    splits *= 2;
+  auto splits_for = [&](int tiles) {
+    int s = 1;
+    while (workspace && tiles * s < 256 && nsteps / (s * 2 * kSkinnyWaves) >= 2 &&
+           plane * s * 2 <= ws_bytes)
+      s *= 2;
+    return s;
+  };
+  // Grouped column tiles only where they keep as many workgroups as single
+  // tiles do (up to 256): a small N leaves too few (N = 1024, K = 4096,
+  // FP8 M = 32: 32 workgroups, 8.5 -> 11.1 us).
+  const int tiles_g = (ctiles + NTG - 1) / NTG, splits_g = splits_for(tiles_g);
+  const int splits_1 = splits_for(ctiles);
+  const bool grouped = NTG > 1 && tiles_g * splits_g >= std::min(256, ctiles * splits_1);
+  const int tiles = grouped ? tiles_g : ctiles, splits = grouped ? splits_g : splits_1;
   const int steps_per_split = (nsteps + splits - 1) / splits;
-  constexpr int U = MT == 4 ? (FMT == kFmtI8 ? 2 : 1) : (FMT == kFmtI8 ? 4 : 2);
-#define KQ_SKINNY(PRED, SW)                                                                   \
-  hipLaunchKernelGGL((w8a8_skinny_kernel<FMT, MT, U, PRED, SW>), dim3(tiles * splits),        \
+  constexpr int U1 = MT == 4 ? (FMT == kFmtI8 ? 2 : 1) : (FMT == kFmtI8 ? 4 : 2);
+  constexpr int UG = FMT == kFmtI8 ? 2 : 1;
+#define KQ_SKINNY(NT, U, PRED, SW)                                                                \
+  hipLaunchKernelGGL((w8a8_skinny_kernel<FMT, MT, NT, U, PRED, SW>), dim3(tiles * splits),        \
                      dim3(64 * kSkinnyWaves), 0, stream, xq, w, K, steps_per_split, splits, ep, \
                      workspace)
+#define KQ_SKINNY_NT(PRED, SW)             \
+  if (grouped) KQ_SKINNY(NTG, UG, PRED, SW); \
+  else KQ_SKINNY(1, U1, PRED, SW);
   if (K % T::kStep == 0) {
-    if (ep.swiglu) KQ_SKINNY(false, true);
-    else KQ_SKINNY(false, false);
+    if (ep.swiglu) { KQ_SKINNY_NT(false, true) }
+    else { KQ_SKINNY_NT(false, false) }
   } else {
-    if (ep.swiglu) KQ_SKINNY(true, true);
-    else KQ_SKINNY(true, false);
+    if (ep.swiglu) { KQ_SKINNY_NT(true, true) }
+    else { KQ_SKINNY_NT(true, false) }
   }
+#undef KQ_SKINNY_NT
 #undef KQ_SKINNY
   if (splits > 1) {
     ReduceArgs r{workspace, splits, ep.M, ep.N, ep.xscale, ep.wscale, ep.ws_per_channel,
@@ -1034,8 +1084,10 @@ extern "C" size_t kq_w8a8_workspace_size(int64_t m, int64_t n, int64_t k) {
   const size_t plane = (size_t)m * (size_t)n * 4;
   if (m <= 64) {
     // skinny split-K as launch_skinny doubles it (the INT8 K step is the
-    // smaller one, so it bounds both formats)
-    const int64_t tiles = (n + kSkinnyCols - 1) / kSkinnyCols;
+    // smaller one, so it bounds both formats; M > 16 groups kSkinnyNT column
+    // tiles per workgroup)
+    const int64_t ctiles = (n + kSkinnyCols - 1) / kSkinnyCols;
+    const int64_t tiles = m > 16 ? (ctiles + kSkinnyNT - 1) / kSkinnyNT : ctiles;
     const int64_t nsteps = (k + W8Traits<kFmtI8>::kStep - 1) / W8Traits<kFmtI8>::kStep;
     int64_t s = 1;
     while (tiles * s < 256 && nsteps / (s * 2 * kSkinnyWaves) >= 2) s *= 2;
@@ -1105,8 +1157,8 @@ extern "C" int kq_w8a8_fp8_linear(const void* x, int x_dtype, int64_t ldx, const
 // Prefill shapes (M > 64, I % 128 == 0, enough 256 x 256 tiles for half the
 // CUs) run the tile engine with the SwiGLU store epilogue: each tile pairs
 // gate columns [n0, n0 + 128) with up columns [I + n0, I + n0 + 128), so the
-// [M, 2I] projection output never reaches memory.  Shapes of M <= 64 (FP8:
-// M <= 32) run the decode or skinny kernels with the SwiGLU epilogue (each workgroup's 16
+// [M, 2I] projection output never reaches memory.  Shapes of M <= 64 run the
+// decode or skinny kernels with the SwiGLU epilogue (each workgroup's 16
 // weight rows are 8 gate rows and the matching 8 up rows; split-K partials
 // meet in the reduce, which pairs the columns).  Other shapes run the packed
 // linear into the workspace and the elementwise pass.  All produce the bits
@@ -1160,13 +1212,7 @@ static int run_swiglu_linear(const char* what, const void* x, int x_dtype, int64
     tg_launch<FMT == kFmtI8 ? kTgI8 : kTgFp8, false, kTgEpiSwiGluStore>(a, stream);
     return check_launch(what);
   }
-  // FP8 at M = 33..64 (four 16-row tiles per skinny workgroup) keeps the two
-  // passes: with the paired rows it measured 8-11% slower (same process,
-  // bit-identical; I = 11008 / 14336 / 18944, K = 4096 / 3584, M = 48 and 64:
-  // e.g. I = 14336 M = 64 105 -> 114 us), while INT8 there and both formats
-  // up to M = 32 measured faster.
-  const int64_t fused_max_m = FMT == kFmtFp8 ? 32 : 64;
-  if (m >= 1 && m <= fused_max_m && k % 16 == 0 && k <= 65536 && ((uintptr_t)w % 16) == 0 &&
+  if (m >= 1 && m <= 64 && k % 16 == 0 && k <= 65536 && ((uintptr_t)w % 16) == 0 &&
       ((uintptr_t)workspace % 16) == 0 && n * k < ((int64_t)1 << 31)) {
     // decode shapes: the decode or skinny kernels (one-row fused quantization
     // or the per-token quantizer first) with the SwiGLU epilogue

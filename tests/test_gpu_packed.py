@@ -136,9 +136,9 @@ def test_pack_graph_replays_match_eager(cuda):
 # W4A16: one kq_w4a16_tiled_swiglu_gemm call; decode shapes (here N = 2 x 4096
 # on K = 4096) apply SwiGLU in the GEMV epilogue, others run the tiled GEMM
 # and the elementwise pass.  W8A8: one kq_w8a8_*_swiglu_linear call; prefill
-# shapes apply SwiGLU in the tile engine's epilogue, M <= 64 (FP8: 32) in
-# the decode or skinny GEMM's (or their split-K reduce), others run the
-# packed GEMM and kq_swiglu.
+# shapes apply SwiGLU in the tile engine's epilogue, M <= 64 in the decode
+# or skinny GEMM's (or their split-K reduce), others run the packed GEMM and
+# kq_swiglu.
 _SWIGLU_CASES = [
     # (scheme, m, k, width, dtype, bias)
     ("gptq", 1, 4096, 4096, torch.float16, False),
@@ -173,7 +173,7 @@ _SWIGLU_CASES = [
     # M = 17-64 (skinny kernel): one K range per tile, and split K whose
     # reduce pairs the columns
     ("fp8", 32, 4096, 14336, torch.bfloat16, True),
-    ("fp8", 40, 4096, 2048, torch.float16, False),     # FP8 M = 33-64: two passes
+    ("fp8", 40, 4096, 2048, torch.float16, False),
     ("int8", 33, 8192, 512, torch.bfloat16, False),
     # prefill shapes: SwiGLU in the tile engine's epilogue (>= 128 tiles of 256 x 256)
     ("fp8", 1024, 1024, 4096, torch.bfloat16, True),
@@ -299,6 +299,8 @@ def test_swiglu_pack_rejects_diverged_g_idx(cuda):
     # skinny kernel (M = 17-64, or K % 128 != 0): one K range per tile,
     # 2- and 4-way split K (reduce with SwiGLU), ragged K steps
     ("fp8", 32, 4096, 14336, torch.bfloat16, True),
+    ("fp8", 64, 4096, 14336, torch.bfloat16, False),
+    ("fp8", 48, 14336, 1024, torch.float16, True),
     ("fp8", 32, 14336, 1024, torch.float16, True),
     ("fp8", 16, 4112, 2048, torch.bfloat16, False),
     ("fp8-static", 24, 4096, 1000, torch.float16, True),

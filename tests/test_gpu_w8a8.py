@@ -440,6 +440,28 @@ def test_fp8_activation_quantization_bit_exact(cuda, mode):
     assert np.array_equal(np32(s), es)
 
 
+# Skinny kernel with grouped column tiles (M = 17..64 where grouping keeps
+# the CUs filled): N = 4100 leaves a last group with one live column tile
+# (257 tiles), K = 8192 splits K 2-4 ways; 2 (FP8 M > 32) or 4 tiles a group.
+@pytest.mark.parametrize("fmt,m", [("int8", 17), ("int8", 40), ("int8", 64),
+                                   ("fp8", 24), ("fp8", 33), ("fp8", 64)])
+def test_grouped_skinny_matches_oracle(cuda, fmt, m):
+    n, k = 4100, 8192
+    banner(f"{fmt} grouped skinny m={m}")
+    x = torch.randn(m, k, generator=torch.Generator().manual_seed(5 * m)).to(torch.bfloat16)
+    if fmt == "int8":
+        module = _int8_module(k, n, seed=m).to(cuda)
+        acc = torch.empty(m, n, dtype=torch.int32, device=cuda)
+        out = hip.int8_linear_forward(x.to(cuda), module, accumulators=acc)
+        expected, xq, xs, eacc = olinear.int8_forward(
+            np32(x), module.weight.cpu().numpy(), module.weight_scale.cpu().numpy(), np32(module.bias))
+        assert np.array_equal(acc.cpu().numpy().astype(np.int64), eacc)
+        assert np.array_equal(np32(out), expected)
+    else:
+        module = _fp8_module(k, n, seed=m).to(cuda)
+        check_fp8(module(x.to(cuda)), x, module, label=f"grouped m={m}")
+
+
 @pytest.mark.parametrize("m", [1, 7, 16, 24, 48, 64, 96, 300])
 def test_fp8_output_matches_oracle_all_paths(cuda, m):
     n, k = 192, 14336 // 4
