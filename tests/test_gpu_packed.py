@@ -248,6 +248,34 @@ def test_swiglu_pack_in_a_graph(cuda):
         assert torch.equal(out, eager)
 
 
+@pytest.mark.parametrize("scheme,m,k,width", [("fp8", 16, 4096, 4096), ("fp8", 40, 14336, 1024),
+                                               ("int8", 24, 3584, 2048)])
+def test_w8a8_swiglu_pack_in_a_graph(cuda, scheme, m, k, width):
+    """W8A8 decode / skinny GEMMs with the SwiGLU epilogue (and, at K = 14336,
+    the split-K reduce that pairs the columns) captured once, replayed with
+    eager work between the replays, every replay equal to the eager call."""
+
+    gate, up = (mod.to(cuda) for mod in _swiglu_pair(scheme, k, width, True, seed=m + k))
+    pack = QuantLinearPack.create([gate, up])
+    x = torch.randn(m, k, generator=torch.Generator().manual_seed(m)).to(torch.bfloat16).to(cuda)
+    eager = pack.swiglu(x).clone()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        pack.swiglu(x)
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = pack.swiglu(x)
+    other = torch.randn(m, k, generator=torch.Generator().manual_seed(m + 1)).to(torch.bfloat16).to(cuda)
+    for _ in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager)
+        pack.swiglu(other)  # eager work between replays reuses the workspace
+        torch.cuda.synchronize()
+
+
 @pytest.mark.parametrize("scheme", ["gptq-ao", "awq"])
 def test_swiglu_pack_holds_the_only_tiled_copy(cuda, scheme):
     """After ``pack.swiglu`` neither projection keeps a tiled operand of its
