@@ -864,13 +864,17 @@ __global__ void w8a8_generic_kernel(const uint8_t* __restrict__ xq, const uint8_
 // Column tiles per skinny workgroup: with MT >= 2 activation row tiles the
 // activation traffic of a K range (every workgroup reads all its rows)
 // outweighs the weights', so NT column tiles share each activation fragment:
-// 4, or 2 for FP8 with four row tiles (its 32-byte fragments in two register
-// batches would spill at 4); the one-row-tile form (M <= 16 with K % 128 !=
-// 0) keeps NT = 1.  kSkinnyNT (the largest) bounds the split count.
+// FP8 4 with two row tiles and 2 with four (its 32-byte fragments in two
+// register batches would spill at 4), INT8 2 with two row tiles and 4 with
+// four (measured, C4's N = 18944: INT8 M = 17 / 32 29.4 / 33.0 us at 4 and
+// 25.1 / 29.8 at 2, M = 64 43.3 at 4 and 45.7 at 2; FP8 N = 28672 M = 32 33.6
+// at 4 and 38.7 at 2); the one-row-tile form (M <= 16 with K % 128 != 0)
+// keeps NT = 1.  kSkinnyNT (the largest) bounds the split count.
 constexpr int kSkinnyNT = 4;
 template <int FMT, int MT>
 constexpr int skinny_nt() {
-  return MT == 1 ? 1 : (FMT == kFmtFp8 && MT == 4 ? 2 : kSkinnyNT);
+  if (MT == 1) return 1;
+  return (FMT == kFmtFp8) == (MT == 2) ? kSkinnyNT : 2;
 }
 
 template <int FMT, int MT>
