@@ -121,10 +121,11 @@ size_t kq_w8a8_linear_workspace_size(int64_t m, int64_t n, int64_t k);
  * rows), and out [m][i_width] (activation dtype) = silu(g) * u for gate
  * column c and up column i_width + c, with the roundings of
  * kq_w8a8_*_linear followed by kq_swiglu (bit-identical to that pair).
- * Prefill shapes apply SwiGLU in the tile engine's epilogue and decode shapes
- * (m <= 16, k % 128 == 0) in the decode GEMM's (the [m][2I] projection never
- * reaches memory); other shapes run the pair through the workspace.  Replaces the reference MLP's act_fn(gate(x)) * up(x)
- * (kairyu/models/layers.py:243-244) over its packed projections
+ * Prefill shapes apply SwiGLU in the tile engine's epilogue and shapes of
+ * m <= 64 in the decode or skinny GEMM's (or the reduce of their K splits):
+ * the [m][2I] projection never reaches memory; other shapes run the pair
+ * through the workspace.  Replaces the reference MLP's act_fn(gate(x)) *
+ * up(x) (kairyu/models/layers.py:243-244) over its packed projections
  * (kairyu/models/packed_linear.py:58-149) for FP8 / INT8 W8A8. */
 int kq_w8a8_i8_swiglu_linear(const void* x, int x_dtype, int64_t ldx, const int8_t* w,
                              const float* wscale, const void* bias, int bias_dtype, void* out,
@@ -240,8 +241,9 @@ int kq_w4a16_tiled_gemm(const void* x, int x_dtype, const int32_t* tiles, const 
  * columns in which 16-column blocks of gate (block b: gate columns 16b..16b+15)
  * and up alternate; qzeros / scales / bias (nullable) are in that column
  * order too.  Decode shapes (the GEMV's conditions, at most 8 column blocks
- * per CU) apply SwiGLU in the GEMV's epilogue; other shapes run the tiled
- * GEMM into the workspace and one elementwise pass
+ * per CU) apply SwiGLU in the GEMV's epilogue, or with K > 4096 in the reduce
+ * of its K chunks, and prefill shapes (M > 64) in the prefill GEMM's; other
+ * shapes run the tiled GEMM into the workspace and one elementwise pass
  * (kq_w4a16_swiglu_workspace_size bytes).  No reference counterpart: the
  * reference packs gate/up only for dense and NVFP4 projections
  * (kairyu/models/packed_linear.py:58-149) and applies SwiGLU separately. */

@@ -190,9 +190,12 @@ __global__ void __launch_bounds__(256) splitk_reduce8_kernel(ReduceArgs a) {
   *(u32x4*)((uint16_t*)a.out + base) = u32x4{o[0], o[1], o[2], o[3]};
 }
 
-// W8A8 with SwiGLU: thread = one output (m, c), gate column c and up column
-// I + c of the [M][2I] partial plane, each summed and scaled as above, then
-// swiglu_bits: the bits of the packed epilogue followed by kq_swiglu.
+// With SwiGLU: thread = one output (m, c); gate and up columns of the
+// [M][2I] partial plane (swiglu 1: c and I + c, the W8A8 packs; 2: gate and
+// up 16-column blocks alternating, (c / 16) * 32 + c % 16 and 16 on, the
+// W4A16 interleaved operand), each summed and scaled as above, then
+// swiglu_bits: the bits of the epilogue's store followed by the elementwise
+// pass.
 template <int MODE>
 __global__ void __launch_bounds__(256) splitk_reduce_swiglu_kernel(ReduceArgs a) {
   const int I = a.N / 2;
@@ -201,12 +204,15 @@ __global__ void __launch_bounds__(256) splitk_reduce_swiglu_kernel(ReduceArgs a)
   if (o >= (int64_t)a.M * I) return;
   const int m = (int)(o / I), c = (int)(o - (int64_t)m * I);
   const int64_t row = (int64_t)m * a.N;
+  const int ng = a.swiglu == 2 ? (c >> 4) * 32 + (c & 15) : c;
+  const int nu = a.swiglu == 2 ? ng + 16 : I + c;
   auto wscale = [&](int n) -> float {
-    return (MODE == kReduceI8 || a.ws_per_channel) ? a.wscale[n] : a.wscale[0];
+    if constexpr (MODE == kReduceW4) return 1.0f;
+    else return (MODE == kReduceI8 || a.ws_per_channel) ? a.wscale[n] : a.wscale[0];
   };
-  const float xs = a.xscale[m];
-  const float g = reduce_epilogue<MODE>(a, row + c, m, c, plane, xs, wscale(c));
-  const float u = reduce_epilogue<MODE>(a, row + I + c, m, I + c, plane, xs, wscale(I + c));
+  const float xs = MODE == kReduceW4 ? 1.0f : a.xscale[m];
+  const float g = reduce_epilogue<MODE>(a, row + ng, m, ng, plane, xs, wscale(ng));
+  const float u = reduce_epilogue<MODE>(a, row + nu, m, nu, plane, xs, wscale(nu));
   ((uint16_t*)a.out)[o] = swiglu_bits(g, u, a.out_dtype);
 }
 
@@ -215,7 +221,8 @@ void launch_splitk_reduce(int mode, const ReduceArgs& a, hipStream_t stream) {
   if (a.swiglu) {
     const dim3 g((unsigned)((total / 2 + 255) / 256)), b(256);
     if (mode == kReduceI8) hipLaunchKernelGGL(splitk_reduce_swiglu_kernel<kReduceI8>, g, b, 0, stream, a);
-    else hipLaunchKernelGGL(splitk_reduce_swiglu_kernel<kReduceFp8>, g, b, 0, stream, a);
+    else if (mode == kReduceFp8) hipLaunchKernelGGL(splitk_reduce_swiglu_kernel<kReduceFp8>, g, b, 0, stream, a);
+    else hipLaunchKernelGGL(splitk_reduce_swiglu_kernel<kReduceW4>, g, b, 0, stream, a);
     return;
   }
   if (mode != kReduceW4 && (a.N & 7) == 0 && ((uintptr_t)a.partials & 15) == 0 &&

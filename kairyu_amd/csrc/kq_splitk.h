@@ -25,8 +25,10 @@ struct ReduceArgs {
   void* out;
   int out_dtype;
   int32_t* acc_out;      // I8: optional raw accumulators
-  // W8A8: N = 2I packed gate / up columns; out [M][I] = silu(gate) * up of
-  // column c and I + c (the elementwise pass's roundings); no acc_out
+  // N = 2I packed gate / up columns, out [M][I] = silu(gate) * up (the
+  // elementwise pass's roundings), no acc_out: 1 gate column c with up column
+  // I + c (W8A8 packs), 2 gate / up 16-column blocks alternating (the W4A16
+  // interleaved operand); 0 none
   int swiglu;
 };
 

@@ -115,6 +115,7 @@ struct W4Args {
   int layout;            // kLayoutRows (qweight [K/8][N]) or kLayoutTiles
   int zu;                // tiles built with one zero for every group and column (zoff)
   int swiglu;            // N = 2I gate/up columns interleaved by 16; out [M][I] = silu(gate) * up
+  int swiglu_split;      // the same output from the split-K reduce of a plain GEMV over those columns
 };
 
 KQ_DEV int group_of(const W4Args& a, int k) {
@@ -1768,7 +1769,7 @@ static int run_w4(const char* what, int fmt, W4Args a, int gmode, void* workspac
     launch_gv(a, gp, xdt, gv_s, gv_spg, a.layout, stream);
     if (gp.splits > 1) {
       ReduceArgs r{a.partials, gp.splits, a.M, a.N, nullptr, nullptr, 0, a.bias, a.bias_dtype,
-                   a.out, a.out_dtype, nullptr};
+                   a.out, a.out_dtype, nullptr, a.swiglu_split ? 2 : 0};
       launch_splitk_reduce(kReduceW4, r, stream);
     }
     return check_launch(what);
@@ -2019,8 +2020,16 @@ extern "C" int kq_w4a16_tiled_swiglu_gemm(const void* x, int x_dtype, const int3
   // elementwise pass
   if (a.M > 0 && (gv_plan(a, kGptq, gmode, &gp, &s_, &spg_) || (a.M > 64 && prefill_applies(a, gmode))))
     return run_w4(what, kGptq, a, gmode, workspace, workspace_bytes, (hipStream_t)stream);
-  // two passes: [m][2I] in the activation dtype after the GEMM's scratch
   a.swiglu = 0;
+  // decode shapes whose K takes more than one GEMV pass (K > 4096): the plain
+  // GEMV's K chunks meet in the split-K reduce, which pairs each gate column
+  // with its up column 16 on and stores silu(gate) * up (the bits of the
+  // reduce's store followed by the elementwise pass)
+  if (a.M > 0 && gv_plan(a, kGptq, gmode, &gp, &s_, &spg_) && gp.splits > 1) {
+    a.swiglu_split = 1;
+    return run_w4(what, kGptq, a, gmode, workspace, workspace_bytes, (hipStream_t)stream);
+  }
+  // two passes: [m][2I] in the activation dtype after the GEMM's scratch
   if (m == 0) return KQ_OK;
   const size_t off = swiglu_ws_offset(m, n, k, gmode);
   const size_t need = off + (size_t)m * (size_t)n * 2;

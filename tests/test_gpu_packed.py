@@ -133,8 +133,9 @@ def test_pack_graph_replays_match_eager(cuda):
 
 # ---------------------------------------------------------------- SwiGLU
 # silu(gate(x)) * up(x) of a (gate, up) pack (kairyu/models/layers.py:243-244).
-# W4A16: one kq_w4a16_tiled_swiglu_gemm call; decode shapes (here N = 2 x 4096
-# on K = 4096) apply SwiGLU in the GEMV epilogue, others run the tiled GEMM
+# W4A16: one kq_w4a16_tiled_swiglu_gemm call; decode shapes apply SwiGLU in
+# the GEMV epilogue (K <= 4096) or in the reduce of its K chunks (K > 4096),
+# prefill shapes (M > 64) in the prefill epilogue, others run the tiled GEMM
 # and the elementwise pass.  W8A8: one kq_w8a8_*_swiglu_linear call; prefill
 # shapes apply SwiGLU in the tile engine's epilogue, M <= 64 in the decode
 # or skinny GEMM's (or their split-K reduce), others run the packed GEMM and
@@ -162,6 +163,11 @@ _SWIGLU_CASES = [
     ("awq", 16, 4096, 11008, torch.float16, False),
     ("gptq-sym-ao", 16, 2048, 14336, torch.float16, False),
     ("gptq", 1, 2048, 11008, torch.bfloat16, True),
+    # decode, K past one GEMV pass: the K chunks' reduce applies SwiGLU
+    ("gptq-ao", 1, 8192, 2048, torch.float16, False),
+    ("gptq", 16, 5120, 1024, torch.bfloat16, True),
+    ("awq", 4, 14336, 1024, torch.float16, False),
+    ("gptq-sym-ao", 16, 4224, 512, torch.float16, False),   # K % 256 == 128: three chunks
     ("fp8", 1, 2048, 2048, torch.bfloat16, True),
     ("fp8", 300, 1024, 1024, torch.float16, False),
     # decode shapes: SwiGLU in the decode GEMM's epilogue (8 gate + 8 up rows
