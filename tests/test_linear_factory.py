@@ -220,3 +220,28 @@ def test_legacy_per_format_modules_forward_to_the_fused_kernels(monkeypatch):
         monkeypatch.setattr(module, "_forward", lambda x, m, _n=name: seen.append((_n, x, m)) or _n)
         assert module.linear_forward("x", "module") == name
     assert seen == [(n, "x", "module") for n in ("awq", "gptq", "fp8", "int8")]
+
+
+def test_checkpoint_member_layout_binding():
+    """``bind_checkpoint_member_layout`` (kairyu/quant/linear.py:101-119),
+    as the reference's MoE router binds its ``e_score_correction_bias``
+    (kairyu/models/moe.py:372-376): a direct member gets one layout; dotted
+    names, unregistered members and a second binding are rejected."""
+
+    from kairyu_amd.quant.linear import CheckpointMemberLayout, bind_checkpoint_member_layout
+
+    gate = torch.nn.Linear(16, 8, bias=False)
+    gate.register_buffer("e_score_correction_bias", torch.zeros(8))
+    layout = CheckpointMemberLayout(column_dim=0, row_dim=None)
+    bind_checkpoint_member_layout(gate, "e_score_correction_bias", layout)
+    assert gate._kairyu_checkpoint_member_layouts == {"e_score_correction_bias": layout}
+    assert layout.shard_dim(TensorParallelMode.COLUMN) == 0
+    assert layout.shard_dim(TensorParallelMode.ROW) is None
+    with pytest.raises(ValueError, match="already has a layout"):
+        bind_checkpoint_member_layout(gate, "e_score_correction_bias", layout)
+    with pytest.raises(ValueError, match="direct member name"):
+        bind_checkpoint_member_layout(gate, "inner.bias", layout)
+    with pytest.raises(ValueError, match="not registered directly"):
+        bind_checkpoint_member_layout(gate, "missing", layout)
+    with pytest.raises(ValueError, match="shard dim"):
+        CheckpointMemberLayout(column_dim=2, row_dim=None)
