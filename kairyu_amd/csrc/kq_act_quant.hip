@@ -43,14 +43,14 @@ KQ_DEV void load8_f32(const uint16_t* row, int64_t i, int64_t k, int dtype, bool
   }
 }
 
+// Block-wide maximum (every thread gets it).  One call per kernel: `red` is
+// not reused afterwards, so no barrier follows the reads.
 KQ_DEV uint32_t block_max_u32(uint32_t v, uint32_t* red) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v = max(v, (uint32_t)__shfl_xor((int)v, off, 64));
+  v = wave_max_u32_dpp(v);
   if (lane_id() == 0) red[wave_id()] = v;
   __syncthreads();
   uint32_t r = red[0];
   for (int w = 1; w < (int)(blockDim.x >> 6); ++w) r = max(r, red[w]);
-  __syncthreads();
   return r;
 }
 

@@ -53,26 +53,6 @@ KQ_DEV uint32_t float_key(float v) {
 }
 
 
-// Wave-wide maximum of a 32-bit key, uniform result.  Within each row of 16
-// lanes: quad exchanges (xor 1, xor 2), then half-row and row mirrors through
-// DPP (register-to-register, no LDS round trip); the four row maxima are then
-// read from lanes 0, 16, 32, 48.
-template <int CTRL>
-KQ_DEV uint32_t dpp_max_u32(uint32_t v) {
-  return max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xf, 0xf, false));
-}
-
-KQ_DEV uint32_t wave_max_u32_dpp(uint32_t v) {
-  v = dpp_max_u32<0xB1>(v);    // quad_perm [1,0,3,2]
-  v = dpp_max_u32<0x4E>(v);    // quad_perm [2,3,0,1]
-  v = dpp_max_u32<0x141>(v);   // row_half_mirror
-  v = dpp_max_u32<0x140>(v);   // row_mirror
-  uint32_t best = (uint32_t)__builtin_amdgcn_readlane((int)v, 0);
-#pragma unroll
-  for (int r = 1; r < 4; ++r) best = max(best, (uint32_t)__builtin_amdgcn_readlane((int)v, 16 * r));
-  return best;
-}
-
 KQ_DEV float wave_sum(float v) {
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);

@@ -556,8 +556,7 @@ w8a8_decode_quant_kernel(const uint16_t* __restrict__ x, int x_dtype, int ldx, i
           }
         }
       }
-#pragma unroll
-      for (int off = 32; off > 0; off >>= 1) mx = max(mx, (uint32_t)__shfl_xor((int)mx, off, 64));
+      mx = wave_max_u32_dpp(mx);
       if (lane == 0) wmax[wave][r] = mx;
     }
     __syncthreads();
