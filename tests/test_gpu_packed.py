@@ -342,6 +342,7 @@ def test_swiglu_pack_rejects_diverged_g_idx(cuda):
     ("int8", 24, 2048, 1000, torch.bfloat16, True),
     ("int8", 33, 8192, 512, torch.float16, False),
     ("int8", 50, 1040, 520, torch.float16, True),
+    ("int8", 40, 8208, 1024, torch.bfloat16, True),   # grouped tiles, K % 64 != 0, 8-way split
 ])
 def test_w8a8_swiglu_epilogue_bit_identical_to_two_passes(cuda, scheme, m, k, width, dtype, bias):
     """The SwiGLU epilogues (tile engine for prefill shapes, decode and

@@ -443,10 +443,12 @@ def test_fp8_activation_quantization_bit_exact(cuda, mode):
 # Skinny kernel with grouped column tiles (M = 17..64 where grouping keeps
 # the CUs filled): N = 4100 leaves a last group with one live column tile
 # (257 tiles), K = 8192 splits K 2-4 ways; 2 (FP8 M > 32) or 4 tiles a group.
-@pytest.mark.parametrize("fmt,m", [("int8", 17), ("int8", 40), ("int8", 64),
-                                   ("fp8", 24), ("fp8", 33), ("fp8", 64)])
-def test_grouped_skinny_matches_oracle(cuda, fmt, m):
-    n, k = 4100, 8192
+@pytest.mark.parametrize("fmt,m,k", [("int8", 17, 8192), ("int8", 40, 8192), ("int8", 64, 8192),
+                                     ("fp8", 24, 8192), ("fp8", 33, 8192), ("fp8", 64, 8192),
+                                     # K % step != 0: the predicated fragment loads
+                                     ("int8", 40, 8208), ("fp8", 24, 8208)])
+def test_grouped_skinny_matches_oracle(cuda, fmt, m, k):
+    n = 4100
     banner(f"{fmt} grouped skinny m={m}")
     x = torch.randn(m, k, generator=torch.Generator().manual_seed(5 * m)).to(torch.bfloat16)
     if fmt == "int8":
