@@ -134,15 +134,28 @@ def _workspace(device: torch.device, nbytes: int = 0) -> torch.Tensor:
     return _native.workspace(device, nbytes)
 
 
+@lru_cache(maxsize=4096)
+def _workspace_bytes(entry: str, device_index: int, *shape: int) -> int:
+    """A workspace-size entry point's answer for one shape (a pure function of
+    the shape and of the device's CU count, fixed for the process)."""
+
+    return int(getattr(_native.library(), entry)(*shape))
+
+
+def _device_index(device: torch.device) -> int:
+    return device.index if device.index is not None else torch.cuda.current_device()
+
+
 def _w8a8_linear_workspace(device: torch.device, m: int, n: int, k: int) -> torch.Tensor:
     """Workspace for a fused W8A8 call of this shape: the quantized rows and
     their scales (when they are staged) and every split-K form's partials."""
 
-    return _workspace(device, int(_native.library().kq_w8a8_linear_workspace_size(m, n, k)))
+    need = _workspace_bytes("kq_w8a8_linear_workspace_size", _device_index(device), m, n, k)
+    return _workspace(device, need)
 
 
 def _w4_workspace(device: torch.device, m: int, n: int, k: int, mode: int) -> torch.Tensor:
-    need = int(_native.library().kq_w4a16_workspace_size(m, n, k, mode))
+    need = _workspace_bytes("kq_w4a16_workspace_size", _device_index(device), m, n, k, mode)
     return _workspace(device, need)
 
 
