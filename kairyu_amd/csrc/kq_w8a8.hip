@@ -908,9 +908,13 @@ static void launch_skinny(const uint8_t* xq, const uint8_t* w, int K, const Epi&
   hipLaunchKernelGGL((w8a8_skinny_kernel<FMT, MT, NT, U, PRED, SW>), dim3(tiles * splits),        \
                      dim3(64 * kSkinnyWaves), 0, stream, xq, w, K, steps_per_split, splits, ep, \
                      workspace)
-#define KQ_SKINNY_NT(PRED, SW)             \
-  if (grouped) KQ_SKINNY(NTG, UG, PRED, SW); \
-  else KQ_SKINNY(1, U1, PRED, SW);
+#define KQ_SKINNY_NT(PRED, SW)                 \
+  if constexpr (NTG > 1) {                       \
+    if (grouped) KQ_SKINNY(NTG, UG, PRED, SW);   \
+    else KQ_SKINNY(1, U1, PRED, SW);             \
+  } else {                                       \
+    KQ_SKINNY(1, U1, PRED, SW);                  \
+  }
   if (K % T::kStep == 0) {
     if (ep.swiglu) { KQ_SKINNY_NT(false, true) }
     else { KQ_SKINNY_NT(false, false) }
