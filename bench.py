@@ -234,7 +234,14 @@ def gemm_launcher(workload, copies: int):
                          _native.stream_handle(device))
 
     nbytes = n * k + 4 * n + m * k + 4 * m + 2 * m * n
-    kernel = ("w8a8_decode_kernel" if m <= 16 else "tile_gemm_kernel (+ split-K reduce when used)")
+    # the launcher's dispatch in kq_w8a8.hip: decode kernel for M <= 16 with
+    # K % 128 == 0, skinny kernel up to M = 64, tile engine above
+    if m <= 16 and k % 128 == 0:
+        kernel = "w8a8_decode_kernel"
+    elif m <= 64:
+        kernel = "w8a8_skinny_kernel (+ split-K reduce when used)"
+    else:
+        kernel = "tile_gemm_kernel (+ split-K reduce when used)"
     return launch, nbytes, 2 * m * n * k, kernel
 
 
@@ -521,6 +528,10 @@ def sweep_entries():
                             lambda m=m, n=n, k=k: W.gptq_layer(m=m, n=n, k=k)))
             entries.append((f"{label} FP8 W8A8 N={n} K={k} M={m}", "fp8",
                             lambda m=m, n=n, k=k: W.fp8_layer(m=m, n=n, k=k)))
+    # batched decode (M = 17..64): the skinny W8A8 GEMM with grouped column tiles
+    entries.append(("Llama-3-8B down_proj FP8 W8A8 N=4096 K=14336 M=64", "fp8",
+                    lambda: W.fp8_layer(m=64, n=4096, k=14336)))
+    entries.append(("Qwen2-7B MLP up INT8 W8A8 N=18944 K=3584 M=32", "int8", lambda: W.int8_layer(m=32)))
     return entries
 
 
